@@ -1,0 +1,75 @@
+"""Builds libfellm_rocm_kernels.so (HIP kernels for gfx950 + the plugin C ABI).
+
+Run ``python -m fellm_amd.build``.  Objects go to ``fellm_amd/_build/``; the
+shared library lands in-tree at ``fellm_amd/libfellm_rocm_kernels.so`` so it
+travels with the source tree to the GPU host.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB_NAME = "libfellm_rocm_kernels.so"
+LIB_PATH = PKG / LIB_NAME
+ARCH = os.environ.get("FELLM_ROCM_ARCH", "gfx950")
+
+SOURCES = ["norm.hip", "elementwise.hip", "embedding.hip", "rope.hip", "router.hip", "plugin.cpp"]
+
+# -ffp-contract=off keeps the reference's operation order (no silent FMA);
+# the packed-fp32 feature is disabled for every HIP translation unit.
+COMMON_FLAGS = [
+    "-O3",
+    "-std=c++20",
+    "-fPIC",
+    "-ffp-contract=off",
+    f"-I{ROOT / 'include'}",
+    f"-I{CSRC}",
+    "-Wall",
+    "-Wno-unused-function",
+]
+DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: install ROCm or set HIPCC")
+
+
+def _compile(src: str) -> Path:
+    obj = BUILD / (Path(src).stem + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build(verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), 6)) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), *DEVICE_FLAGS, "-shared", "-fPIC", f"-Wl,--version-script={CSRC / 'exports.map'}",
+           "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

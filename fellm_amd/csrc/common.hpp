@@ -1,0 +1,256 @@
+// Shared device helpers for the gfx950 kernels: activation dtypes, wavefront
+// reductions, bit-exact glibc expf, launch bookkeeping.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "fellm_abi.h"
+#include "fellm_rocm.h"
+
+namespace fellm {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Activation element types.  Arithmetic is always f32; storage is f32, f16
+// (IEEE binary16) or bf16.  Narrowing rounds to nearest-even once.
+// ---------------------------------------------------------------------------
+struct F32 {
+    using T = float;
+    static constexpr uint32_t code = FELLM_DTYPE_F32;
+    __device__ __forceinline__ static float load(T v) { return v; }
+    __device__ __forceinline__ static T store(float v) { return v; }
+};
+
+struct F16 {
+    using T = _Float16;
+    static constexpr uint32_t code = FELLM_DTYPE_F16;
+    __device__ __forceinline__ static float load(T v) { return (float)v; }
+    // v_cvt_f16_f32 under the default MODE register rounds to nearest-even.
+    // The empty asm pins the f32 value: without it the compiler folds
+    // fptrunc(f32 * fpext(f16)) into one mixed-precision FMA that rounds the
+    // exact product straight to f16, skipping the f32 rounding the CPU does.
+    __device__ __forceinline__ static T store(float v) {
+        __asm__("" : "+v"(v));
+        return (_Float16)v;
+    }
+};
+
+struct BF16 {
+    using T = uint16_t;
+    static constexpr uint32_t code = FELLM_DTYPE_BF16;
+    // Widening is exact: bits << 16 (dequant.rs:36-42).
+    __device__ __forceinline__ static float load(T v) { return __uint_as_float((uint32_t)v << 16); }
+    // Round to nearest-even on the top 16 bits; NaN stays a quiet NaN.
+    __device__ __forceinline__ static T store(float v) {
+        uint32_t u = __float_as_uint(v);
+        if ((u & 0x7fffffffu) > 0x7f800000u) return (T)((u >> 16) | 0x0040u);
+        u += 0x7fffu + ((u >> 16) & 1u);
+        return (T)(u >> 16);
+    }
+};
+
+// Host-side dispatch helper: call f.template operator()<Type>() for a dtype code.
+template <typename Fn>
+inline int dispatch_act(uint32_t dtype, Fn &&f) {
+    switch (dtype) {
+        case FELLM_DTYPE_F32: return f.template operator()<F32>();
+        case FELLM_DTYPE_F16: return f.template operator()<F16>();
+        case FELLM_DTYPE_BF16: return f.template operator()<BF16>();
+        default: return FELLM_ERR_DTYPE;
+    }
+}
+
+inline size_t act_bytes(uint32_t dtype) {
+    return dtype == FELLM_DTYPE_F32 ? 4 : (dtype == FELLM_DTYPE_F16 || dtype == FELLM_DTYPE_BF16) ? 2 : 0;
+}
+
+// ---------------------------------------------------------------------------
+// Vector load/store of N elements (N * sizeof(T) must be 4, 8, 16 or 32 bytes).
+// ---------------------------------------------------------------------------
+template <typename T, int N>
+struct alignas(sizeof(T) * N) Pack {
+    T v[N];
+};
+
+template <typename A, int N>
+__device__ __forceinline__ void load_f32(const typename A::T *p, float (&out)[N]) {
+    Pack<typename A::T, N> pk = *reinterpret_cast<const Pack<typename A::T, N> *>(p);
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = A::load(pk.v[i]);
+}
+
+template <typename A, int N>
+__device__ __forceinline__ void store_f32(typename A::T *p, const float (&in)[N]) {
+    Pack<typename A::T, N> pk;
+#pragma unroll
+    for (int i = 0; i < N; ++i) pk.v[i] = A::store(in[i]);
+    *reinterpret_cast<Pack<typename A::T, N> *>(p) = pk;
+}
+
+// Streaming variants: data touched exactly once bypasses cache retention.
+template <typename A, int N>
+__device__ __forceinline__ void load_f32_nt(const typename A::T *p, float (&out)[N]) {
+    using P = Pack<typename A::T, N>;
+    if constexpr (sizeof(P) % 4 != 0) {
+        load_f32<A, N>(p, out);
+    } else {
+        constexpr int W = sizeof(P) / 4;
+        uint32_t w[W];
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(p);
+#pragma unroll
+        for (int i = 0; i < W; ++i) w[i] = __builtin_nontemporal_load(src + i);
+        P pk;
+        memcpy(&pk, w, sizeof(P));
+#pragma unroll
+        for (int i = 0; i < N; ++i) out[i] = A::load(pk.v[i]);
+    }
+}
+
+template <typename A, int N>
+__device__ __forceinline__ void store_f32_nt(typename A::T *p, const float (&in)[N]) {
+    using P = Pack<typename A::T, N>;
+    if constexpr (sizeof(P) % 4 != 0) {
+        store_f32<A, N>(p, in);
+    } else {
+        constexpr int W = sizeof(P) / 4;
+        P pk;
+#pragma unroll
+        for (int i = 0; i < N; ++i) pk.v[i] = A::store(in[i]);
+        uint32_t w[W];
+        memcpy(w, &pk, sizeof(P));
+        uint32_t *dst = reinterpret_cast<uint32_t *>(p);
+#pragma unroll
+        for (int i = 0; i < W; ++i) __builtin_nontemporal_store(w[i], dst + i);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Reductions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        uint64_t o = __shfl_xor(v, off, kWave);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Block-wide f32 sum; every thread gets the result.  `scratch` holds one
+// float per wave.  Contains __syncthreads, so all threads must call it.
+template <int BLOCK>
+__device__ __forceinline__ float block_sum(float v, float *scratch) {
+    constexpr int NW = BLOCK / kWave;
+    v = wave_sum(v);
+    if constexpr (NW == 1) {
+        return v;
+    } else {
+        const int lane = threadIdx.x % kWave, wid = threadIdx.x / kWave;
+        if (lane == 0) scratch[wid] = v;
+        __syncthreads();
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) t += scratch[i];
+        __syncthreads();
+        return t;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// expf, bit-exact with glibc >= 2.27 on x86_64 (the libm that Rust's f32::exp
+// calls on linux-gnu).  Algorithm: Szabolcs Nagy's expf from ARM
+// optimized-routines (MIT), as shipped in glibc: x*32/ln2 = k + r,
+// exp(x) = 2^(k/32) * p(r), p cubic, all in double, one final rounding.
+// The x86_64 build contracts r = x*InvLn2N - kd and the Horner steps into FMA;
+// this restatement does the same.  Table: tab[i] = bits(2^(i/32)) - (i << 47).
+// Exhaustively equal to glibc expf over every float in (-103.97, 88.73).
+// ---------------------------------------------------------------------------
+struct ExpfTable {
+    uint64_t tab[32];
+};
+
+__host__ __device__ constexpr ExpfTable make_expf_table() {
+    // 2^(i/32) rounded to double; verified against exp2l at build-test time.
+    return ExpfTable{{0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full,
+                      0x3fef9301d0125b51ull, 0x3fef72b83c7d517bull, 0x3fef54873168b9aaull,
+                      0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull, 0x3fef06fe0a31b715ull,
+                      0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+                      0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull,
+                      0x3feea47eb03a5585ull, 0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull,
+                      0x3feea11473eb0187ull, 0x3feea589994cce13ull, 0x3feeace5422aa0dbull,
+                      0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+                      0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull,
+                      0x3fef3720dcef9069ull, 0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full,
+                      0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull}};
+}
+
+__device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
+    const uint32_t ux = __float_as_uint(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {  // |x| >= 88 or NaN/Inf
+        if (ux == 0xff800000u) return 0.0f;          // -inf
+        if (abstop >= 0x7f8u) return x + x;           // +inf or NaN
+        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);  // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;          // underflow
+    }
+    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    const double Shift = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    const double z = InvLn2N * xd;
+    double kd = __dadd_rn(z, Shift);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd = __dsub_rn(kd, Shift);
+    const double r = __fma_rn(InvLn2N, xd, -kd);
+    uint64_t t = tab[ki % 32];
+    t += ki << 47;
+    const double s = __longlong_as_double((long long)t);
+    const double zz = __fma_rn(C0, r, C1);
+    const double r2 = __dmul_rn(r, r);
+    double y = __fma_rn(C2, r, 1.0);
+    y = __fma_rn(zz, r2, y);
+    y = __dmul_rn(y, s);
+    return (float)y;
+}
+
+// Copies the 32-entry table into LDS once per block; returns the LDS pointer.
+// Contains __syncthreads.
+__device__ __forceinline__ const uint64_t *stage_expf_table(uint64_t *lds) {
+    constexpr ExpfTable T = make_expf_table();
+    if (threadIdx.x < 32) lds[threadIdx.x] = T.tab[threadIdx.x];
+    __syncthreads();
+    return lds;
+}
+
+// ---------------------------------------------------------------------------
+// Host helpers.
+// ---------------------------------------------------------------------------
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int launch_status() {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? FELLM_OK : FELLM_ERR_LAUNCH;
+}
+
+inline bool aligned_to(const void *p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+}  // namespace fellm

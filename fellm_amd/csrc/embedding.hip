@@ -1,0 +1,303 @@
+// Token-embedding gather with dequant-on-gather, optionally fused with RMSNorm.
+//
+// Reference: crates/backend-cpu/src/backend.rs:1026-1046 (launch_embedding)
+//   -> kernels/embedding.rs:10-23 (embedding_row) -> dequant.rs:19-55
+//   F32 copy, F16 widen (half::f16::to_f32), BF16 bits << 16,
+//   Q4_K dequant.rs:251-305, Q6_K dequant.rs:315-370.
+//
+// One workgroup gathers one token row.  A row is cut into "parts", each a
+// fixed set of output elements one thread produces:
+//   dense : 8 consecutive elements (one 16-byte load for 16-bit tables);
+//   Q4_K  : 16 elements = one 8-byte slice of a 32-byte qs chunk, whose low
+//           nibbles are 8 consecutive outputs and high nibbles the 8 outputs
+//           32 further on; the 16-byte block header (d, dmin, 12 scale bytes,
+//           16-byte aligned because a block is 144 = 9*16 bytes) is loaded
+//           straight from global memory and shared via L1 by the 16 parts of
+//           the block;
+//   Q6_K  : 16 elements = 4 runs of 4.  210-byte blocks are only 2-byte
+//           aligned, so the whole row is first staged into LDS with
+//           coalesced dword loads and decoded from there.
+// The arithmetic order is the reference's, with FMA contraction disabled at
+// compile time:  Q4_K  y = (d*sc)*q - (dmin*m);   Q6_K  y = (d*sc)*(q-32).
+// With NORM the decoded row stays in registers for the sum of squares and
+// is written once as h (gathered row) and once as y (normalised row).
+#include "common.hpp"
+
+namespace fellm {
+namespace {
+
+__device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+// ---- decoders --------------------------------------------------------------
+template <typename A, int VEC>
+struct DenseDec {
+    static constexpr int OUT = VEC, RUNS = 1, RUNLEN = VEC;
+    static constexpr bool kStage = false;
+    __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)dim * sizeof(typename A::T); }
+    __host__ __device__ static uint32_t parts(uint32_t dim) { return dim / VEC; }
+    __device__ static uint32_t run_off(uint32_t p, int) { return p * VEC; }
+    __device__ static void decode(const uint8_t *row, uint32_t p, float (&v)[OUT]) {
+        load_f32<A, VEC>(reinterpret_cast<const typename A::T *>(row) + (size_t)p * VEC, v);
+    }
+};
+
+struct Q4KDec {
+    static constexpr int OUT = 16, RUNS = 2, RUNLEN = 8;
+    static constexpr bool kStage = false;
+    __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)(dim / 256) * 144; }
+    __host__ __device__ static uint32_t parts(uint32_t dim) { return (dim / 256) * 16; }
+    __device__ static uint32_t run_off(uint32_t p, int r) {
+        const uint32_t q = p % 16;
+        return (p / 16) * 256 + 64 * (q / 4) + 8 * (q % 4) + 32 * r;
+    }
+    // get_scale_min_k4 (dequant.rs:295-305) on the 12 scale bytes held as 3 dwords.
+    __device__ static void scale_min(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,
+                                     uint32_t &m) {
+        if (j < 4) {
+            sc = (s0 >> (8 * j)) & 63u;
+            m = (s1 >> (8 * j)) & 63u;
+        } else {
+            const uint32_t k = 8 * (j - 4);
+            const uint32_t b_hi = (s2 >> k) & 0xffu;  // q[j + 4]
+            sc = (b_hi & 0x0fu) | (((s0 >> k) & 0xffu) >> 6) << 4;  // q[j - 4] >> 6
+            m = (b_hi >> 4) | (((s1 >> k) & 0xffu) >> 6) << 4;      // q[j] >> 6
+        }
+    }
+    __device__ static void decode(const uint8_t *row, uint32_t p, float (&v)[OUT]) {
+        const uint8_t *blk = row + (size_t)(p / 16) * 144;
+        const uint32_t q = p % 16, c = q / 4, j = q % 4;
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
+        const float d = half_bits_to_f32(hdr.x & 0xffffu);
+        const float dmin = half_bits_to_f32(hdr.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        scale_min(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
+        scale_min(2 * c + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+        const float d1 = d * (float)sc0, m1f = dmin * (float)m0;
+        const float d2 = d * (float)sc1, m2f = dmin * (float)m1;
+        const uint2 qs = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * c + 8 * j);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t b = ((k < 4 ? qs.x : qs.y) >> (8 * (k % 4))) & 0xffu;
+            v[k] = d1 * (float)(b & 0x0fu) - m1f;
+            v[8 + k] = d2 * (float)(b >> 4) - m2f;
+        }
+    }
+};
+
+struct Q6KDec {
+    static constexpr int OUT = 16, RUNS = 4, RUNLEN = 4;
+    static constexpr bool kStage = true;
+    __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)(dim / 256) * 210; }
+    __host__ __device__ static uint32_t parts(uint32_t dim) { return (dim / 256) * 16; }
+    __device__ static uint32_t run_off(uint32_t p, int r) {
+        const uint32_t q = p % 16;
+        return (p / 16) * 256 + 128 * (q / 8) + 4 * (q % 8) + 32 * r;
+    }
+    // `row` points into LDS.  Block layout (dequant.rs:315-370): ql[128],
+    // qh[64], int8 scales[16], f16 d at 208.
+    __device__ static void decode(const uint8_t *row, uint32_t p, float (&v)[OUT]) {
+        const uint8_t *blk = row + (size_t)(p / 16) * 210;
+        const uint32_t q = p % 16, hh = q / 8, l0 = 4 * (q % 8), is = l0 / 16;
+        const uint8_t *ql = blk + 64 * hh;
+        const uint8_t *qh = blk + 128 + 32 * hh;
+        const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192 + 8 * hh);
+        const float d = half_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+        const float ds0 = d * (float)sc[is], ds1 = d * (float)sc[is + 2];
+        const float ds2 = d * (float)sc[is + 4], ds3 = d * (float)sc[is + 6];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t l = l0 + m;
+            const int32_t a = ql[l], b = ql[l + 32], h = qh[l];
+            const int32_t q1 = ((a & 0xf) | ((h & 3) << 4)) - 32;
+            const int32_t q2 = ((b & 0xf) | (((h >> 2) & 3) << 4)) - 32;
+            const int32_t q3 = ((a >> 4) | (((h >> 4) & 3) << 4)) - 32;
+            const int32_t q4 = ((b >> 4) | (((h >> 6) & 3) << 4)) - 32;
+            v[m] = ds0 * (float)q1;
+            v[4 + m] = ds1 * (float)q2;
+            v[8 + m] = ds2 * (float)q3;
+            v[12 + m] = ds3 * (float)q4;
+        }
+    }
+};
+
+template <typename D, typename O>
+__device__ __forceinline__ void store_part(typename O::T *row, uint32_t p, const float (&v)[D::OUT]) {
+#pragma unroll
+    for (int r = 0; r < D::RUNS; ++r) {
+        float t[D::RUNLEN];
+#pragma unroll
+        for (int k = 0; k < D::RUNLEN; ++k) t[k] = v[r * D::RUNLEN + k];
+        store_f32_nt<O, D::RUNLEN>(row + D::run_off(p, r), t);
+    }
+}
+
+// Stages `bytes` (even) of a table row into LDS.  Dword loads when the source
+// is 4-byte aligned, else 16-bit loads.
+template <int BLOCK>
+__device__ __forceinline__ void stage_row(const uint8_t *src, uint8_t *lds, uint64_t bytes) {
+    if ((reinterpret_cast<uintptr_t>(src) & 3) == 0) {
+        const uint32_t nw = (uint32_t)(bytes / 4);
+        for (uint32_t i = threadIdx.x; i < nw; i += BLOCK)
+            reinterpret_cast<uint32_t *>(lds)[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(src) + i);
+        if ((bytes & 2) && threadIdx.x == 0)
+            reinterpret_cast<uint16_t *>(lds)[bytes / 2 - 1] = reinterpret_cast<const uint16_t *>(src)[bytes / 2 - 1];
+    } else {
+        const uint32_t nh = (uint32_t)(bytes / 2);
+        for (uint32_t i = threadIdx.x; i < nh; i += BLOCK)
+            reinterpret_cast<uint16_t *>(lds)[i] = reinterpret_cast<const uint16_t *>(src)[i];
+    }
+    __syncthreads();
+}
+
+constexpr int kEmbBlock = 256;
+
+template <typename D, typename O, int MAXC, bool NORM>
+__global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
+    const uint8_t *__restrict__ table, uint64_t vocab, uint32_t dim, const uint32_t *__restrict__ ids,
+    typename O::T *__restrict__ h, typename O::T *__restrict__ y, const float *__restrict__ w, float eps,
+    uint32_t *__restrict__ err) {
+    extern __shared__ __align__(16) uint8_t lds_row[];
+    __shared__ float red[kEmbBlock / kWave];
+    const uint32_t row = blockIdx.x;
+    const uint32_t id = ids[row];
+    const bool bad = id >= vocab;
+    if (bad && threadIdx.x == 0 && err) atomicOr(err, 1u);
+    const uint64_t rb = D::row_bytes(dim);
+    const uint8_t *src = table + (bad ? 0 : (uint64_t)id * rb);
+    if constexpr (D::kStage) {
+        stage_row<kEmbBlock>(src, lds_row, rb);
+        src = lds_row;
+    }
+    const uint32_t parts = D::parts(dim);
+    const size_t obase = (size_t)row * dim;
+    if constexpr (!NORM) {
+        for (uint32_t p = threadIdx.x; p < parts; p += kEmbBlock) {
+            float v[D::OUT];
+            D::decode(src, p, v);
+            if (bad) {
+#pragma unroll
+                for (int k = 0; k < D::OUT; ++k) v[k] = 0.0f;
+            }
+            store_part<D, O>(h + obase, p, v);
+        }
+    } else {
+        float v[MAXC][D::OUT];
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+            const uint32_t p = c * kEmbBlock + threadIdx.x;
+            if (p < parts) {
+                D::decode(src, p, v[c]);
+#pragma unroll
+                for (int k = 0; k < D::OUT; ++k) {
+                    if (bad) v[c][k] = 0.0f;
+                    ss += v[c][k] * v[c][k];
+                }
+            }
+        }
+        ss = block_sum<kEmbBlock>(ss, red);
+        const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+            const uint32_t p = c * kEmbBlock + threadIdx.x;
+            if (p < parts) {
+                if (h) store_part<D, O>(h + obase, p, v[c]);
+                float o[D::OUT];
+#pragma unroll
+                for (int r = 0; r < D::RUNS; ++r) {
+                    const uint32_t off = D::run_off(p, r);
+#pragma unroll
+                    for (int k = 0; k < D::RUNLEN; ++k)
+                        o[r * D::RUNLEN + k] = (v[c][r * D::RUNLEN + k] * scale) * w[off + k];
+                }
+                store_part<D, O>(y + obase, p, o);
+            }
+        }
+    }
+}
+
+template <typename D, typename O>
+int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids,
+               void *h, void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
+    using TO = typename O::T;
+    const size_t lds = D::kStage ? (size_t)((D::row_bytes(dim) + 15) / 16 * 16) : 0;
+    if (lds > 64 * 1024) return FELLM_ERR_SHAPE;
+    const dim3 grid(n_ids), block(kEmbBlock);
+    const uint8_t *tb = static_cast<const uint8_t *>(table);
+    if (!w) {
+        hipLaunchKernelGGL((embedding_kernel<D, O, 1, false>), grid, block, lds, s, tb, vocab, dim, ids,
+                           (TO *)h, nullptr, nullptr, 0.0f, err);
+        return launch_status();
+    }
+    const uint32_t chunks = (D::parts(dim) + kEmbBlock - 1) / kEmbBlock;
+#define FELLM_EMB_NORM(C)                                                                          \
+    if (chunks <= C) {                                                                             \
+        hipLaunchKernelGGL((embedding_kernel<D, O, C, true>), grid, block, lds, s, tb, vocab, dim, ids, \
+                           (TO *)h, (TO *)y, w, eps, err);                                          \
+        return launch_status();                                                                    \
+    }
+    FELLM_EMB_NORM(1)
+    FELLM_EMB_NORM(2)
+    FELLM_EMB_NORM(4)
+    FELLM_EMB_NORM(8)
+#undef FELLM_EMB_NORM
+    return FELLM_ERR_SHAPE;
+}
+
+template <typename O>
+int dispatch_table(const void *table, uint32_t table_dtype, uint64_t vocab, uint32_t dim,
+                   const uint32_t *ids, uint32_t n_ids, void *h, void *y, const float *w, float eps,
+                   uint32_t *err, hipStream_t s) {
+    switch (table_dtype) {
+        case FELLM_DTYPE_Q4K:
+            if (dim % 256 || !aligned_to(table, 16)) return FELLM_ERR_SHAPE;
+            return launch_emb<Q4KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
+        case FELLM_DTYPE_Q6K:
+            if (dim % 256 || !aligned_to(table, 2)) return FELLM_ERR_SHAPE;
+            return launch_emb<Q6KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
+        default:
+            break;
+    }
+    return dispatch_act(table_dtype, [&]<typename A>() -> int {
+        constexpr int VEC = 8;
+        const bool vec = dim % VEC == 0 && aligned_to(table, sizeof(typename A::T) * VEC);
+        if (vec) return launch_emb<DenseDec<A, VEC>, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
+        return launch_emb<DenseDec<A, 1>, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
+    });
+}
+
+int embedding_common(const void *table, uint32_t table_dtype, uint64_t vocab, uint32_t dim,
+                     const uint32_t *ids, uint32_t n_ids, void *h, void *y, uint32_t out_dtype,
+                     const float *w, float eps, uint32_t *err, void *stream) {
+    if (!table || !ids) return FELLM_ERR_ARITY;
+    if (dim == 0 || vocab == 0) return FELLM_ERR_SHAPE;
+    if (n_ids == 0) return FELLM_OK;
+    // Output runs are up to 8 elements: 16-byte alignment covers every case.
+    if ((h && !aligned_to(h, 16)) || (y && !aligned_to(y, 16))) return FELLM_ERR_SHAPE;
+    hipStream_t s = as_stream(stream);
+    return dispatch_act(out_dtype, [&]<typename O>() -> int {
+        return dispatch_table<O>(table, table_dtype, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
+    });
+}
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" int fellm_rocm_embedding(const void *table, uint32_t table_dtype, uint64_t vocab,
+                                    uint32_t dim, const uint32_t *ids, uint32_t n_ids, void *out,
+                                    uint32_t out_dtype, uint32_t *err_flag, void *stream) {
+    if (!out) return FELLM_ERR_ARITY;
+    return fellm::embedding_common(table, table_dtype, vocab, dim, ids, n_ids, out, nullptr, out_dtype,
+                                   nullptr, 0.0f, err_flag, stream);
+}
+
+extern "C" int fellm_rocm_embedding_rmsnorm(const void *table, uint32_t table_dtype, uint64_t vocab,
+                                            uint32_t dim, const uint32_t *ids, uint32_t n_ids,
+                                            const float *norm_weight, float eps, void *h_out, void *y,
+                                            uint32_t out_dtype, uint32_t *err_flag, void *stream) {
+    if (!norm_weight || !y) return FELLM_ERR_ARITY;
+    return fellm::embedding_common(table, table_dtype, vocab, dim, ids, n_ids, h_out, y, out_dtype,
+                                   norm_weight, eps, err_flag, stream);
+}

@@ -1,0 +1,161 @@
+// Residual add + RMSNorm for gfx950.
+//
+// Reference semantics: Add (crates/backend-cpu/src/kernels/simd_f32.rs:175-197)
+// then RmsNorm (crates/backend-cpu/src/kernels/norm.rs:6-53, launcher
+// crates/backend-cpu/src/backend.rs:1104-1133): per row of `group` elements,
+// sumsq = sum(h^2), scale = 1 / sqrt(sumsq / group + eps), y = (h * scale) * w.
+//
+// Layout: one workgroup per row.  Each thread owns NCHUNK chunks of VEC
+// consecutive elements (16-byte accesses for 16-bit types), keeps them in
+// registers between the reduction and the scaling pass, so x and residual are
+// read exactly once and h and y written exactly once: 4 row-passes of HBM
+// traffic with the residual fused (the unfused graph needs 6).
+// The sum of squares is one wavefront shuffle reduction plus one LDS exchange.
+#include "common.hpp"
+
+namespace fellm {
+namespace {
+
+template <typename A, typename O, int BLOCK, int VEC, int NCHUNK, bool ADD, bool STORE_H>
+__global__ __launch_bounds__(BLOCK) void add_rmsnorm_kernel(
+    // h may alias x or r (in-place residual update): no __restrict__ on them.
+    const typename A::T *x, const typename A::T *r, typename A::T *h, const float *__restrict__ w,
+    typename O::T *y, uint32_t group, float eps) {
+    __shared__ float red[BLOCK / kWave];
+    const size_t row = blockIdx.x;
+    const typename A::T *xr = x + row * group;
+    float v[NCHUNK][VEC];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCHUNK; ++c) {
+        const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
+        if (base < group) {
+            load_f32_nt<A, VEC>(xr + base, v[c]);
+            if constexpr (ADD) {
+                float rv[VEC];
+                load_f32_nt<A, VEC>(r + row * group + base, rv);
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) {
+                    // h is stored in the activation dtype and normalised as stored.
+                    v[c][i] = A::load(A::store(v[c][i] + rv[i]));
+                }
+                if constexpr (STORE_H) store_f32_nt<A, VEC>(h + row * group + base, v[c]);
+            }
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) ss += v[c][i] * v[c][i];
+        }
+    }
+    ss = block_sum<BLOCK>(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)group + eps);
+#pragma unroll
+    for (int c = 0; c < NCHUNK; ++c) {
+        const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
+        if (base < group) {
+            float wv[VEC], o[VEC];
+            load_f32<F32, VEC>(w + base, wv);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) o[i] = (v[c][i] * scale) * wv[i];
+            store_f32_nt<O, VEC>(y + row * group + base, o);
+        }
+    }
+}
+
+// Generic fallback for rows that do not fit the register-resident layout
+// (group % VEC != 0 or group > BLOCK * VEC * 8): two passes, the second
+// re-reading h (or x) from cache.
+template <typename A, typename O, bool ADD>
+__global__ __launch_bounds__(256) void add_rmsnorm_generic(
+    const typename A::T *x, const typename A::T *r, typename A::T *h, const float *__restrict__ w,
+    typename O::T *y, uint32_t group, float eps) {
+    __shared__ float red[256 / kWave];
+    const size_t off = (size_t)blockIdx.x * group;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < group; i += 256) {
+        float hv = A::load(x[off + i]);
+        if constexpr (ADD) {
+            hv = A::load(A::store(hv + A::load(r[off + i])));
+            if (h) h[off + i] = A::store(hv);
+        }
+        ss += hv * hv;
+    }
+    ss = block_sum<256>(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)group + eps);
+    for (uint32_t i = threadIdx.x; i < group; i += 256) {
+        float hv;
+        if (ADD && h) {
+            hv = A::load(h[off + i]);  // x or r may have been overwritten by h
+        } else {
+            hv = A::load(x[off + i]);
+            if constexpr (ADD) hv = A::load(A::store(hv + A::load(r[off + i])));
+        }
+        y[off + i] = O::store((hv * scale) * w[i]);
+    }
+}
+
+template <typename A, typename O, int BLOCK, int VEC, int NCHUNK>
+int launch_fast(const void *x, const void *r, void *h, const float *w, void *y, uint32_t group,
+                uint64_t rows, float eps, hipStream_t s) {
+    using TA = typename A::T;
+    using TO = typename O::T;
+    dim3 grid((uint32_t)rows), block(BLOCK);
+    if (r == nullptr) {
+        hipLaunchKernelGGL((add_rmsnorm_kernel<A, O, BLOCK, VEC, NCHUNK, false, false>), grid, block, 0, s,
+                           (const TA *)x, nullptr, nullptr, w, (TO *)y, group, eps);
+    } else if (h == nullptr) {
+        hipLaunchKernelGGL((add_rmsnorm_kernel<A, O, BLOCK, VEC, NCHUNK, true, false>), grid, block, 0, s,
+                           (const TA *)x, (const TA *)r, nullptr, w, (TO *)y, group, eps);
+    } else {
+        hipLaunchKernelGGL((add_rmsnorm_kernel<A, O, BLOCK, VEC, NCHUNK, true, true>), grid, block, 0, s,
+                           (const TA *)x, (const TA *)r, (TA *)h, w, (TO *)y, group, eps);
+    }
+    return launch_status();
+}
+
+template <typename A, typename O>
+int launch_typed(const void *x, const void *r, void *h, const float *w, void *y, uint32_t group,
+                 uint64_t rows, float eps, hipStream_t s) {
+    constexpr int VEC = 8;
+    const bool vec_ok = group % VEC == 0 && aligned_to(x, 16) && aligned_to(y, 16) &&
+                        aligned_to(w, 32) && (!r || aligned_to(r, 16)) && (!h || aligned_to(h, 16));
+    if (vec_ok) {
+        // Few rows (decode): wide blocks keep more bytes in flight per CU.
+        if (rows < 1024 && group <= 1024 * VEC * 2) {
+            if (group <= 1024 * VEC) return launch_fast<A, O, 1024, VEC, 1>(x, r, h, w, y, group, rows, eps, s);
+            return launch_fast<A, O, 1024, VEC, 2>(x, r, h, w, y, group, rows, eps, s);
+        }
+        if (group <= 256 * VEC) return launch_fast<A, O, 256, VEC, 1>(x, r, h, w, y, group, rows, eps, s);
+        if (group <= 256 * VEC * 2) return launch_fast<A, O, 256, VEC, 2>(x, r, h, w, y, group, rows, eps, s);
+        if (group <= 256 * VEC * 4) return launch_fast<A, O, 256, VEC, 4>(x, r, h, w, y, group, rows, eps, s);
+        if (group <= 256 * VEC * 8) return launch_fast<A, O, 256, VEC, 8>(x, r, h, w, y, group, rows, eps, s);
+    }
+    using TA = typename A::T;
+    using TO = typename O::T;
+    if (r == nullptr)
+        hipLaunchKernelGGL((add_rmsnorm_generic<A, O, false>), dim3((uint32_t)rows), dim3(256), 0, s,
+                           (const TA *)x, nullptr, nullptr, w, (TO *)y, group, eps);
+    else
+        hipLaunchKernelGGL((add_rmsnorm_generic<A, O, true>), dim3((uint32_t)rows), dim3(256), 0, s,
+                           (const TA *)x, (const TA *)r, (TA *)h, w, (TO *)y, group, eps);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" int fellm_rocm_add_rmsnorm(const void *x, const void *residual, void *h_out,
+                                      uint32_t act_dtype, const float *weight, uint32_t group,
+                                      void *y, uint32_t y_dtype, uint64_t n_elems, float eps,
+                                      void *stream) {
+    using namespace fellm;
+    if (!x || !weight || !y) return FELLM_ERR_ARITY;
+    if (!residual && h_out) return FELLM_ERR_ARITY;
+    if (group == 0 || n_elems == 0 || n_elems % group != 0) return FELLM_ERR_SHAPE;
+    const uint64_t rows = n_elems / group;
+    if (rows > 0x7fffffffull) return FELLM_ERR_SHAPE;
+    hipStream_t s = as_stream(stream);
+    return dispatch_act(act_dtype, [&]<typename A>() -> int {
+        if (y_dtype == act_dtype) return launch_typed<A, A>(x, residual, h_out, weight, y, group, rows, eps, s);
+        if (y_dtype == FELLM_DTYPE_F32) return launch_typed<A, F32>(x, residual, h_out, weight, y, group, rows, eps, s);
+        return FELLM_ERR_DTYPE;
+    });
+}

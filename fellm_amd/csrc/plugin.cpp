@@ -1,0 +1,796 @@
+// FeLLM kernel-plugin C ABI for the gfx950 kernels.
+//
+// Mirrors what plugins/cuda_kernels/src/lib.rs and launchers.rs export to
+// fellm-plugin-host (crates/fellm-plugin-host/src/loader.rs:363-437,
+// registry.rs): ABI version 0.9.0, a JSON manifest, init with a HostContext,
+// per-op registration under (op, input dtypes, output dtype) keys, and
+// launchers with the PluginLaunchFn signature.
+//
+// Buffer contract (plugins/cuda_kernels/src/buffers.rs:119-560,
+// launchers.rs:147-189): TensorRef/TensorMut data are HOST pointers owned by
+// the caller.  The plugin keeps a device mirror per (host ptr, byte length):
+//   * immutable weights (logical_id != 0) are uploaded once per logical id;
+//   * activations are uploaded unless the mirror is already device-valid;
+//   * outputs are produced on the device and marked device-valid; they are
+//     copied back only when FELLM_ROCM_SYNC_OUTPUTS (or the reference's
+//     FELLM_CUDA_SYNC_OUTPUTS) is set, or by an explicit Cast launch;
+//   * _fellm_plugin_invalidate_f32 marks a mirror stale after a host write;
+//   * _fellm_plugin_register_device_tensor binds a host view to an existing
+//     device allocation (no copies at all).
+// All work runs on one non-blocking stream of default priority, exported by
+// _fellm_plugin_device_stream.  Launches are serialised by a process mutex,
+// as in the reference.  Every entry point catches exceptions (-99).
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+#include "fellm_abi.h"
+#include "fellm_rocm.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Custom op ids: OpKind::custom(ns, name) (crates/fellm-plugin-abi/src/op.rs:69-80).
+// ---------------------------------------------------------------------------
+constexpr uint32_t custom_op(const char *ns, const char *name) {
+    uint32_t h = 0x811c9dc5u;
+    for (const char *p = ns; *p; ++p) h = (h ^ (uint8_t)*p) * 0x01000193u;
+    h = (h ^ (uint8_t)':') * 0x01000193u;
+    for (const char *p = name; *p; ++p) h = (h ^ (uint8_t)*p) * 0x01000193u;
+    return h | FELLM_OP_CUSTOM_TAG;
+}
+constexpr uint32_t kOpAddRmsNorm = custom_op("rocm", "add_rmsnorm");
+constexpr uint32_t kOpRopeKvWrite = custom_op("rocm", "rope_kv_write");
+constexpr uint32_t kOpRouterTopK = custom_op("rocm", "router_topk");
+constexpr uint32_t kOpEmbeddingRmsNorm = custom_op("rocm", "embedding_rmsnorm");
+
+struct LaunchError {
+    int code;
+};
+[[noreturn]] void fail(int code) { throw LaunchError{code}; }
+void check(int rc) {
+    if (rc != 0) fail(rc);
+}
+void hip_check(hipError_t e, int code = FELLM_ERR_ALLOC) {
+    if (e != hipSuccess) fail(code);
+}
+
+// ---------------------------------------------------------------------------
+// Process state.
+// ---------------------------------------------------------------------------
+struct Mirror {
+    void *dev = nullptr;
+    size_t bytes = 0;
+    bool device_valid = false;
+};
+
+struct State {
+    std::mutex mu;
+    bool have_ctx = false;
+    FellmHostContext ctx{};
+    hipStream_t stream = nullptr;
+    std::map<std::pair<uintptr_t, size_t>, Mirror> act;          // activations
+    std::unordered_map<uint64_t, Mirror> weights;                 // logical_id (or ptr) -> mirror
+    std::map<std::pair<uintptr_t, size_t>, uint64_t> external;   // registered device tensors
+    Mirror step_params;
+    Mirror scratch;                                              // per-launch small uploads
+    void *pinned = nullptr;                                      // host staging for `scratch`
+    size_t pinned_bytes = 0;
+    bool host_reads_pending = false;  // an H2D copy may still read caller memory
+    Mirror err_flag;                                             // u32 error word
+    int sync_outputs = -1;
+};
+
+State &state() {
+    static State *s = new State();  // never destroyed: device memory outlives static teardown
+    return *s;
+}
+
+hipStream_t stream_locked(State &st) {
+    if (!st.stream) hip_check(hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking));
+    return st.stream;
+}
+
+bool sync_outputs(State &st) {
+    if (st.sync_outputs < 0) {
+        auto on = [](const char *name) {
+            const char *v = std::getenv(name);
+            return v && std::strcmp(v, "0") != 0 && std::strcmp(v, "false") != 0 && std::strcmp(v, "off") != 0;
+        };
+        st.sync_outputs = (on("FELLM_ROCM_SYNC_OUTPUTS") || on("FELLM_CUDA_SYNC_OUTPUTS")) ? 1 : 0;
+    }
+    return st.sync_outputs == 1;
+}
+
+void ensure_capacity(Mirror &m, size_t bytes) {
+    if (m.dev && m.bytes >= bytes) return;
+    if (m.dev) hip_check(hipFree(m.dev));
+    m.dev = nullptr;
+    m.bytes = 0;
+    hip_check(hipMalloc(&m.dev, bytes ? bytes : 1));
+    m.bytes = bytes;
+}
+
+// H2D copy from caller-owned memory.  The caller owns its buffers only for
+// the duration of the launch, so a launch that uploaded anything waits for
+// its stream before returning (see guarded()).
+void upload(State &st, void *dev, const void *host, size_t bytes) {
+    if (!bytes) return;
+    hip_check(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, stream_locked(st)));
+    st.host_reads_pending = true;
+}
+
+const uint64_t *find_external(State &st, const void *host, size_t bytes) {
+    auto it = st.external.find({reinterpret_cast<uintptr_t>(host), bytes});
+    return it == st.external.end() ? nullptr : &it->second;
+}
+
+// Device address of an input, uploading it if needed.
+void *ensure_input(State &st, const FellmTensorRef &t) {
+    if (!t.data || t.byte_len == 0) fail(FELLM_ERR_ARITY);
+    if (const uint64_t *ext = find_external(st, t.data, t.byte_len)) return reinterpret_cast<void *>(*ext);
+    if (t.logical_id != 0) {
+        Mirror &m = st.weights[t.logical_id];
+        if (!m.device_valid || m.bytes != t.byte_len) {
+            ensure_capacity(m, t.byte_len);
+            m.bytes = t.byte_len;
+            upload(st, m.dev, t.data, t.byte_len);
+            m.device_valid = true;
+        }
+        return m.dev;
+    }
+    Mirror &m = st.act[{reinterpret_cast<uintptr_t>(t.data), (size_t)t.byte_len}];
+    if (!m.device_valid) {
+        ensure_capacity(m, t.byte_len);
+        upload(st, m.dev, t.data, t.byte_len);
+        m.device_valid = true;
+    }
+    return m.dev;
+}
+
+// Device address of an output mirror (no upload unless `inout`).
+void *ensure_output(State &st, const FellmTensorMut &t, bool inout = false) {
+    if (!t.data || t.byte_len == 0) fail(FELLM_ERR_ARITY);
+    if (const uint64_t *ext = find_external(st, t.data, t.byte_len)) return reinterpret_cast<void *>(*ext);
+    Mirror &m = st.act[{reinterpret_cast<uintptr_t>(t.data), (size_t)t.byte_len}];
+    if (!m.dev || m.bytes < t.byte_len) {
+        const bool had = m.device_valid && m.dev;
+        if (had) fail(FELLM_ERR_SHAPE);
+        ensure_capacity(m, t.byte_len);
+    }
+    if (inout && !m.device_valid) upload(st, m.dev, t.data, t.byte_len);
+    m.device_valid = false;  // until the launch completes on the stream
+    return m.dev;
+}
+
+// Marks outputs device-valid and downloads them when sync is requested
+// (launchers.rs:174-189).
+void finish_outputs(State &st, FellmTensorMut *outs, uint32_t n, bool sync_host = false) {
+    const bool sync = sync_host || sync_outputs(st);
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!outs[i].data) continue;
+        if (find_external(st, outs[i].data, outs[i].byte_len)) continue;
+        auto it = st.act.find({reinterpret_cast<uintptr_t>(outs[i].data), (size_t)outs[i].byte_len});
+        if (it == st.act.end()) continue;
+        it->second.device_valid = true;
+        if (sync)
+            hip_check(hipMemcpyAsync(outs[i].data, it->second.dev, outs[i].byte_len, hipMemcpyDeviceToHost,
+                                     stream_locked(st)));
+    }
+    if (sync) hip_check(hipStreamSynchronize(stream_locked(st)));
+}
+
+// Small per-launch host arrays (positions, block tables, ids) staged through
+// one growing device buffer.  The copy is ordered on the plugin stream before
+// the kernel that reads it; the host waits for the stream before reusing it.
+void *stage_small(State &st, const std::vector<const void *> &srcs, const std::vector<size_t> &sizes,
+                  std::vector<void *> &dsts) {
+    size_t total = 0;
+    std::vector<size_t> offs;
+    for (size_t sz : sizes) {
+        offs.push_back(total);
+        total += (sz + 255) / 256 * 256;
+    }
+    hip_check(hipStreamSynchronize(stream_locked(st)));  // earlier readers of scratch/pinned are done
+    ensure_capacity(st.scratch, total);
+    if (st.pinned_bytes < total) {
+        if (st.pinned) hip_check(hipHostFree(st.pinned));
+        st.pinned = nullptr;
+        st.pinned_bytes = 0;
+        hip_check(hipHostMalloc(&st.pinned, total, hipHostMallocDefault));
+        st.pinned_bytes = total;
+    }
+    dsts.clear();
+    for (size_t i = 0; i < srcs.size(); ++i) {
+        std::memcpy(static_cast<uint8_t *>(st.pinned) + offs[i], srcs[i], sizes[i]);
+        dsts.push_back(static_cast<uint8_t *>(st.scratch.dev) + offs[i]);
+    }
+    hip_check(hipMemcpyAsync(st.scratch.dev, st.pinned, total, hipMemcpyHostToDevice, stream_locked(st)));
+    return st.scratch.dev;
+}
+
+uint32_t *err_word(State &st) {
+    if (!st.err_flag.dev) {
+        ensure_capacity(st.err_flag, 4);
+    }
+    hip_check(hipMemsetAsync(st.err_flag.dev, 0, 4, stream_locked(st)));
+    return static_cast<uint32_t *>(st.err_flag.dev);
+}
+
+int read_err(State &st) {
+    uint32_t v = 0;
+    hip_check(hipMemcpyAsync(&v, st.err_flag.dev, 4, hipMemcpyDeviceToHost, stream_locked(st)));
+    hip_check(hipStreamSynchronize(stream_locked(st)));
+    return v ? FELLM_ERR_PAGED_RANGE : FELLM_OK;
+}
+
+bool snapshot(State &st, FellmPagedKvSnapshot &out) {
+    if (!st.have_ctx || !st.ctx.snapshot_paged) return false;
+    std::memset(&out, 0, sizeof(out));
+    return st.ctx.snapshot_paged(&out) == 0;
+}
+
+size_t dtype_size(uint32_t dt) {
+    switch (dt) {
+        case FELLM_DTYPE_F32:
+        case FELLM_DTYPE_U32:
+        case FELLM_DTYPE_I32: return 4;
+        case FELLM_DTYPE_F16:
+        case FELLM_DTYPE_BF16: return 2;
+        default: return 0;
+    }
+}
+
+size_t elems(const FellmTensorRef &t, uint32_t dt) {
+    const size_t es = dtype_size(dt);
+    if (!es || t.byte_len % es) fail(FELLM_ERR_SHAPE);
+    return t.byte_len / es;
+}
+size_t elems(const FellmTensorMut &t, uint32_t dt) {
+    const size_t es = dtype_size(dt);
+    if (!es || t.byte_len % es) fail(FELLM_ERR_SHAPE);
+    return t.byte_len / es;
+}
+
+template <typename Body>
+int guarded(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+            uint32_t n_out, uint32_t min_in, uint32_t min_out, bool need_attrs, Body &&body) {
+    try {
+        if (!in || !out || n_in < min_in || n_out < min_out || (need_attrs && !attrs)) return FELLM_ERR_ARITY;
+        State &st = state();
+        std::lock_guard<std::mutex> lock(st.mu);
+        st.host_reads_pending = false;
+        body(st);
+        if (st.host_reads_pending) {
+            st.host_reads_pending = false;
+            hip_check(hipStreamSynchronize(stream_locked(st)));
+        }
+        return FELLM_OK;
+    } catch (const LaunchError &e) {
+        return e.code;
+    } catch (...) {
+        return FELLM_ERR_PANIC;
+    }
+}
+
+void *stream_ptr(State &st) { return reinterpret_cast<void *>(stream_locked(st)); }
+
+// ---------------------------------------------------------------------------
+// Launchers.
+// ---------------------------------------------------------------------------
+
+// RmsNorm [x, w] -> y.  Groups of w.len() (backend.rs:1104-1133 and
+// launchers.rs:336-401 both reduce to this when x.len() % w.len() == 0).
+int launch_rmsnorm(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                   uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 2, 1, true, [&](State &st) {
+        const uint32_t dt = in[0].dtype;
+        if (in[1].dtype != FELLM_DTYPE_F32 || out[0].dtype != dt) fail(FELLM_ERR_DTYPE);
+        const size_t n = elems(in[0], dt), g = elems(in[1], FELLM_DTYPE_F32);
+        if (elems(out[0], dt) != n || g == 0 || n % g) fail(FELLM_ERR_SHAPE);
+        void *x = ensure_input(st, in[0]);
+        void *w = ensure_input(st, in[1]);
+        void *y = ensure_output(st, out[0]);
+        check(fellm_rocm_add_rmsnorm(x, nullptr, nullptr, dt, (const float *)w, (uint32_t)g, y, dt, n, attrs->eps,
+                                     stream_ptr(st)));
+        finish_outputs(st, out, 1);
+    });
+}
+
+// Custom rocm:add_rmsnorm [x, residual, w] -> [h, y].
+int launch_add_rmsnorm(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                       uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 3, 2, true, [&](State &st) {
+        const uint32_t dt = in[0].dtype;
+        if (in[1].dtype != dt || in[2].dtype != FELLM_DTYPE_F32 || out[0].dtype != dt || out[1].dtype != dt)
+            fail(FELLM_ERR_DTYPE);
+        const size_t n = elems(in[0], dt), g = elems(in[2], FELLM_DTYPE_F32);
+        if (elems(in[1], dt) != n || elems(out[0], dt) != n || elems(out[1], dt) != n || g == 0 || n % g)
+            fail(FELLM_ERR_SHAPE);
+        void *x = ensure_input(st, in[0]);
+        void *r = ensure_input(st, in[1]);
+        void *w = ensure_input(st, in[2]);
+        void *h = ensure_output(st, out[0]);
+        void *y = ensure_output(st, out[1]);
+        check(fellm_rocm_add_rmsnorm(x, r, h, dt, (const float *)w, (uint32_t)g, y, dt, n, attrs->eps, stream_ptr(st)));
+        finish_outputs(st, out, 2);
+    });
+}
+
+// Add [a, b] -> out (backend.rs:1543-1553).
+int launch_add(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+               uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 2, 1, false, [&](State &st) {
+        const uint32_t dt = in[0].dtype;
+        if (in[1].dtype != dt || out[0].dtype != dt) fail(FELLM_ERR_DTYPE);
+        const size_t n = elems(in[0], dt);
+        if (elems(in[1], dt) != n || elems(out[0], dt) != n) fail(FELLM_ERR_SHAPE);
+        void *a = ensure_input(st, in[0]);
+        void *b = ensure_input(st, in[1]);
+        void *o = ensure_output(st, out[0]);
+        check(fellm_rocm_add(a, b, dt, o, dt, n, stream_ptr(st)));
+        finish_outputs(st, out, 1);
+    });
+}
+
+// SiluGate [gate, up] -> out (backend.rs:1174-1184, launchers.rs:192-234).
+int launch_silu_gate(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                     uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 2, 1, false, [&](State &st) {
+        const uint32_t dt = in[0].dtype;
+        if (in[1].dtype != dt || out[0].dtype != dt) fail(FELLM_ERR_DTYPE);
+        const size_t n = elems(in[0], dt);
+        if (elems(in[1], dt) != n || elems(out[0], dt) != n) fail(FELLM_ERR_SHAPE);
+        void *g = ensure_input(st, in[0]);
+        void *u = ensure_input(st, in[1]);
+        void *o = ensure_output(st, out[0]);
+        check(fellm_rocm_silu_gate(g, u, dt, o, dt, n, stream_ptr(st)));
+        finish_outputs(st, out, 1);
+    });
+}
+
+// Per-row RoPE positions, as backend.rs:1148-1151: the paged context's
+// row_rope_positions[row] when present, else attrs.position + row.
+std::vector<uint32_t> rope_positions(State &st, const FellmOpAttrs &a, uint32_t rows, bool &any) {
+    std::vector<uint32_t> pos(rows);
+    FellmPagedKvSnapshot snap;
+    any = false;
+    const bool have = snapshot(st, snap) && snap.row_rope_positions;
+    for (uint32_t r = 0; r < rows; ++r) {
+        if (have && r < snap.batch_size) {
+            pos[r] = snap.row_rope_positions[r];
+            any = true;
+        } else {
+            const uint64_t p = (uint64_t)a.position + r;
+            pos[r] = p > 0xffffffffull ? 0xffffffffu : (uint32_t)p;  // saturating_add
+        }
+    }
+    return pos;
+}
+
+// Rope [x, inv_freqs] -> out (backend.rs:1135-1172).
+int launch_rope(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 2, 1, true, [&](State &st) {
+        const FellmOpAttrs &a = *attrs;
+        const uint32_t dt = in[0].dtype;
+        if (in[1].dtype != FELLM_DTYPE_F32 || out[0].dtype != dt) fail(FELLM_ERR_DTYPE);
+        if (a.custom_op_id == 1) fail(FELLM_ERR_DTYPE);  // pre-RoPE side channel: not provided
+        const size_t n = elems(in[0], dt);
+        if (elems(out[0], dt) != n) fail(FELLM_ERR_SHAPE);
+        const size_t nh = a.n_heads ? a.n_heads : 1, hd = a.head_dim ? a.head_dim : 1;
+        const size_t width = nh * hd;
+        if (n % width || elems(in[1], FELLM_DTYPE_F32) < a.rope_dim / 2) fail(FELLM_ERR_SHAPE);
+        const uint32_t rows = (uint32_t)(n / width);
+        bool any = false;
+        std::vector<uint32_t> pos = rope_positions(st, a, rows, any);
+        void *x = ensure_input(st, in[0]);
+        void *f = ensure_input(st, in[1]);
+        void *o = ensure_output(st, out[0]);
+        std::vector<void *> d;
+        const uint32_t *pd = nullptr;
+        if (any) {
+            stage_small(st, {pos.data()}, {pos.size() * 4}, d);
+            pd = static_cast<const uint32_t *>(d[0]);
+        }
+        check(fellm_rocm_rope(x, o, (uint32_t)nh, nullptr, nullptr, 0, dt, rows, (uint32_t)hd, a.rope_dim,
+                              a.rope_pairing, (const float *)f, pd, a.position, stream_ptr(st)));
+        finish_outputs(st, out, 1);
+    });
+}
+
+// Paged geometry from the host snapshot (paged_ctx.rs:14-53); the arena must
+// be device-resident (the ROCm backend allocates it in HBM).
+FellmRocmPagedKv paged_geometry(State &st, const FellmPagedKvSnapshot &snap, uint32_t layer, uint32_t kv_dtype,
+                                std::vector<void *> &staged, const uint32_t *positions_a,
+                                const uint32_t *positions_b) {
+    if (!snap.device_arena || snap.device_arena_len == 0) fail(FELLM_ERR_PAGED_NO_DEVICE);
+    if (snap.elem_bytes != 2 || !snap.block_table || snap.block_size == 0 || snap.tokens_stride == 0)
+        fail(FELLM_ERR_PAGED_RANGE);
+    std::vector<const void *> srcs{snap.block_table};
+    std::vector<size_t> sizes{snap.n_block_table * 4};
+    if (positions_a) {
+        srcs.push_back(positions_a);
+        sizes.push_back(snap.batch_size * 4);
+    }
+    if (positions_b) {
+        srcs.push_back(positions_b);
+        sizes.push_back(snap.batch_size * 4);
+    }
+    stage_small(st, srcs, sizes, staged);
+    FellmRocmPagedKv kv{};
+    kv.arena = snap.device_arena;
+    kv.arena_len = snap.device_arena_len;
+    kv.block_table = static_cast<const uint32_t *>(staged[0]);
+    kv.n_block_table = snap.n_block_table;
+    kv.n_logical_blocks = (uint32_t)snap.n_logical_blocks;
+    kv.n_layers = (uint32_t)snap.n_layers;
+    kv.layer = layer;
+    kv.block_size = (uint32_t)snap.block_size;
+    kv.block_bytes = snap.block_bytes;
+    kv.stride = (uint32_t)snap.tokens_stride;
+    kv.kv_dtype = kv_dtype;
+    return kv;
+}
+
+// KvWrite [row(s), (cache)] -> cache (backend.rs:1734-1793, launchers.rs:3770-3900).
+int launch_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                    uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 1, 1, true, [&](State &st) {
+        const FellmOpAttrs &a = *attrs;
+        const uint32_t dt = in[0].dtype;
+        if (dt != FELLM_DTYPE_F32 && dt != FELLM_DTYPE_F16 && dt != FELLM_DTYPE_BF16) fail(FELLM_ERR_DTYPE);
+        const size_t n = elems(in[0], dt);
+        FellmPagedKvSnapshot snap;
+        const bool paged = a.block_size > 0 && snapshot(st, snap);
+        if (paged) {
+            const size_t batch = snap.batch_size ? snap.batch_size : 1;
+            if (snap.tokens_stride == 0 || n != batch * snap.tokens_stride) fail(FELLM_ERR_SHAPE);
+            if (!snap.row_positions) fail(FELLM_ERR_PAGED_MISSING);
+            void *rows = ensure_input(st, in[0]);
+            std::vector<void *> staged;
+            FellmRocmPagedKv kv = paged_geometry(st, snap, a.layer_ord, FELLM_DTYPE_F16, staged, snap.row_positions, nullptr);
+            uint32_t *err = err_word(st);
+            check(fellm_rocm_kv_write(rows, dt, (uint32_t)batch, static_cast<const uint32_t *>(staged[1]), &kv,
+                                      a.kv_slot != 0, err, stream_ptr(st)));
+            check(read_err(st));
+            return;
+        }
+        // Contiguous layout (also when block_size > 0 but no paged context is
+        // installed, as backend.rs:1742 does): kv_buf [max_seq, dim] of the
+        // row dtype, row written at attrs.position.
+        FellmTensorMut &buf = out[0];
+        if (buf.dtype != dt || buf.rank != 2) fail(FELLM_ERR_SHAPE);
+        const size_t max_seq = buf.dims[0], dim = buf.dims[1];
+        if (n != dim) fail(FELLM_ERR_SHAPE);
+        if (a.position >= max_seq) fail(FELLM_ERR_SHAPE);
+        if (elems(buf, dt) < max_seq * dim) fail(FELLM_ERR_SHAPE);
+        void *row = ensure_input(st, in[0]);
+        void *cache = ensure_output(st, buf, /*inout=*/true);
+        const size_t es = dtype_size(dt);
+        hip_check(hipMemcpyAsync(static_cast<uint8_t *>(cache) + (size_t)a.position * dim * es, row, dim * es,
+                                 hipMemcpyDeviceToDevice, stream_locked(st)),
+                  FELLM_ERR_LAUNCH);
+        finish_outputs(st, out, 1);
+    });
+}
+
+// Custom rocm:rope_kv_write [q, k, v, inv_freqs] -> [q_out, (k_out)].
+// attrs: n_heads, n_kv_heads, head_dim, rope_dim, rope_pairing, layer_ord,
+// cast_to = cache dtype (BF16, else F16 as in the reference arena).
+int launch_rope_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                         uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 4, 1, true, [&](State &st) {
+        const FellmOpAttrs &a = *attrs;
+        const uint32_t dt = in[0].dtype;
+        if (in[1].dtype != dt || in[2].dtype != dt || in[3].dtype != FELLM_DTYPE_F32 || out[0].dtype != dt)
+            fail(FELLM_ERR_DTYPE);
+        FellmPagedKvSnapshot snap;
+        if (!snapshot(st, snap) || !snap.row_positions) fail(FELLM_ERR_PAGED_MISSING);
+        const size_t batch = snap.batch_size ? snap.batch_size : 1;
+        const size_t hd = a.head_dim, nq = a.n_heads, nkv = a.n_kv_heads;
+        if (!hd || !nq || !nkv) fail(FELLM_ERR_SHAPE);
+        if (elems(in[0], dt) != batch * nq * hd || elems(in[1], dt) != batch * nkv * hd ||
+            elems(in[2], dt) != batch * nkv * hd || elems(out[0], dt) != batch * nq * hd ||
+            snap.tokens_stride != nkv * hd)
+            fail(FELLM_ERR_SHAPE);
+        const bool has_kout = n_out >= 2 && out[1].data;
+        if (has_kout && (out[1].dtype != dt || elems(out[1], dt) != batch * nkv * hd)) fail(FELLM_ERR_SHAPE);
+        void *q = ensure_input(st, in[0]);
+        void *k = ensure_input(st, in[1]);
+        void *v = ensure_input(st, in[2]);
+        void *f = ensure_input(st, in[3]);
+        void *qo = ensure_output(st, out[0]);
+        void *ko = has_kout ? ensure_output(st, out[1]) : nullptr;
+        const uint32_t kv_dt = a.cast_to == FELLM_DTYPE_BF16 ? FELLM_DTYPE_BF16 : FELLM_DTYPE_F16;
+        std::vector<void *> staged;
+        FellmRocmPagedKv kv = paged_geometry(st, snap, a.layer_ord, kv_dt, staged, snap.row_positions,
+                                             snap.row_rope_positions);
+        const uint32_t *rope_pos = snap.row_rope_positions ? static_cast<const uint32_t *>(staged[2]) : nullptr;
+        uint32_t *err = err_word(st);
+        check(fellm_rocm_rope_kv_write(q, qo, (uint32_t)nq, k, ko, v, (uint32_t)nkv, dt, (uint32_t)batch, (uint32_t)hd,
+                                       a.rope_dim, a.rope_pairing, (const float *)f, rope_pos,
+                                       static_cast<const uint32_t *>(staged[1]), &kv, err, stream_ptr(st)));
+        finish_outputs(st, out, has_kout ? 2 : 1);
+        check(read_err(st));
+    });
+}
+
+void check_ids(const FellmTensorRef &ids_t, uint64_t vocab, std::vector<uint32_t> &ids) {
+    if (ids_t.dtype != FELLM_DTYPE_U32 || !ids_t.data || ids_t.byte_len == 0 || ids_t.byte_len % 4) fail(FELLM_ERR_SHAPE);
+    ids.resize(ids_t.byte_len / 4);
+    std::memcpy(ids.data(), ids_t.data, ids_t.byte_len);
+    for (uint32_t id : ids)
+        if (id >= vocab) fail(FELLM_ERR_SHAPE);  // CPU panics on out-of-range rows; CUDA returns -2
+}
+
+uint64_t table_row_bytes(uint32_t dt, uint64_t dim) {
+    switch (dt) {
+        case FELLM_DTYPE_Q4K: return dim % 256 ? 0 : dim / 256 * 144;
+        case FELLM_DTYPE_Q6K: return dim % 256 ? 0 : dim / 256 * 210;
+        default: return dim * dtype_size(dt);
+    }
+}
+
+// Embedding [table, ids] -> rows (backend.rs:1026-1046).
+int launch_embedding(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                     uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 2, 1, false, [&](State &st) {
+        const FellmTensorRef &w = in[0];
+        if (w.rank < 2) fail(FELLM_ERR_SHAPE);
+        const uint64_t vocab = w.dims[0], dim = w.dims[1];
+        const uint64_t rb = table_row_bytes(w.dtype, dim);
+        if (!rb || w.byte_len < vocab * rb || dim > 0xffffffffull) fail(FELLM_ERR_SHAPE);
+        std::vector<uint32_t> ids;
+        check_ids(in[1], vocab, ids);
+        const uint32_t odt = out[0].dtype;
+        if (elems(out[0], odt) != ids.size() * dim) fail(FELLM_ERR_SHAPE);
+        void *table = ensure_input(st, w);
+        std::vector<void *> staged;
+        stage_small(st, {ids.data()}, {ids.size() * 4}, staged);
+        void *idd = staged[0];
+        void *o = ensure_output(st, out[0]);
+        check(fellm_rocm_embedding(table, w.dtype, vocab, (uint32_t)dim, (const uint32_t *)idd, (uint32_t)ids.size(), o,
+                                   odt, nullptr, stream_ptr(st)));
+        finish_outputs(st, out, 1);
+    });
+}
+
+// Custom rocm:embedding_rmsnorm [table, ids, w] -> [h, y]; attrs.eps.
+int launch_embedding_rmsnorm(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                             uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 3, 2, true, [&](State &st) {
+        const FellmTensorRef &w = in[0];
+        if (w.rank < 2) fail(FELLM_ERR_SHAPE);
+        const uint64_t vocab = w.dims[0], dim = w.dims[1];
+        const uint64_t rb = table_row_bytes(w.dtype, dim);
+        if (!rb || w.byte_len < vocab * rb || dim > 0xffffffffull) fail(FELLM_ERR_SHAPE);
+        std::vector<uint32_t> ids;
+        check_ids(in[1], vocab, ids);
+        if (in[2].dtype != FELLM_DTYPE_F32 || elems(in[2], FELLM_DTYPE_F32) != dim) fail(FELLM_ERR_SHAPE);
+        const uint32_t odt = out[0].dtype;
+        if (out[1].dtype != odt || elems(out[0], odt) != ids.size() * dim || elems(out[1], odt) != ids.size() * dim)
+            fail(FELLM_ERR_SHAPE);
+        void *table = ensure_input(st, w);
+        std::vector<void *> staged;
+        stage_small(st, {ids.data()}, {ids.size() * 4}, staged);
+        void *idd = staged[0];
+        void *nw = ensure_input(st, in[2]);
+        void *h = ensure_output(st, out[0]);
+        void *y = ensure_output(st, out[1]);
+        check(fellm_rocm_embedding_rmsnorm(table, w.dtype, vocab, (uint32_t)dim, (const uint32_t *)idd,
+                                           (uint32_t)ids.size(), (const float *)nw, attrs->eps, h, y, odt, nullptr,
+                                           stream_ptr(st)));
+        finish_outputs(st, out, 2);
+    });
+}
+
+// Custom rocm:router_topk [logits f32 [T, E]] -> [ids u32 [T, k], weights f32 [T, k]].
+int launch_router_topk(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                       uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 1, 2, true, [&](State &st) {
+        const FellmOpAttrs &a = *attrs;
+        if (in[0].dtype != FELLM_DTYPE_F32 || out[0].dtype != FELLM_DTYPE_U32 || out[1].dtype != FELLM_DTYPE_F32)
+            fail(FELLM_ERR_DTYPE);
+        const size_t n = elems(in[0], FELLM_DTYPE_F32), e = a.n_experts;
+        if (!e || n % e) fail(FELLM_ERR_SHAPE);
+        const size_t tokens = n / e;
+        const size_t k = a.n_expert_used < e ? a.n_expert_used : e;
+        if (elems(out[0], FELLM_DTYPE_U32) != tokens * k || elems(out[1], FELLM_DTYPE_F32) != tokens * k)
+            fail(FELLM_ERR_SHAPE);
+        void *l = ensure_input(st, in[0]);
+        void *ids = ensure_output(st, out[0]);
+        void *wts = ensure_output(st, out[1]);
+        check(fellm_rocm_router_topk((const float *)l, (uint32_t)tokens, (uint32_t)e, a.n_expert_used,
+                                     a.expert_gating_func, a.norm_topk_prob, a.routed_scaling_factor,
+                                     (uint32_t *)ids, (float *)wts, stream_ptr(st)));
+        finish_outputs(st, out, 2);
+    });
+}
+
+// Cast [x f32] -> host f32: materialise a device-valid mirror into host
+// storage (launchers.rs:140-170).
+int launch_materialize(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                       uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 1, 1, false, [&](State &st) {
+        if (in[0].byte_len != out[0].byte_len || !out[0].data) fail(FELLM_ERR_SHAPE);
+        void *src = ensure_input(st, in[0]);
+        hip_check(hipMemcpyAsync(out[0].data, src, out[0].byte_len, hipMemcpyDeviceToHost, stream_locked(st)));
+        hip_check(hipStreamSynchronize(stream_locked(st)), FELLM_ERR_ALLOC);
+    });
+}
+
+const char kManifest[] =
+    "{\"schema\":1,\"id\":\"fellm.rocm\",\"name\":\"FeLLM ROCm gfx950 kernels\",\"version\":\"0.1.0\","
+    "\"provides\":[{\"type\":\"backend\",\"id\":\"rocm\"},{\"type\":\"kernels\",\"backend\":\"rocm\"}]}";
+
+int register_one(FellmKernelRegistryVtable *vt, uint32_t op, std::initializer_list<uint32_t> ins, uint32_t out,
+                 FellmPluginLaunchFn fn) {
+    FellmPluginOpRegistration reg;
+    std::memset(&reg, 0, sizeof(reg));
+    reg.op_kind = op;
+    reg.n_input_dtypes = (uint32_t)ins.size();
+    uint32_t i = 0;
+    for (uint32_t d : ins) reg.input_dtypes[i++] = d;
+    reg.output_dtype = out;
+    reg.launch = fn;
+    return vt->register_op(vt->registry, &reg);
+}
+
+}  // namespace
+
+extern "C" {
+
+FellmAbiVersion _fellm_plugin_abi_version(void) { return FellmAbiVersion{0, 9, 0}; }
+
+FellmPluginManifestJson _fellm_plugin_manifest_json(void) {
+    return FellmPluginManifestJson{reinterpret_cast<const uint8_t *>(kManifest), sizeof(kManifest) - 1};
+}
+
+int _fellm_plugin_init(const FellmHostContext *ctx) {
+    try {
+        if (!ctx) return FELLM_ERR_ARITY;
+        State &st = state();
+        std::lock_guard<std::mutex> lock(st.mu);
+        st.ctx = *ctx;
+        st.have_ctx = true;
+        return FELLM_OK;  // device work is deferred to the first launch
+    } catch (...) {
+        return FELLM_ERR_PANIC;
+    }
+}
+
+int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
+    try {
+        if (!vt || !vt->register_op) return FELLM_ERR_ARITY;
+        const uint32_t F32 = FELLM_DTYPE_F32, F16 = FELLM_DTYPE_F16, BF16 = FELLM_DTYPE_BF16;
+        const uint32_t Q4K = FELLM_DTYPE_Q4K, Q6K = FELLM_DTYPE_Q6K, U32 = FELLM_DTYPE_U32;
+        struct R {
+            uint32_t op;
+            std::initializer_list<uint32_t> ins;
+            uint32_t out;
+            FellmPluginLaunchFn fn;
+        };
+        const R regs[] = {
+            // Reference keys (plugins/cuda_kernels/src/lib.rs:337-720).
+            {FELLM_OP_CAST, {F32}, F32, launch_materialize},
+            {FELLM_OP_RMSNORM, {F32, F32}, F32, launch_rmsnorm},
+            {FELLM_OP_SILU_GATE, {F32, F32}, F32, launch_silu_gate},
+            {FELLM_OP_ROPE, {F32, F32}, F32, launch_rope},
+            {FELLM_OP_KV_WRITE, {F32, F32}, F32, launch_kv_write},
+            {FELLM_OP_ADD, {F32, F32}, F32, launch_add},
+            {FELLM_OP_EMBEDDING, {F32, U32}, F32, launch_embedding},
+            {FELLM_OP_EMBEDDING, {BF16, U32}, F32, launch_embedding},
+            {FELLM_OP_EMBEDDING, {Q4K, U32}, F32, launch_embedding},
+            {FELLM_OP_EMBEDDING, {Q6K, U32}, F32, launch_embedding},
+            // backend-cpu also serves F16 tables (backend.rs:453-467).
+            {FELLM_OP_EMBEDDING, {F16, U32}, F32, launch_embedding},
+            // 16-bit activation variants.
+            {FELLM_OP_RMSNORM, {F16, F32}, F16, launch_rmsnorm},
+            {FELLM_OP_RMSNORM, {BF16, F32}, BF16, launch_rmsnorm},
+            {FELLM_OP_SILU_GATE, {F16, F16}, F16, launch_silu_gate},
+            {FELLM_OP_SILU_GATE, {BF16, BF16}, BF16, launch_silu_gate},
+            {FELLM_OP_ROPE, {F16, F32}, F16, launch_rope},
+            {FELLM_OP_ROPE, {BF16, F32}, BF16, launch_rope},
+            {FELLM_OP_ADD, {F16, F16}, F16, launch_add},
+            {FELLM_OP_ADD, {BF16, BF16}, BF16, launch_add},
+            {FELLM_OP_KV_WRITE, {F16, F32}, F32, launch_kv_write},
+            {FELLM_OP_KV_WRITE, {BF16, F32}, F32, launch_kv_write},
+            {FELLM_OP_EMBEDDING, {F16, U32}, F16, launch_embedding},
+            {FELLM_OP_EMBEDDING, {BF16, U32}, BF16, launch_embedding},
+            {FELLM_OP_EMBEDDING, {Q4K, U32}, F16, launch_embedding},
+            {FELLM_OP_EMBEDDING, {Q6K, U32}, F16, launch_embedding},
+            // Fused custom ops (OpKind::custom("rocm", ...)).
+            {kOpAddRmsNorm, {F32, F32, F32}, F32, launch_add_rmsnorm},
+            {kOpAddRmsNorm, {F16, F16, F32}, F16, launch_add_rmsnorm},
+            {kOpAddRmsNorm, {BF16, BF16, F32}, BF16, launch_add_rmsnorm},
+            {kOpRopeKvWrite, {F32, F32, F32, F32}, F32, launch_rope_kv_write},
+            {kOpRopeKvWrite, {F16, F16, F16, F32}, F16, launch_rope_kv_write},
+            {kOpRopeKvWrite, {BF16, BF16, BF16, F32}, BF16, launch_rope_kv_write},
+            {kOpRouterTopK, {F32}, U32, launch_router_topk},
+            {kOpEmbeddingRmsNorm, {F32, U32, F32}, F32, launch_embedding_rmsnorm},
+            {kOpEmbeddingRmsNorm, {F16, U32, F32}, F16, launch_embedding_rmsnorm},
+            {kOpEmbeddingRmsNorm, {Q4K, U32, F32}, F16, launch_embedding_rmsnorm},
+            {kOpEmbeddingRmsNorm, {Q6K, U32, F32}, F16, launch_embedding_rmsnorm},
+        };
+        int idx = 0;
+        for (const R &r : regs) {
+            ++idx;
+            if (register_one(vt, r.op, r.ins, r.out, r.fn) != 0) return -100 - idx;
+        }
+        return FELLM_OK;
+    } catch (...) {
+        return FELLM_ERR_PANIC;
+    }
+}
+
+void _fellm_plugin_shutdown(void) {
+    try {
+        State &st = state();
+        std::lock_guard<std::mutex> lock(st.mu);
+        st.have_ctx = false;
+        std::memset(&st.ctx, 0, sizeof(st.ctx));
+    } catch (...) {
+    }
+}
+
+void _fellm_plugin_invalidate_f32(const float *ptr, size_t nbytes) {
+    try {
+        if (!ptr || nbytes == 0) return;
+        State &st = state();
+        std::lock_guard<std::mutex> lock(st.mu);
+        auto it = st.act.find({reinterpret_cast<uintptr_t>(ptr), nbytes});
+        if (it != st.act.end()) it->second.device_valid = false;
+    } catch (...) {
+    }
+}
+
+FellmStreamHandle _fellm_plugin_device_stream(void) {
+    try {
+        State &st = state();
+        std::lock_guard<std::mutex> lock(st.mu);
+        return reinterpret_cast<FellmStreamHandle>(stream_locked(st));
+    } catch (...) {
+        return 0;
+    }
+}
+
+int _fellm_plugin_update_step_params(const FellmDeviceStepParams *params) {
+    try {
+        if (!params) return FELLM_ERR_ARITY;
+        State &st = state();
+        std::lock_guard<std::mutex> lock(st.mu);
+        ensure_capacity(st.step_params, sizeof(FellmDeviceStepParams));
+        upload(st, st.step_params.dev, params, sizeof(FellmDeviceStepParams));
+        hip_check(hipStreamSynchronize(stream_locked(st)));
+        return FELLM_OK;
+    } catch (const LaunchError &e) {
+        return e.code;
+    } catch (...) {
+        return FELLM_ERR_PANIC;
+    }
+}
+
+int _fellm_plugin_register_device_tensor(const uint8_t *host_ptr, size_t nbytes, uint64_t device_ptr) {
+    try {
+        if (!host_ptr || nbytes == 0 || device_ptr == 0) return FELLM_ERR_ARITY;
+        State &st = state();
+        std::lock_guard<std::mutex> lock(st.mu);
+        st.external[{reinterpret_cast<uintptr_t>(host_ptr), nbytes}] = device_ptr;
+        return FELLM_OK;
+    } catch (...) {
+        return FELLM_ERR_PANIC;
+    }
+}
+
+const char *fellm_rocm_version(void) { return "fellm-rocm 0.1.0 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,335 @@
+// Rotary position embedding, paged KV append, and the two fused.
+//
+// RoPE reference: crates/backend-cpu/src/backend.rs:1135-1172 (launch_rope)
+//   -> kernels/rope.rs:28-62 (rope_inplace_with_freqs_ex):
+//   theta = (pos as f32) * inv_freq[i]; (s, c) = sin_cos(theta)
+//   a' = a*c - b*s;  b' = a*s + b*c        (no FMA contraction)
+//   pairing 0: (2i, 2i+1); 1: (i, i + rope_dim/2); 2: adjacent over the last
+//   rope_dim dims of the head.  Dims outside the rotated span pass through.
+// KvWrite reference: backend.rs:1734-1775 and the paged addressing of
+//   crates/fellm-plugin-abi/src/paged_ctx.rs:341-360 (row_mut_for),
+//   block bytes from crates/backend-cuda/src/vram_pool.rs:31-35.
+//
+// One workgroup handles one token row.  The rope_dim/2 (sin, cos) pairs for
+// that row's position are computed once into LDS (in double precision, then
+// rounded to f32, which matches the correctly-rounded libm values) and shared
+// by every head of q and k, instead of once per (head, pair) as on the CPU.
+// The row is then cut into items of PV pairs (PV = 4: one 16-byte access per
+// item for 16-bit activations) spread over the block.  In KV mode the rotated
+// K row and the V row are also rounded once to the cache dtype and written
+// into their paged slots, so K never makes an extra HBM round trip.
+#include <initializer_list>
+
+#include "common.hpp"
+
+namespace fellm {
+namespace {
+
+constexpr int kRopeBlock = 256;
+constexpr uint32_t kMaxHalf = 512;  // rope_dim <= 1024
+
+struct KvDev {
+    uint8_t *arena;
+    uint64_t arena_len;
+    const uint32_t *table;
+    uint64_t n_table;
+    uint32_t n_logical, n_layers, layer, block_size;
+    uint64_t block_bytes;
+    uint32_t stride;
+};
+
+// Byte offset of (batch row, position)'s K row, or UINT64_MAX if the slot lies
+// outside the table or the arena.  V rows sit block_size rows further on.
+__device__ __forceinline__ uint64_t kv_slot_offset(const KvDev &kv, uint32_t row, uint32_t pos) {
+    const uint32_t logical = pos / kv.block_size;
+    const uint32_t slot = pos % kv.block_size;
+    if (logical >= kv.n_logical) return ~0ull;
+    const uint64_t idx = ((uint64_t)row * kv.n_layers + kv.layer) * kv.n_logical + logical;
+    if (idx >= kv.n_table) return ~0ull;
+    const uint64_t phys = kv.table[idx];
+    const uint64_t row_bytes = (uint64_t)kv.stride * 2;
+    const uint64_t base = phys * kv.block_bytes + (uint64_t)slot * row_bytes;
+    if (base + (uint64_t)kv.block_size * row_bytes + row_bytes > kv.arena_len) return ~0ull;
+    return base;
+}
+
+template <typename C, int N>
+__device__ __forceinline__ void store_cache(uint8_t *arena, uint64_t byte_off, uint32_t elem,
+                                            const float (&v)[N]) {
+    store_f32<C, N>(reinterpret_cast<typename C::T *>(arena + byte_off) + elem, v);
+}
+
+// Rotates item `it` of one head.  Items [0, n_rot) are rotated, the rest
+// pass through.  Returns the element offsets of the two runs of PV values.
+template <typename A, int PV>
+__device__ __forceinline__ void rope_item(const typename A::T *src, uint32_t it, uint32_t n_rot,
+                                          uint32_t head_dim, uint32_t rope_dim, uint32_t pairing,
+                                          const float2 *cs, float (&lo)[PV], float (&hi)[PV],
+                                          uint32_t &off_lo, uint32_t &off_hi) {
+    if (it >= n_rot) {  // passthrough: 2*PV consecutive elements after the rotated span
+        const uint32_t start = pairing == 2 ? 0 : rope_dim;
+        off_lo = start + (it - n_rot) * 2 * PV;
+        off_hi = off_lo + PV;
+        load_f32<A, PV>(src + off_lo, lo);
+        load_f32<A, PV>(src + off_hi, hi);
+        return;
+    }
+    if (pairing == 1) {
+        const uint32_t half = rope_dim / 2;
+        const uint32_t i0 = it * PV;
+        off_lo = i0;
+        off_hi = i0 + half;
+        float a[PV], b[PV];
+        load_f32<A, PV>(src + off_lo, a);
+        load_f32<A, PV>(src + off_hi, b);
+#pragma unroll
+        for (int k = 0; k < PV; ++k) {
+            const float2 sc = cs[i0 + k];  // (sin, cos)
+            lo[k] = a[k] * sc.y - b[k] * sc.x;
+            hi[k] = a[k] * sc.x + b[k] * sc.y;
+        }
+        return;
+    }
+    // Adjacent pairs; pairing 2 shifts the span to the tail of the head.
+    const uint32_t start = pairing == 2 ? head_dim - rope_dim : 0;
+    const uint32_t i0 = it * PV;  // first pair index
+    off_lo = start + 2 * i0;
+    off_hi = off_lo + PV;
+    float e[2 * PV];
+    load_f32<A, 2 * PV>(src + off_lo, e);
+#pragma unroll
+    for (int k = 0; k < PV; ++k) {
+        const float2 sc = cs[i0 + k];
+        const float a = e[2 * k], b = e[2 * k + 1];
+        e[2 * k] = a * sc.y - b * sc.x;
+        e[2 * k + 1] = a * sc.x + b * sc.y;
+    }
+#pragma unroll
+    for (int k = 0; k < PV; ++k) {
+        lo[k] = e[k];
+        hi[k] = e[PV + k];
+    }
+}
+
+// MODE 0: rotate x1 -> out1 and x2 -> out2.
+// MODE 1: additionally write rotated x2 (K) and x3 (V) into the paged cache
+//         (cache element type C).
+template <typename A, typename C, int PV, int MODE>
+__global__ __launch_bounds__(kRopeBlock) void rope_kernel(
+    // x1/out1 and x2/out2 may alias (in-place rotation): no __restrict__.
+    const typename A::T *x1, typename A::T *out1, uint32_t nh1,
+    const typename A::T *x2, typename A::T *out2, uint32_t nh2,
+    const typename A::T *__restrict__ x3, uint32_t head_dim, uint32_t rope_dim, uint32_t pairing,
+    const float *__restrict__ inv_freqs, const uint32_t *__restrict__ rope_pos, uint32_t pos0,
+    const uint32_t *__restrict__ kv_pos, KvDev kv, uint32_t *__restrict__ err) {
+    __shared__ float2 cs[kMaxHalf];
+    const uint32_t row = blockIdx.x;
+    uint32_t pos;
+    if constexpr (MODE == 1)
+        pos = rope_pos ? rope_pos[row] : kv_pos[row];
+    else
+        pos = rope_pos ? rope_pos[row] : pos0 + row;
+    const uint32_t half = rope_dim / 2;
+    const float pf = (float)pos;
+    for (uint32_t i = threadIdx.x; i < half; i += kRopeBlock) {
+        const float theta = pf * inv_freqs[i];
+        double sd, cd;
+        sincos((double)theta, &sd, &cd);
+        cs[i] = make_float2((float)sd, (float)cd);
+    }
+    uint64_t kbase = ~0ull;
+    if constexpr (MODE == 1) {
+        kbase = kv_slot_offset(kv, row, kv_pos[row]);
+        if (kbase == ~0ull && threadIdx.x == 0 && err) atomicOr(err, 1u);
+    }
+    __syncthreads();
+
+    const uint32_t n_rot = half / PV;  // rotated items of PV pairs
+    const uint32_t items_head = head_dim / (2 * PV);             // all items of a head
+    const uint32_t items1 = nh1 * items_head;
+    const uint32_t items2 = x2 ? nh2 * items_head : 0;
+    const uint32_t items3 = (MODE == 1) ? nh2 * items_head : 0;
+    const uint32_t total = items1 + items2 + items3;
+    const size_t w1 = (size_t)nh1 * head_dim, w2 = (size_t)nh2 * head_dim;
+    const uint64_t v_off = (uint64_t)kv.block_size * kv.stride * 2;
+
+    for (uint32_t u = threadIdx.x; u < total; u += kRopeBlock) {
+        float lo[PV], hi[PV];
+        uint32_t off_lo, off_hi;
+        if (u < items1) {
+            const uint32_t hd = u / items_head, it = u % items_head;
+            const size_t base = (size_t)row * w1 + (size_t)hd * head_dim;
+            rope_item<A, PV>(x1 + base, it, n_rot, head_dim, rope_dim, pairing, cs, lo, hi, off_lo, off_hi);
+            if (out1 != x1 || it < n_rot) {
+                store_f32<A, PV>(out1 + base + off_lo, lo);
+                store_f32<A, PV>(out1 + base + off_hi, hi);
+            }
+        } else if (u < items1 + items2) {
+            const uint32_t v = u - items1;
+            const uint32_t hd = v / items_head, it = v % items_head;
+            const size_t base = (size_t)row * w2 + (size_t)hd * head_dim;
+            rope_item<A, PV>(x2 + base, it, n_rot, head_dim, rope_dim, pairing, cs, lo, hi, off_lo, off_hi);
+            if (out2 && (out2 != x2 || it < n_rot)) {
+                store_f32<A, PV>(out2 + base + off_lo, lo);
+                store_f32<A, PV>(out2 + base + off_hi, hi);
+            }
+            if constexpr (MODE == 1) {
+                if (kbase != ~0ull) {
+                    const uint32_t e = hd * head_dim;
+                    store_cache<C, PV>(kv.arena, kbase, e + off_lo, lo);
+                    store_cache<C, PV>(kv.arena, kbase, e + off_hi, hi);
+                }
+            }
+        } else if constexpr (MODE == 1) {
+            // V row: 2*PV consecutive elements per item, converted to the cache dtype.
+            const uint32_t v = u - items1 - items2;
+            const uint32_t e = v * 2 * PV;
+            float vals[2 * PV];
+            load_f32<A, 2 * PV>(x3 + (size_t)row * w2 + e, vals);
+            if (kbase != ~0ull)
+                store_f32<C, 2 * PV>(reinterpret_cast<typename C::T *>(kv.arena + kbase + v_off) + e, vals);
+        }
+    }
+}
+
+// Standalone KvWrite: one workgroup per batch row, items of VEC elements.
+template <typename A, typename C, int VEC>
+__global__ __launch_bounds__(kRopeBlock) void kv_write_kernel(const typename A::T *__restrict__ rows,
+                                                              const uint32_t *__restrict__ kv_pos,
+                                                              KvDev kv, uint32_t is_v,
+                                                              uint32_t *__restrict__ err) {
+    const uint32_t row = blockIdx.x;
+    const uint64_t base = kv_slot_offset(kv, row, kv_pos[row]);
+    if (base == ~0ull) {
+        if (threadIdx.x == 0 && err) atomicOr(err, 1u);
+        return;
+    }
+    const uint64_t off = base + (is_v ? (uint64_t)kv.block_size * kv.stride * 2 : 0);
+    typename C::T *dst = reinterpret_cast<typename C::T *>(kv.arena + off);
+    const typename A::T *src = rows + (size_t)row * kv.stride;
+    for (uint32_t e = threadIdx.x * VEC; e < kv.stride; e += kRopeBlock * VEC) {
+        float v[VEC];
+        load_f32<A, VEC>(src + e, v);
+        store_f32<C, VEC>(dst + e, v);
+    }
+}
+
+bool make_kv(const FellmRocmPagedKv *p, KvDev &kv) {
+    if (!p || !p->arena || !p->block_table || p->block_size == 0 || p->stride == 0 || p->n_layers == 0 ||
+        p->n_logical_blocks == 0 || p->layer >= p->n_layers)
+        return false;
+    // A block holds block_size K rows then block_size V rows of 2-byte elements.
+    if (p->block_bytes < (uint64_t)2 * p->block_size * p->stride * 2 || p->block_bytes % 4) return false;
+    kv = KvDev{(uint8_t *)p->arena, p->arena_len, p->block_table, p->n_block_table, p->n_logical_blocks,
+               p->n_layers, p->layer, p->block_size, p->block_bytes, p->stride};
+    return true;
+}
+
+template <typename Fn>
+int dispatch_cache(uint32_t kv_dtype, Fn &&f) {
+    if (kv_dtype == FELLM_DTYPE_F16) return f.template operator()<F16>();
+    if (kv_dtype == FELLM_DTYPE_BF16) return f.template operator()<BF16>();
+    return FELLM_ERR_DTYPE;
+}
+
+// PV = 4 needs every item boundary on a 4-pair (8-element) grid and
+// 8-element-aligned rows; otherwise single pairs.
+bool rope_vec_ok(uint32_t head_dim, uint32_t rope_dim, uint32_t pairing, size_t esize,
+                 std::initializer_list<const void *> ptrs) {
+    if (head_dim % 8 || rope_dim % 8) return false;
+    (void)pairing;
+    for (const void *p : ptrs)
+        if (p && !aligned_to(p, esize * 8)) return false;
+    return true;
+}
+
+int check_rope_shape(uint32_t head_dim, uint32_t rope_dim, uint32_t pairing) {
+    if (head_dim == 0 || head_dim % 2) return FELLM_ERR_SHAPE;
+    if (rope_dim % 2 || rope_dim > head_dim || rope_dim / 2 > kMaxHalf) return FELLM_ERR_SHAPE;
+    if (pairing > 2) return FELLM_ERR_SHAPE;
+    return FELLM_OK;
+}
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" int fellm_rocm_rope(const void *x1, void *out1, uint32_t n_heads1, const void *x2, void *out2,
+                               uint32_t n_heads2, uint32_t act_dtype, uint32_t rows, uint32_t head_dim,
+                               uint32_t rope_dim, uint32_t pairing, const float *inv_freqs,
+                               const uint32_t *positions, uint32_t position0, void *stream) {
+    using namespace fellm;
+    if (!x1 || !out1 || (rope_dim && !inv_freqs) || n_heads1 == 0) return FELLM_ERR_ARITY;
+    if (x2 && (!out2 || n_heads2 == 0)) return FELLM_ERR_ARITY;
+    if (int rc = check_rope_shape(head_dim, rope_dim, pairing)) return rc;
+    if (rows == 0) return FELLM_OK;
+    hipStream_t s = as_stream(stream);
+    return dispatch_act(act_dtype, [&]<typename A>() -> int {
+        using T = typename A::T;
+        const bool vec = rope_vec_ok(head_dim, rope_dim, pairing, sizeof(T), {x1, out1, x2, out2});
+        auto go = [&]<int PV>() {
+            hipLaunchKernelGGL((rope_kernel<A, F16, PV, 0>), dim3(rows), dim3(kRopeBlock), 0, s, (const T *)x1,
+                               (T *)out1, n_heads1, (const T *)x2, (T *)out2, x2 ? n_heads2 : 0, nullptr,
+                               head_dim, rope_dim, pairing, inv_freqs, positions, position0, nullptr, KvDev{},
+                               nullptr);
+            return launch_status();
+        };
+        return vec ? go.template operator()<4>() : go.template operator()<1>();
+    });
+}
+
+extern "C" int fellm_rocm_kv_write(const void *rows, uint32_t act_dtype, uint32_t batch,
+                                   const uint32_t *kv_positions, const FellmRocmPagedKv *kvp, uint32_t is_v,
+                                   uint32_t *err_flag, void *stream) {
+    using namespace fellm;
+    if (!rows || !kv_positions || !kvp) return FELLM_ERR_ARITY;
+    KvDev kv;
+    if (!make_kv(kvp, kv)) return FELLM_ERR_SHAPE;
+    if (batch == 0) return FELLM_OK;
+    hipStream_t s = as_stream(stream);
+    return dispatch_act(act_dtype, [&]<typename A>() -> int {
+        return dispatch_cache(kvp->kv_dtype, [&]<typename C>() -> int {
+            using T = typename A::T;
+            const bool vec = kv.stride % 8 == 0 && aligned_to(rows, sizeof(T) * 8) && aligned_to(kvp->arena, 16) &&
+                             kv.block_bytes % 16 == 0;
+            if (vec)
+                hipLaunchKernelGGL((kv_write_kernel<A, C, 8>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)rows,
+                                   kv_positions, kv, is_v, err_flag);
+            else
+                hipLaunchKernelGGL((kv_write_kernel<A, C, 1>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)rows,
+                                   kv_positions, kv, is_v, err_flag);
+            return launch_status();
+        });
+    });
+}
+
+extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q_heads, const void *k,
+                                        void *k_out, const void *v, uint32_t n_kv_heads, uint32_t act_dtype,
+                                        uint32_t batch, uint32_t head_dim, uint32_t rope_dim, uint32_t pairing,
+                                        const float *inv_freqs, const uint32_t *rope_positions,
+                                        const uint32_t *kv_positions, const FellmRocmPagedKv *kvp,
+                                        uint32_t *err_flag, void *stream) {
+    using namespace fellm;
+    if (!q || !q_out || !k || !v || !kv_positions || !kvp || (rope_dim && !inv_freqs)) return FELLM_ERR_ARITY;
+    if (n_q_heads == 0 || n_kv_heads == 0) return FELLM_ERR_SHAPE;
+    if (int rc = check_rope_shape(head_dim, rope_dim, pairing)) return rc;
+    KvDev kv;
+    if (!make_kv(kvp, kv)) return FELLM_ERR_SHAPE;
+    if (kv.stride != n_kv_heads * head_dim) return FELLM_ERR_SHAPE;
+    if (batch == 0) return FELLM_OK;
+    hipStream_t s = as_stream(stream);
+    return dispatch_act(act_dtype, [&]<typename A>() -> int {
+        return dispatch_cache(kvp->kv_dtype, [&]<typename C>() -> int {
+            using T = typename A::T;
+            const bool vec = rope_vec_ok(head_dim, rope_dim, pairing, sizeof(T), {q, q_out, k, k_out, v}) &&
+                             aligned_to(kvp->arena, 16) && kv.block_bytes % 16 == 0;
+            auto go = [&]<int PV>() {
+                hipLaunchKernelGGL((rope_kernel<A, C, PV, 1>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)q,
+                                   (T *)q_out, n_q_heads, (const T *)k, (T *)k_out, n_kv_heads, (const T *)v,
+                                   head_dim, rope_dim, pairing, inv_freqs, rope_positions, 0u, kv_positions, kv,
+                                   err_flag);
+                return launch_status();
+            };
+            return vec ? go.template operator()<4>() : go.template operator()<1>();
+        });
+    });
+}

@@ -1,0 +1,253 @@
+"""Torch-facing entry points for the gfx950 kernels.
+
+Every function takes device tensors already resident in HBM, launches one
+HIP kernel through the C ABI on torch's current stream and returns the
+outputs.  There is no CPU path: tensors must live on a ROCm device and the
+kernel library must be built (``python -m fellm_amd.build``).
+
+Reference semantics are documented on the C entry points (include/fellm_rocm.h).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .abi import DType
+
+_ACT = {torch.float32: DType.F32, torch.float16: DType.F16, torch.bfloat16: DType.BF16}
+_TORCH = {v: k for k, v in _ACT.items()}
+QTYPES = {"q4k": (DType.Q4K, 144), "q6k": (DType.Q6K, 210)}
+
+
+def _code(t: torch.Tensor) -> int:
+    try:
+        return int(_ACT[t.dtype])
+    except KeyError as e:
+        raise TypeError(f"unsupported activation dtype {t.dtype}") from e
+
+
+def _dev(*ts: torch.Tensor | None) -> None:
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError("fellm_amd ops need device tensors (no CPU fallback)")
+        if not t.is_contiguous():
+            raise ValueError("fellm_amd ops need contiguous tensors")
+
+
+def _p(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def add_rmsnorm(x, residual, weight, eps: float, *, h_out=None, y_out=None, y_dtype=None, store_h=True):
+    """h = x + residual (stored in x's dtype); y = rmsnorm(h) * weight.
+
+    ``residual=None`` gives plain RMSNorm of ``x`` (returns ``(None, y)``).
+    Rows are the last-dimension groups of ``weight.numel()`` elements.
+    """
+    _dev(x, residual, weight)
+    group = weight.numel()
+    if weight.dtype != torch.float32:
+        raise TypeError("RMSNorm weight must be float32")
+    y_dtype = y_dtype or x.dtype
+    y = y_out if y_out is not None else torch.empty(x.shape, dtype=y_dtype, device=x.device)
+    h = None
+    if residual is not None and store_h:
+        h = h_out if h_out is not None else torch.empty_like(x)
+    if residual is not None and residual.dtype != x.dtype:
+        raise TypeError("x and residual dtypes differ")
+    _dev(y, h)
+    _lib.call("fellm_rocm_add_rmsnorm", _p(x), _p(residual), _p(h), _code(x), _p(weight), group, _p(y),
+              _code(y), x.numel(), eps, _stream())
+    return h, y
+
+
+def rmsnorm(x, weight, eps: float, out=None):
+    return add_rmsnorm(x, None, weight, eps, y_out=out)[1]
+
+
+def silu_gate(gate, up, out=None, out_dtype=None):
+    """out = silu(gate) * up, elementwise."""
+    _dev(gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError("gate/up mismatch")
+    out = out if out is not None else torch.empty(gate.shape, dtype=out_dtype or gate.dtype, device=gate.device)
+    _dev(out)
+    _lib.call("fellm_rocm_silu_gate", _p(gate), _p(up), _code(gate), _p(out), _code(out), gate.numel(), _stream())
+    return out
+
+
+def add(a, b, out=None):
+    _dev(a, b)
+    out = out if out is not None else torch.empty_like(a)
+    _lib.call("fellm_rocm_add", _p(a), _p(b), _code(a), _p(out), _code(out), a.numel(), _stream())
+    return out
+
+
+def _table_code(table: torch.Tensor, qtype: str | None) -> int:
+    if qtype is None:
+        return _code(table)
+    return int(QTYPES[qtype][0])
+
+
+def embedding(table, ids, *, dim: int | None = None, qtype: str | None = None, out=None,
+              out_dtype=torch.float32, err_flag=None):
+    """Gather rows ``table[ids]``.
+
+    Dense tables are ``[vocab, dim]`` f32/f16/bf16 tensors.  Quantized tables
+    (``qtype`` "q4k" or "q6k") are uint8 ``[vocab, row_bytes]`` with ``dim``
+    elements per row.  ``ids`` is int32 (read as u32).
+    """
+    _dev(table, ids)
+    vocab = table.shape[0]
+    dim = dim if dim is not None else table.shape[1]
+    out = out if out is not None else torch.empty((ids.numel(), dim), dtype=out_dtype, device=table.device)
+    _dev(out)
+    _lib.call("fellm_rocm_embedding", _p(table), _table_code(table, qtype), vocab, dim, _p(ids), ids.numel(),
+              _p(out), _code(out), _p(err_flag), _stream())
+    return out
+
+
+def embedding_rmsnorm(table, ids, weight, eps: float, *, dim: int | None = None, qtype: str | None = None,
+                      out_dtype=torch.float16, h_out=None, y_out=None, store_h=True, err_flag=None):
+    """Gather fused with RMSNorm of each gathered row: returns (h, y)."""
+    _dev(table, ids, weight)
+    vocab = table.shape[0]
+    dim = dim if dim is not None else table.shape[1]
+    y = y_out if y_out is not None else torch.empty((ids.numel(), dim), dtype=out_dtype, device=table.device)
+    h = None
+    if store_h:
+        h = h_out if h_out is not None else torch.empty_like(y)
+    _lib.call("fellm_rocm_embedding_rmsnorm", _p(table), _table_code(table, qtype), vocab, dim, _p(ids),
+              ids.numel(), _p(weight), eps, _p(h), _p(y), _code(y), _p(err_flag), _stream())
+    return h, y
+
+
+def rope(x1, inv_freqs, *, head_dim: int, rope_dim: int | None = None, pairing: int = 0, positions=None,
+         position0: int = 0, x2=None, out1=None, out2=None, inplace: bool = False):
+    """RoPE over ``x1`` (and ``x2``, sharing positions).  Shapes ``[rows, heads*head_dim]``."""
+    _dev(x1, x2, inv_freqs, positions)
+    rope_dim = head_dim if rope_dim is None else rope_dim
+    rows = x1.shape[0]
+    nh1 = x1.numel() // (rows * head_dim)
+    out1 = x1 if inplace else (out1 if out1 is not None else torch.empty_like(x1))
+    nh2 = 0
+    if x2 is not None:
+        nh2 = x2.numel() // (rows * head_dim)
+        out2 = x2 if inplace else (out2 if out2 is not None else torch.empty_like(x2))
+    _lib.call("fellm_rocm_rope", _p(x1), _p(out1), nh1, _p(x2), _p(out2), nh2, _code(x1), rows, head_dim, rope_dim,
+              pairing, _p(inv_freqs), _p(positions), position0, _stream())
+    return (out1, out2) if x2 is not None else out1
+
+
+@dataclass
+class PagedKvCache:
+    """Device paged KV arena in FeLLM's layout (paged_ctx.rs:341-360).
+
+    ``arena`` is a uint8 device tensor of ``n_blocks * block_bytes``; each
+    block holds ``block_size`` K rows then ``block_size`` V rows of
+    ``stride`` elements (f16 as in the reference, or bf16).
+    ``block_table`` is an int32 device tensor (read as u32) of
+    ``batch * n_layers * n_logical_blocks`` physical block ids.
+    """
+
+    arena: torch.Tensor
+    block_table: torch.Tensor
+    n_layers: int
+    n_logical_blocks: int
+    block_size: int
+    block_bytes: int
+    stride: int
+    kv_dtype: torch.dtype = torch.float16
+
+    @staticmethod
+    def block_bytes_for(stride: int, block_size: int = 16) -> int:
+        """round_up(2 * block_size * stride * 2, 64) (backend-cuda/src/vram_pool.rs:31-35)."""
+        return (2 * block_size * stride * 2 + 63) // 64 * 64
+
+    def c_struct(self, layer: int) -> _lib.FellmRocmPagedKv:
+        s = _lib.FellmRocmPagedKv()
+        s.arena = self.arena.data_ptr()
+        s.arena_len = self.arena.numel()
+        s.block_table = self.block_table.data_ptr()
+        s.n_block_table = self.block_table.numel()
+        s.n_logical_blocks = self.n_logical_blocks
+        s.n_layers = self.n_layers
+        s.layer = layer
+        s.block_size = self.block_size
+        s.block_bytes = self.block_bytes
+        s.stride = self.stride
+        s.kv_dtype = int(_ACT[self.kv_dtype])
+        return s
+
+
+def kv_write(rows, kv_positions, cache: PagedKvCache, *, layer: int = 0, is_v: bool = False, err_flag=None):
+    """Write rows ``[batch, stride]`` into K (or V) slots at ``kv_positions``."""
+    _dev(rows, kv_positions)
+    kv = cache.c_struct(layer)
+    _lib.call("fellm_rocm_kv_write", _p(rows), _code(rows), rows.shape[0], _p(kv_positions), C.byref(kv),
+              int(is_v), _p(err_flag), _stream())
+
+
+def rope_kv_write(q, k, v, inv_freqs, kv_positions, cache: PagedKvCache, *, head_dim: int,
+                  rope_dim: int | None = None, pairing: int = 0, rope_positions=None, layer: int = 0,
+                  q_out=None, k_out=None, inplace_q: bool = False, err_flag=None):
+    """Fused RoPE(q), RoPE(k) and paged append of rotated K and V."""
+    _dev(q, k, v, inv_freqs, kv_positions, rope_positions)
+    rope_dim = head_dim if rope_dim is None else rope_dim
+    batch = q.shape[0]
+    nq = q.numel() // (batch * head_dim)
+    nkv = k.numel() // (batch * head_dim)
+    q_out = q if inplace_q else (q_out if q_out is not None else torch.empty_like(q))
+    kv = cache.c_struct(layer)
+    _lib.call("fellm_rocm_rope_kv_write", _p(q), _p(q_out), nq, _p(k), _p(k_out), _p(v), nkv, _code(q), batch,
+              head_dim, rope_dim, pairing, _p(inv_freqs), _p(rope_positions), _p(kv_positions), C.byref(kv),
+              _p(err_flag), _stream())
+    return q_out
+
+
+def router_topk(logits, k: int, *, gating_func: int = 1, norm_topk_prob: bool = True,
+                routed_scaling_factor: float = 0.0, ids=None, weights=None):
+    """Softmax/sigmoid gate + top-k + renorm: returns (ids int32 [T, k], weights f32 [T, k])."""
+    _dev(logits)
+    if logits.dtype != torch.float32:
+        raise TypeError("router logits must be float32")
+    tokens, n_exp = logits.shape
+    kk = min(k, n_exp)
+    ids = ids if ids is not None else torch.empty((tokens, kk), dtype=torch.int32, device=logits.device)
+    weights = weights if weights is not None else torch.empty((tokens, kk), dtype=torch.float32, device=logits.device)
+    _lib.call("fellm_rocm_router_topk", _p(logits), tokens, n_exp, k, gating_func, int(norm_topk_prob),
+              routed_scaling_factor, _p(ids), _p(weights), _stream())
+    return ids, weights
+
+
+def expf(x):
+    """Device glibc-exact expf (self-check of the restatement)."""
+    _dev(x)
+    out = torch.empty_like(x)
+    _lib.call("fellm_rocm_expf", _p(x), _p(out), x.numel(), _stream())
+    return out
+
+
+def rope_inv_freqs(theta: float, rope_dim: int) -> torch.Tensor:
+    """inv_freq[i] = theta ** (-(2i) / rope_dim) in f32 with libm powf
+    (crates/fellm-model/src/rope.rs:13-40, no scaling), as a CPU tensor."""
+    import ctypes.util
+
+    libm = C.CDLL(ctypes.util.find_library("m") or "libm.so.6")
+    libm.powf.restype = C.c_float
+    libm.powf.argtypes = [C.c_float, C.c_float]
+    out = []
+    for i in range(rope_dim // 2):
+        e = C.c_float(-float(2 * i)).value / C.c_float(float(rope_dim)).value
+        e = C.c_float(e).value
+        out.append(libm.powf(theta, e))
+    return torch.tensor(out, dtype=torch.float32)

@@ -1,0 +1,164 @@
+/*
+ * fellm_rocm.h — device-pointer entry points of libfellm_rocm_kernels.so.
+ *
+ * These are the kernels behind the plugin launchers declared in fellm_abi.h.
+ * They take DEVICE pointers that are already resident in HBM and a hipStream_t
+ * (passed as void*; NULL = the null stream), enqueue work and return without
+ * synchronising.  All return 0 or a negative FELLM_ERR_* code from fellm_abi.h;
+ * argument validation happens on the host before anything is enqueued.
+ *
+ * Activation dtypes are FELLM_DTYPE_F32, FELLM_DTYPE_F16 or FELLM_DTYPE_BF16.
+ * All arithmetic is f32 (the reference's op boundary is f32 everywhere:
+ * crates/backend-cpu/src/backend.rs:798-816); 16-bit outputs are the f32
+ * result rounded once, to nearest-even.
+ *
+ * Where a reference interface is replaced, the comment names it (file:line,
+ * paths relative to the FeLLM repository root).
+ */
+#ifndef FELLM_ROCM_H
+#define FELLM_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version string, e.g. "fellm-rocm 0.1.0 gfx950". */
+const char *fellm_rocm_version(void);
+
+/*
+ * Residual add + RMSNorm over rows of `group` elements.
+ *   replaces: Add (backend-cpu/src/backend.rs:1543-1553, kernels/simd_f32.rs:175-197)
+ *             followed by RmsNorm (backend.rs:1104-1133, kernels/norm.rs:6-53).
+ * x, residual, h_out: act_dtype, n_elems elements (n_elems % group == 0).
+ * residual == NULL: plain RMSNorm of x (h_out must then be NULL).
+ * h = x + residual is stored (rounded to act_dtype) in h_out when non-NULL and
+ * the norm is taken of h as stored.  y = (h * scale) * w with
+ * scale = 1 / sqrt(sum(h^2) / group + eps); y has y_dtype.
+ * weight: f32 [group].
+ */
+int fellm_rocm_add_rmsnorm(const void *x, const void *residual, void *h_out, uint32_t act_dtype,
+                           const float *weight, uint32_t group, void *y, uint32_t y_dtype,
+                           uint64_t n_elems, float eps, void *stream);
+
+/*
+ * out = silu(gate) * up, silu(g) = g / (1 + exp(-g)).
+ *   replaces: SiluGate (backend.rs:1174-1184, kernels/swiglu.rs:5-16).
+ * exp is a bit-exact restatement of glibc's expf, so f32 output is bit-exact
+ * with the CPU reference.
+ */
+int fellm_rocm_silu_gate(const void *gate, const void *up, uint32_t in_dtype, void *out,
+                         uint32_t out_dtype, uint64_t n_elems, void *stream);
+
+/* out = a + b elementwise (Add: backend.rs:1543-1553). */
+int fellm_rocm_add(const void *a, const void *b, uint32_t in_dtype, void *out, uint32_t out_dtype,
+                   uint64_t n_elems, void *stream);
+
+/*
+ * Embedding gather: out[t, :] = dequant(table[ids[t], :]).
+ *   replaces: Embedding (backend.rs:1026-1046, kernels/embedding.rs:10-23,
+ *             dequant.rs:19-55 F32/F16/BF16, :251-305 Q4_K, :315-370 Q6_K).
+ * table_dtype: F32, F16, BF16, Q4K or Q6K (Q4K/Q6K need dim % 256 == 0).
+ * out_dtype:   F32, F16 or BF16.
+ * An id >= vocab yields a zero row and sets *err_flag (device u32, may be NULL)
+ * to 1; the CPU reference rejects such ids.
+ * When norm_weight != NULL the gather is fused with RMSNorm over the row:
+ * h_out (may be NULL) gets the gathered row and y the normalised row, with the
+ * norm taken of the f32 dequantised values (out is then ignored and may be NULL).
+ */
+int fellm_rocm_embedding(const void *table, uint32_t table_dtype, uint64_t vocab, uint32_t dim,
+                         const uint32_t *ids, uint32_t n_ids, void *out, uint32_t out_dtype,
+                         uint32_t *err_flag, void *stream);
+int fellm_rocm_embedding_rmsnorm(const void *table, uint32_t table_dtype, uint64_t vocab,
+                                 uint32_t dim, const uint32_t *ids, uint32_t n_ids,
+                                 const float *norm_weight, float eps, void *h_out, void *y,
+                                 uint32_t out_dtype, uint32_t *err_flag, void *stream);
+
+/*
+ * RoPE over one or two row-major tensors sharing positions (q and k).
+ *   replaces: Rope (backend.rs:1135-1172, kernels/rope.rs:28-62).
+ * x1: [rows, n_heads1 * head_dim], x2: [rows, n_heads2 * head_dim] or NULL.
+ * out1/out2 may alias x1/x2 (in place).  Pairing: 0 adjacent (2i, 2i+1),
+ * 1 split-half (i, i + rope_dim/2), 2 adjacent over the last rope_dim dims.
+ * theta = float(pos) * inv_freqs[i]; (s, c) = (sin, cos)(theta);
+ * a' = a*c - b*s, b' = a*s + b*c.  pos = positions[row] when positions != NULL,
+ * else position0 + row.  Dims outside the rotated span are copied.
+ */
+int fellm_rocm_rope(const void *x1, void *out1, uint32_t n_heads1, const void *x2, void *out2,
+                    uint32_t n_heads2, uint32_t act_dtype, uint32_t rows, uint32_t head_dim,
+                    uint32_t rope_dim, uint32_t pairing, const float *inv_freqs,
+                    const uint32_t *positions, uint32_t position0, void *stream);
+
+/*
+ * Paged KV geometry, as FeLLM lays it out
+ * (crates/fellm-plugin-abi/src/paged_ctx.rs:341-360, backend-cuda/src/vram_pool.rs:31-35):
+ * block p occupies arena[p * block_bytes ...]: block_size K rows then
+ * block_size V rows, each row `stride` elements of kv_dtype (F16 or BF16).
+ * Row r's entry for token position t in layer L is
+ *   block_table[(r * n_layers + L) * n_logical_blocks + t / block_size].
+ */
+typedef struct FellmRocmPagedKv {
+    void *arena;               /* device */
+    uint64_t arena_len;        /* bytes */
+    const uint32_t *block_table; /* device */
+    uint64_t n_block_table;
+    uint32_t n_logical_blocks;
+    uint32_t n_layers;
+    uint32_t layer;
+    uint32_t block_size;
+    uint64_t block_bytes;
+    uint32_t stride;           /* elements per K or V row (n_kv_heads * head_dim) */
+    uint32_t kv_dtype;         /* FELLM_DTYPE_F16 (reference) or FELLM_DTYPE_BF16 */
+} FellmRocmPagedKv;
+
+/*
+ * KvWrite: write rows[b, :] into the K (is_v = 0) or V (is_v = 1) slot of
+ * batch row b at kv_positions[b].   replaces: backend.rs:1734-1775.
+ * Slots outside the arena or table set *err_flag (device, may be NULL) and are skipped.
+ */
+int fellm_rocm_kv_write(const void *rows, uint32_t act_dtype, uint32_t batch,
+                        const uint32_t *kv_positions, const FellmRocmPagedKv *kv, uint32_t is_v,
+                        uint32_t *err_flag, void *stream);
+
+/*
+ * Fused RoPE(q), RoPE(k) + paged K/V append, one launch.
+ *   replaces: the graph sequence q_rope -> k_rope -> k_write -> v_write
+ *   (crates/fellm-model/src/graph.rs:2136-2215).
+ * q_out gets rotated q; k_out (may be NULL) rotated k; rotated k and raw v are
+ * rounded once to kv->kv_dtype and stored at kv_positions[b].  RoPE uses
+ * rope_positions[b] (NULL: kv_positions).
+ */
+int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q_heads, const void *k,
+                             void *k_out, const void *v, uint32_t n_kv_heads, uint32_t act_dtype,
+                             uint32_t batch, uint32_t head_dim, uint32_t rope_dim,
+                             uint32_t pairing, const float *inv_freqs,
+                             const uint32_t *rope_positions, const uint32_t *kv_positions,
+                             const FellmRocmPagedKv *kv, uint32_t *err_flag, void *stream);
+
+/*
+ * MoE router: softmax (gating_func != 2) or sigmoid (gating_func == 2) over
+ * each token's n_experts logits, top-k by score (ties -> lower expert id),
+ * optional renormalisation over the k selected, times routed_scaling_factor
+ * (0 -> 1).   replaces: kernels/moe.rs:79-186 and :820-855.
+ * logits f32 [tokens, n_experts] (n_experts <= 512), ids u32 [tokens, k],
+ * weights f32 [tokens, k], k = min(n_expert_used, n_experts).
+ * Scores use a bit-exact restatement of glibc expf and the CPU summation
+ * order, so ids and weights are bit-exact with the CPU reference.
+ */
+int fellm_rocm_router_topk(const float *logits, uint32_t tokens, uint32_t n_experts,
+                           uint32_t n_expert_used, uint32_t gating_func, uint32_t norm_topk_prob,
+                           float routed_scaling_factor, uint32_t *ids, float *weights,
+                           void *stream);
+
+/*
+ * Self-check of the device expf restatement: out[i] = expf(in[i]) on the GPU.
+ * Diagnostic only (no counterpart in the reference).
+ */
+int fellm_rocm_expf(const float *in, float *out, uint64_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FELLM_ROCM_H */

@@ -1,0 +1,235 @@
+"""CPU oracle for parity tests: numpy wrapper over liboracle.so (fellm_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg as the checker; the product library never uses
+it.  Build with ``make -C oracle``.
+
+Also composes the 16-bit activation variants the way the reference's f32 op
+boundary implies: widen inputs exactly, run the f32 reference op, round the
+f32 result once (f16: IEEE RNE as half::f16::from_f32; bf16: RNE).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        l = C.CDLL(str(LIB_PATH))
+        P, S, U32, F = C.c_void_p, C.c_size_t, C.c_uint32, C.c_float
+        sigs = {
+            "oracle_f16_to_f32": (None, [P, P, S]),
+            "oracle_f32_to_f16": (None, [P, P, S]),
+            "oracle_bf16_to_f32": (None, [P, P, S]),
+            "oracle_f32_to_bf16": (None, [P, P, S, C.c_int]),
+            "oracle_expf": (None, [P, P, S]),
+            "oracle_get_scale_min_k4": (None, [S, P, P, P]),
+            "oracle_row_bytes": (S, [U32, S]),
+            "oracle_dequantize_row": (C.c_int, [U32, P, P, S]),
+            "oracle_embedding": (C.c_int, [P, U32, S, S, P, S, P]),
+            "oracle_add": (None, [P, P, P, S]),
+            "oracle_rmsnorm": (C.c_int, [P, P, S, S, F, P]),
+            "oracle_silu_gate": (None, [P, P, P, S]),
+            "oracle_rope_inv_freqs": (None, [F, U32, P]),
+            "oracle_rope": (C.c_int, [P, P, S, S, S, S, U32, P, P, S, U32]),
+            "oracle_kv_write_paged": (C.c_int, [P, S, S, P, P, S, S, S, S, S, S, P, S, C.c_int, C.c_int]),
+            "oracle_router": (C.c_int, [P, S, S, S, U32, U32, F, P, P]),
+        }
+        for name, (res, args) in sigs.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _c(a: np.ndarray, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ---- dtype edges -------------------------------------------------------------
+def f16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    b = _c(bits, np.uint16)
+    out = np.empty(b.shape, np.float32)
+    lib().oracle_f16_to_f32(_p(b), _p(out), b.size)
+    return out
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    a = _c(x, np.float32)
+    out = np.empty(a.shape, np.uint16)
+    lib().oracle_f32_to_f16(_p(a), _p(out), a.size)
+    return out
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    b = _c(bits, np.uint16)
+    out = np.empty(b.shape, np.float32)
+    lib().oracle_bf16_to_f32(_p(b), _p(out), b.size)
+    return out
+
+
+def f32_to_bf16_bits(x: np.ndarray, truncate: bool = False) -> np.ndarray:
+    a = _c(x, np.float32)
+    out = np.empty(a.shape, np.uint16)
+    lib().oracle_f32_to_bf16(_p(a), _p(out), a.size, int(truncate))
+    return out
+
+
+def widen(bits_or_f32: np.ndarray, kind: str) -> np.ndarray:
+    """Exact f32 value of stored activations ('f32', 'f16' bits or 'bf16' bits)."""
+    if kind == "f32":
+        return _c(bits_or_f32, np.float32)
+    if kind == "f16":
+        return f16_bits_to_f32(bits_or_f32)
+    if kind == "bf16":
+        return bf16_bits_to_f32(bits_or_f32)
+    raise ValueError(kind)
+
+
+def narrow(x: np.ndarray, kind: str) -> np.ndarray:
+    """Store an f32 result as 'f32', or as f16/bf16 bits rounded once (RNE)."""
+    if kind == "f32":
+        return _c(x, np.float32)
+    if kind == "f16":
+        return f32_to_f16_bits(x)
+    if kind == "bf16":
+        return f32_to_bf16_bits(x)
+    raise ValueError(kind)
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    a = _c(x, np.float32)
+    out = np.empty_like(a)
+    lib().oracle_expf(_p(a), _p(out), a.size)
+    return out
+
+
+# ---- ops ---------------------------------------------------------------------
+def get_scale_min_k4(j: int, scales: bytes) -> tuple[int, int]:
+    q = _c(np.frombuffer(scales, np.uint8), np.uint8)
+    d, m = C.c_uint8(), C.c_uint8()
+    lib().oracle_get_scale_min_k4(j, _p(q), C.addressof(d), C.addressof(m))
+    return d.value, m.value
+
+
+def row_bytes(dtype: int, dim: int) -> int:
+    return lib().oracle_row_bytes(dtype, dim)
+
+
+def dequantize_row(dtype: int, src: np.ndarray, n: int) -> np.ndarray:
+    s = _c(src, np.uint8)
+    out = np.empty(n, np.float32)
+    rc = lib().oracle_dequantize_row(dtype, _p(s), _p(out), n)
+    if rc:
+        raise ValueError(f"dequantize_row rc={rc}")
+    return out
+
+
+def embedding(table: np.ndarray, dtype: int, vocab: int, dim: int, ids: np.ndarray) -> np.ndarray:
+    t = _c(table, np.uint8).reshape(-1)
+    i = _c(ids, np.uint32)
+    out = np.empty((i.size, dim), np.float32)
+    rc = lib().oracle_embedding(_p(t), dtype, vocab, dim, _p(i), i.size, _p(out))
+    if rc:
+        raise ValueError(f"embedding rc={rc}")
+    return out
+
+
+def add(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    out = np.empty_like(a)
+    lib().oracle_add(_p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    out = np.empty_like(x)
+    rc = lib().oracle_rmsnorm(_p(x), _p(w), w.size, x.size, eps, _p(out))
+    if rc:
+        raise ValueError(f"rmsnorm rc={rc}")
+    return out
+
+
+def add_rmsnorm(x, r, w, eps, kind: str = "f32"):
+    """Fused residual add + RMSNorm on stored activations of `kind`.
+
+    h = narrow(widen(x) + widen(r)); y = narrow(rmsnorm(widen(h))).
+    Returns (h, y) in storage form (f32 values or 16-bit bits).
+    """
+    h = narrow(add(widen(x, kind), widen(r, kind)), kind)
+    y = narrow(rmsnorm(widen(h, kind), w, eps), kind)
+    return h, y
+
+
+def silu_gate(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    g, u = _c(g, np.float32), _c(u, np.float32)
+    out = np.empty_like(g)
+    lib().oracle_silu_gate(_p(g), _p(u), _p(out), g.size)
+    return out
+
+
+def rope_inv_freqs(theta: float, rope_dim: int) -> np.ndarray:
+    out = np.empty(rope_dim // 2, np.float32)
+    lib().oracle_rope_inv_freqs(theta, rope_dim, _p(out))
+    return out
+
+
+def rope(x: np.ndarray, n_heads: int, head_dim: int, rope_dim: int, pairing: int, inv_freqs: np.ndarray,
+         positions: np.ndarray | None = None, position0: int = 0) -> np.ndarray:
+    x = _c(x, np.float32)
+    f = _c(inv_freqs, np.float32)
+    out = np.empty_like(x)
+    pos = _c(positions, np.uint32) if positions is not None else None
+    lib().oracle_rope(_p(x), _p(out), x.size, n_heads, head_dim, rope_dim, pairing, _p(f),
+                      _p(pos) if pos is not None else None, pos.size if pos is not None else 0, position0)
+    return out
+
+
+def kv_write_paged(rows: np.ndarray, stride: int, row_positions: np.ndarray, table: np.ndarray, n_logical: int,
+                   n_layers: int, layer: int, block_size: int, block_bytes: int, arena: np.ndarray, is_v: bool,
+                   elem: str = "f16") -> None:
+    """In-place write into `arena` (uint8) as backend.rs:1734-1775."""
+    rows = _c(rows, np.float32)
+    pos = _c(row_positions, np.uint32)
+    tab = _c(table, np.uint32)
+    assert arena.dtype == np.uint8 and arena.flags.c_contiguous
+    rc = lib().oracle_kv_write_paged(_p(rows), pos.size, stride, _p(pos), _p(tab), tab.size, n_logical, n_layers,
+                                     layer, block_size, block_bytes, _p(arena), arena.size, int(is_v),
+                                     1 if elem == "bf16" else 0)
+    if rc:
+        raise ValueError(f"kv_write rc={rc}")
+
+
+def router(logits: np.ndarray, k: int, gating: int = 1, norm: bool = True, rsf: float = 0.0):
+    l = _c(logits, np.float32)
+    t, e = l.shape
+    kk = min(k, e)
+    ids = np.empty((t, kk), np.uint32)
+    w = np.empty((t, kk), np.float32)
+    rc = lib().oracle_router(_p(l), t, e, k, gating, int(norm), rsf, _p(ids), _p(w))
+    if rc:
+        raise ValueError(f"router rc={rc}")
+    return ids, w

@@ -1,0 +1,357 @@
+"""GPU parity: every kernel through the device-pointer C ABI against the CPU oracle.
+
+Seeded inputs at sizes the oracle finishes in well under a second; the
+tolerances are stated in parity_util.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from parity_util import (KINDS, assert_close, assert_exact, assert_rope_close, from_dev, pair_magnitude,
+                         random_stored, to_dev)
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from fellm_amd import ops as _ops
+
+    return _ops
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+# ---- expf --------------------------------------------------------------------
+def test_device_expf_matches_glibc(ops, dev):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, size=1 << 22, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    special = np.array([0.0, -0.0, 1.0, -1.0, 88.0, 88.7, float.fromhex('0x1.62e42ep6'), 89.0, -103.0, -103.97, -104.0,
+                        float.fromhex('-0x1.9fe368p6'),
+                        np.inf, -np.inf, np.nan, 1e-45, -1e-45], np.float32)
+    dense = np.linspace(-110.0, 90.0, 1 << 20, dtype=np.float32)
+    x = np.concatenate([x, special, dense])
+    got = from_dev(ops.expf(torch.from_numpy(x).to(dev)))
+    ref = oracle.expf(x)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_exact(got[~nan], ref[~nan], "expf")
+
+
+# ---- SwiGLU --------------------------------------------------------------------
+@pytest.mark.parametrize("kind", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("n", [1, 7, 8, 4096 * 3 + 5, 64 * 8192])
+def test_silu_gate(ops, dev, kind, n):
+    rng = np.random.default_rng(n)
+    g = random_stored(rng, n, kind)
+    u = random_stored(rng, n, kind)
+    ref = oracle.narrow(oracle.silu_gate(oracle.widen(g, kind), oracle.widen(u, kind)), kind)
+    got = from_dev(ops.silu_gate(to_dev(g, kind, dev), to_dev(u, kind, dev)))
+    assert_exact(got, ref, f"silu_gate {kind} n={n}")
+
+
+def test_silu_gate_unaligned_and_extremes(ops, dev):
+    g = np.array([0.0, -0.0, 100.0, -100.0, 20.0, -20.0, 88.0, -88.0, 1e-30, np.inf, -np.inf, 3.5], np.float32)
+    u = np.full_like(g, 1.5)
+    ref = oracle.silu_gate(g, u)
+    gd = torch.from_numpy(np.concatenate([[0.0], g]).astype(np.float32)).to(dev)[1:]
+    ud = torch.from_numpy(np.concatenate([[0.0], u]).astype(np.float32)).to(dev)[1:]
+    got = from_dev(ops.silu_gate(gd, ud))
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_exact(got[~nan], ref[~nan], "silu extremes")
+    assert got[0] == 0.0
+
+
+# ---- Add + RMSNorm -------------------------------------------------------------
+@pytest.mark.parametrize("kind", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("rows,group", [(1, 2048), (3, 4096), (64, 2048), (1500, 4096), (7, 8192), (5, 3584),
+                                        (9, 100), (2, 65536), (33, 16)])
+def test_add_rmsnorm(ops, dev, kind, rows, group):
+    rng = np.random.default_rng(rows * 7919 + group)
+    x = random_stored(rng, (rows, group), kind)
+    r = random_stored(rng, (rows, group), kind, sigma=2.0)
+    w = rng.normal(1.0, 0.1, size=group).astype(np.float32)
+    eps = 1e-5
+    h_ref, y_ref = oracle.add_rmsnorm(x, r, w, eps, kind)
+    h, y = ops.add_rmsnorm(to_dev(x, kind, dev), to_dev(r, kind, dev), torch.from_numpy(w).to(dev), eps)
+    assert_exact(from_dev(h), h_ref, f"h {kind}")
+    assert_close(from_dev(y), y_ref, kind, what=f"y {kind} {rows}x{group}")
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16"])
+def test_rmsnorm_plain_and_no_h(ops, dev, kind):
+    rng = np.random.default_rng(5)
+    x = random_stored(rng, (256, 8192), kind)
+    w = rng.normal(1.0, 0.1, size=8192).astype(np.float32)
+    y_ref = oracle.narrow(oracle.rmsnorm(oracle.widen(x, kind), w, 1e-6), kind)
+    y = ops.rmsnorm(to_dev(x, kind, dev), torch.from_numpy(w).to(dev), 1e-6)
+    assert_close(from_dev(y), y_ref, kind, what="plain rmsnorm")
+    r = random_stored(rng, (256, 8192), kind)
+    _, y_ref2 = oracle.add_rmsnorm(x, r, w, 1e-6, kind)
+    h, y2 = ops.add_rmsnorm(to_dev(x, kind, dev), to_dev(r, kind, dev), torch.from_numpy(w).to(dev), 1e-6,
+                            store_h=False)
+    assert h is None
+    assert_close(from_dev(y2), y_ref2, kind, what="no-h rmsnorm")
+
+
+def test_add_rmsnorm_inplace_residual(ops, dev):
+    rng = np.random.default_rng(11)
+    kind = "f16"
+    for group in (4096, 100, 65536):
+        x = random_stored(rng, (4, group), kind)
+        r = random_stored(rng, (4, group), kind)
+        w = rng.normal(1.0, 0.1, size=group).astype(np.float32)
+        h_ref, y_ref = oracle.add_rmsnorm(x, r, w, 1e-5, kind)
+        xd = to_dev(x, kind, dev)
+        h, y = ops.add_rmsnorm(xd, to_dev(r, kind, dev), torch.from_numpy(w).to(dev), 1e-5, h_out=xd)
+        assert_exact(from_dev(xd), h_ref, "in-place h")
+        assert_close(from_dev(y), y_ref, kind, what="in-place y")
+
+
+# ---- Embedding -----------------------------------------------------------------
+def _dense_table(rng, vocab, dim, kind):
+    return random_stored(rng, (vocab, dim), kind, sigma=0.02)
+
+
+@pytest.mark.parametrize("table_kind", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("out_kind", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("dim", [2048, 100])
+def test_embedding_dense(ops, dev, table_kind, out_kind, dim):
+    rng = np.random.default_rng(dim)
+    vocab = 1000
+    t = _dense_table(rng, vocab, dim, table_kind)
+    ids = rng.integers(0, vocab, size=77, dtype=np.uint32)
+    code = {"f32": 0, "f16": 1, "bf16": 30}[table_kind]
+    ref = oracle.narrow(oracle.embedding(t.view(np.uint8), code, vocab, dim, ids), out_kind)
+    got = ops.embedding(to_dev(t, table_kind, dev), torch.from_numpy(ids.view(np.int32)).to(dev),
+                        out_dtype=KINDS[out_kind])
+    assert_exact(from_dev(got), ref, f"embedding {table_kind}->{out_kind}")
+
+
+@pytest.mark.parametrize("qtype", ["q4k", "q6k"])
+@pytest.mark.parametrize("out_kind", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("dim", [256, 3584, 4096, 1280])
+def test_embedding_quant(ops, dev, qtype, out_kind, dim):
+    from fellm_amd import synth
+
+    rng = np.random.default_rng(dim + len(qtype))
+    vocab = 300
+    table = synth.q4k_table(rng, vocab, dim) if qtype == "q4k" else synth.q6k_table(rng, vocab, dim)
+    ids = synth.zipf_ids(rng, 200, vocab)
+    code = 12 if qtype == "q4k" else 14
+    ref = oracle.narrow(oracle.embedding(table, code, vocab, dim, ids), out_kind)
+    got = ops.embedding(torch.from_numpy(table).to(dev), torch.from_numpy(ids.view(np.int32)).to(dev), dim=dim,
+                        qtype=qtype, out_dtype=KINDS[out_kind])
+    assert_exact(from_dev(got), ref, f"embedding {qtype} dim={dim} -> {out_kind}")
+
+
+@pytest.mark.parametrize("src", ["q4k", "q6k", "f16", "f32"])
+def test_embedding_rmsnorm_fused(ops, dev, src):
+    from fellm_amd import synth
+
+    rng = np.random.default_rng(3)
+    vocab, dim = 500, 3584
+    out_kind = "f32" if src == "f32" else "f16"
+    if src == "q4k":
+        table, code = synth.q4k_table(rng, vocab, dim), 12
+        td = torch.from_numpy(table).to(dev)
+    elif src == "q6k":
+        table, code = synth.q6k_table(rng, vocab, dim), 14
+        td = torch.from_numpy(table).to(dev)
+    else:
+        st = _dense_table(rng, vocab, dim, src)
+        table, code = st.view(np.uint8), {"f16": 1, "f32": 0}[src]
+        td = to_dev(st, src, dev)
+    ids = synth.zipf_ids(rng, 300, vocab)
+    w = rng.normal(1.0, 0.1, size=dim).astype(np.float32)
+    e = oracle.embedding(table, code, vocab, dim, ids)
+    h_ref = oracle.narrow(e, out_kind)
+    y_ref = oracle.narrow(oracle.rmsnorm(e, w, 1e-6), out_kind)
+    h, y = ops.embedding_rmsnorm(td, torch.from_numpy(ids.view(np.int32)).to(dev), torch.from_numpy(w).to(dev),
+                                 1e-6, dim=dim, qtype=src if src.startswith("q") else None,
+                                 out_dtype=KINDS[out_kind])
+    assert_exact(from_dev(h), h_ref, "fused h")
+    assert_close(from_dev(y), y_ref, out_kind, what="fused y")
+
+
+def test_embedding_bad_id_sets_flag(ops, dev):
+    rng = np.random.default_rng(0)
+    t = _dense_table(rng, 10, 64, "f32")
+    ids = np.array([1, 10, 3], np.uint32)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    got = from_dev(ops.embedding(to_dev(t, "f32", dev), torch.from_numpy(ids.view(np.int32)).to(dev),
+                                 err_flag=flag))
+    assert int(flag.item()) == 1
+    assert_exact(got[0], t[1], "row 0")
+    assert np.all(got[1] == 0)
+    assert_exact(got[2], t[3], "row 2")
+
+
+# ---- RoPE ----------------------------------------------------------------------
+@pytest.mark.parametrize("kind", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("pairing", [0, 1, 2])
+@pytest.mark.parametrize("head_dim,rope_dim", [(128, 128), (64, 64), (128, 64), (6, 4)])
+def test_rope_qk(ops, dev, kind, pairing, head_dim, rope_dim):
+    rng = np.random.default_rng(head_dim * 10 + rope_dim + pairing)
+    rows, nq, nk = 37, 8, 2
+    theta = 500000.0
+    inv = oracle.rope_inv_freqs(theta, rope_dim)
+    q = random_stored(rng, (rows, nq * head_dim), kind)
+    k = random_stored(rng, (rows, nk * head_dim), kind)
+    pos = rng.integers(0, 32768, size=rows, dtype=np.uint32)
+    qr = oracle.narrow(oracle.rope(oracle.widen(q, kind), nq, head_dim, rope_dim, pairing, inv, pos), kind)
+    kr = oracle.narrow(oracle.rope(oracle.widen(k, kind), nk, head_dim, rope_dim, pairing, inv, pos), kind)
+    qo, ko = ops.rope(to_dev(q, kind, dev), torch.from_numpy(inv).to(dev), head_dim=head_dim, rope_dim=rope_dim,
+                      pairing=pairing, positions=torch.from_numpy(pos.view(np.int32)).to(dev),
+                      x2=to_dev(k, kind, dev))
+    assert_rope_close(from_dev(qo), qr, pair_magnitude(oracle.widen(q, kind), nq, head_dim, rope_dim, pairing),
+                      kind, "q")
+    assert_rope_close(from_dev(ko), kr, pair_magnitude(oracle.widen(k, kind), nk, head_dim, rope_dim, pairing),
+                      kind, "k")
+    # passthrough dims are copied exactly
+    if rope_dim < head_dim:
+        qv, rv = from_dev(qo).reshape(rows, nq, head_dim), q.reshape(rows, nq, head_dim)
+        sl = slice(0, head_dim - rope_dim) if pairing == 2 else slice(rope_dim, head_dim)
+        assert_exact(qv[..., sl], rv[..., sl], "passthrough")
+
+
+def test_rope_position0_inplace(ops, dev):
+    rng = np.random.default_rng(9)
+    rows, nh, hd = 64, 32, 64
+    inv = oracle.rope_inv_freqs(500000.0, hd)
+    x = rng.normal(size=(rows, nh * hd)).astype(np.float32)
+    ref = oracle.rope(x, nh, hd, hd, 0, inv, None, position0=100)
+    xd = torch.from_numpy(x).to(dev)
+    ops.rope(xd, torch.from_numpy(inv).to(dev), head_dim=hd, position0=100, inplace=True)
+    assert_rope_close(from_dev(xd), ref, pair_magnitude(x, nh, hd, hd, 0), "f32", "in-place pos0")
+    # position 0 is the identity (rope.rs:69-77)
+    x0 = rng.normal(size=(1, nh * hd)).astype(np.float32)
+    got = from_dev(ops.rope(torch.from_numpy(x0).to(dev), torch.from_numpy(inv).to(dev), head_dim=hd))
+    assert_exact(got, x0, "pos 0 identity")
+
+
+# ---- Paged KV ------------------------------------------------------------------
+def _cache(dev, n_blocks, block_size, stride, kv_kind):
+    from fellm_amd.ops import PagedKvCache
+
+    bb = PagedKvCache.block_bytes_for(stride, block_size)
+    arena = torch.zeros(n_blocks * bb, dtype=torch.uint8, device=dev)
+    return bb, arena
+
+
+@pytest.mark.parametrize("kv_kind", ["f16", "bf16"])
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_kv_write_paged(ops, dev, kv_kind, act):
+    from fellm_amd import synth
+    from fellm_amd.ops import PagedKvCache
+
+    rng = np.random.default_rng(21)
+    batch, nkv, hd, bs, n_blocks, n_layers = 19, 2, 64, 16, 64, 2
+    stride = nkv * hd
+    pos, table, n_logical = synth.paged_layout(rng, batch, n_blocks, bs, 512, n_layers)
+    bb, arena = _cache(dev, n_blocks, bs, stride, kv_kind)
+    rows = random_stored(rng, (batch, stride), act)
+    cache = PagedKvCache(arena, torch.from_numpy(table.view(np.int32)).to(dev), n_layers, n_logical, bs, bb, stride,
+                         KINDS[kv_kind])
+    ref = np.zeros(arena.numel(), np.uint8)
+    for is_v in (False, True):
+        ops.kv_write(to_dev(rows, act, dev), torch.from_numpy(pos.view(np.int32)).to(dev), cache, layer=1,
+                     is_v=is_v)
+        oracle.kv_write_paged(oracle.widen(rows, act), stride, pos, table, n_logical, n_layers, 1, bs, bb, ref,
+                              is_v, kv_kind)
+    sync()
+    assert_exact(arena.cpu().numpy(), ref, "arena")
+
+
+@pytest.mark.parametrize("kind,kv_kind", [("bf16", "bf16"), ("f32", "f16"), ("f16", "f16")])
+@pytest.mark.parametrize("pairing", [0, 1])
+def test_rope_kv_write_fused(ops, dev, kind, kv_kind, pairing):
+    from fellm_amd import synth
+    from fellm_amd.ops import PagedKvCache
+
+    rng = np.random.default_rng(31 + pairing)
+    batch, nq, nkv, hd, bs, n_blocks = 33, 16, 2, 128, 16, 128
+    stride = nkv * hd
+    kv_pos, table, n_logical = synth.paged_layout(rng, batch, n_blocks, bs, 2048)
+    rope_pos = kv_pos + 7
+    inv = oracle.rope_inv_freqs(500000.0, hd)
+    q = random_stored(rng, (batch, nq * hd), kind)
+    k = random_stored(rng, (batch, stride), kind)
+    v = random_stored(rng, (batch, stride), kind)
+    bb, arena = _cache(dev, n_blocks, bs, stride, kv_kind)
+    cache = PagedKvCache(arena, torch.from_numpy(table.view(np.int32)).to(dev), 1, n_logical, bs, bb, stride,
+                         KINDS[kv_kind])
+    k_out = to_dev(np.zeros_like(k), kind, dev)
+    qo = ops.rope_kv_write(to_dev(q, kind, dev), to_dev(k, kind, dev), to_dev(v, kind, dev),
+                           torch.from_numpy(inv).to(dev), torch.from_numpy(kv_pos.view(np.int32)).to(dev), cache,
+                           head_dim=hd, pairing=pairing,
+                           rope_positions=torch.from_numpy(rope_pos.view(np.int32)).to(dev), k_out=k_out)
+    sync()
+    qf, kf = oracle.widen(q, kind), oracle.widen(k, kind)
+    q_ref = oracle.rope(qf, nq, hd, hd, pairing, inv, rope_pos)
+    k_ref = oracle.rope(kf, nkv, hd, hd, pairing, inv, rope_pos)
+    assert_rope_close(from_dev(qo), oracle.narrow(q_ref, kind), pair_magnitude(qf, nq, hd, hd, pairing), kind, "q")
+    assert_rope_close(from_dev(k_out), oracle.narrow(k_ref, kind), pair_magnitude(kf, nkv, hd, hd, pairing), kind,
+                      "k_out")
+    # V slots: bit-exact.  K slots: the rotated K rounded once to the cache dtype.
+    ref = np.zeros(arena.numel(), np.uint8)
+    oracle.kv_write_paged(k_ref, stride, kv_pos, table, n_logical, 1, 0, bs, bb, ref, False, kv_kind)
+    oracle.kv_write_paged(oracle.widen(v, kind), stride, kv_pos, table, n_logical, 1, 0, bs, bb, ref, True, kv_kind)
+    got = arena.cpu().numpy()
+    row_bytes = stride * 2
+    kmag = pair_magnitude(kf, nkv, hd, hd, pairing)
+    for b in range(batch):
+        phys = table[kv_pos[b] // bs]
+        base = phys * bb + (kv_pos[b] % bs) * row_bytes
+        vbase = base + bs * row_bytes
+        assert_exact(got[vbase:vbase + row_bytes], ref[vbase:vbase + row_bytes], f"V row {b}")
+        gk = got[base:base + row_bytes].view(np.uint16)
+        rk = ref[base:base + row_bytes].view(np.uint16)
+        assert_rope_close(gk, rk, kmag[b], kv_kind, f"K row {b}")
+        got[base:base + row_bytes] = ref[base:base + row_bytes]
+        got[vbase:vbase + row_bytes] = ref[vbase:vbase + row_bytes]
+    assert_exact(got, ref, "untouched arena bytes")
+
+
+def test_kv_write_out_of_range_flags(ops, dev):
+    from fellm_amd.ops import PagedKvCache
+
+    stride, bs = 64, 16
+    bb, arena = _cache(dev, 4, bs, stride, "f16")
+    # row 1, logical block 3 -> physical block 9, outside the 4-block arena
+    table = np.array([0, 1, 2, 3, 0, 1, 2, 9], np.uint32)
+    cache = PagedKvCache(arena, torch.from_numpy(table.view(np.int32)).to(dev), 1, 4, bs, bb, stride, torch.float16)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    rows = torch.ones((2, stride), dtype=torch.float32, device=dev)
+    pos = torch.tensor([5, 3 * bs + 1], dtype=torch.int32, device=dev)
+    ops.kv_write(rows, pos, cache, err_flag=flag)
+    sync()
+    assert int(flag.item()) == 1
+    a = arena.cpu().numpy()
+    assert (a[5 * stride * 2: 6 * stride * 2].view(np.uint16) == 0x3C00).all()  # f16 1.0 in block 0 slot 5
+
+
+# ---- Router --------------------------------------------------------------------
+@pytest.mark.parametrize("n_exp,k", [(128, 8), (64, 6), (256, 8), (512, 32), (60, 1), (128, 128)])
+@pytest.mark.parametrize("gating,norm,rsf", [(1, True, 0.0), (2, False, 2.5), (1, False, 1.0)])
+def test_router_topk(ops, dev, n_exp, k, gating, norm, rsf):
+    rng = np.random.default_rng(n_exp * 100 + k)
+    tokens = 1023
+    logits = rng.normal(size=(tokens, n_exp)).astype(np.float32)
+    # constructed ties: equal logits in a few rows, and logits that differ by one ulp
+    logits[0, :] = 0.5
+    logits[1, : n_exp // 2] = logits[1, n_exp // 2 - 1]
+    logits[2, 1] = np.nextafter(logits[2, 0], np.float32(np.inf))
+    ids_ref, w_ref = oracle.router(logits, k, gating, norm, rsf)
+    ids, w = ops.router_topk(torch.from_numpy(logits).to(dev), k, gating_func=gating, norm_topk_prob=norm,
+                             routed_scaling_factor=rsf)
+    assert_exact(from_dev(ids), ids_ref, "ids")
+    assert_exact(from_dev(w), w_ref, "weights")
