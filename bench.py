@@ -1,0 +1,389 @@
+"""Benchmark of FeLLM's per-layer memory-bound op chain on one MI355X.
+
+Default workload: BASELINE configs[1], Llama-3-8B-shaped prefill, T = 4096
+tokens, f16 activations with f32 arithmetic:
+  embedding gather  128256 x 4096 f16 table -> f16 rows
+  residual add + RMSNorm  H = 4096, eps 1e-5 (reads x, r; writes h, y)
+  RoPE q + k  head_dim 128, 32 Q / 8 KV heads, theta 5e5, positions 0..4095
+  SwiGLU  I = 14336
+One step = one pass of the four kernels over one batch of synthetic inputs
+already resident in HBM.  Three input sets rotate between steps (> 1.8 GB
+touched per rotation) so the 256 MB MALL cannot serve repeated reads.
+
+Per-op kernel time comes from HIP events recorded on the stream the kernels
+run on; achieved GB/s = algorithmic bytes / kernel time (bytes each op must
+read and write once).  `value` = tokens per second of the whole timed
+region (wall clock, K steps).  The CPU baseline times the C restatement of
+backend-cpu (oracle/, 1 thread) on a bounded sample of the same chain.
+
+--suite measures every BASELINE config's ops (per-op GB/s table) instead.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "achieved HBM GB/s (% of peak) per fused op; tokens/s for op chain at 8B shape"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--sets", type=int, default=3, help="rotating input sets")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
+    ap.add_argument("--suite", action="store_true", help="per-op table for every config")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 512 MiB device copy (PMC byte-counter calibration)")
+    return ap.parse_args()
+
+
+# --------------------------------------------------------------------------- #
+# Workloads
+# --------------------------------------------------------------------------- #
+class Op:
+    def __init__(self, name, nbytes, fn):
+        self.name, self.nbytes, self.fn = name, nbytes, fn
+
+
+def c2_ops(torch, ops, dev, n_sets, seed=1):
+    """Llama-3-8B prefill chain."""
+    T, H, I, V = 4096, 4096, 14336, 128256
+    nq, nkv, hd, theta = 32, 8, 128, 500000.0
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    f16 = torch.float16
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * std).to(f16)
+
+    table = randn(V, H, std=0.02)
+    w_norm = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).float()
+    inv = ops.rope_inv_freqs(theta, hd).to(dev)
+    pos = torch.arange(T, dtype=torch.int32, device=dev)
+    sets = []
+    for _ in range(n_sets):
+        s = {
+            "ids": torch.randint(0, V, (T,), generator=g, device=dev, dtype=torch.int32),
+            "emb": torch.empty(T, H, dtype=f16, device=dev),
+            "x": randn(T, H), "r": randn(T, H, std=2.0),
+            "h": torch.empty(T, H, dtype=f16, device=dev), "y": torch.empty(T, H, dtype=f16, device=dev),
+            "q": randn(T, nq * hd), "k": randn(T, nkv * hd),
+            "qo": torch.empty(T, nq * hd, dtype=f16, device=dev), "ko": torch.empty(T, nkv * hd, dtype=f16, device=dev),
+            "gate": randn(T, I), "up": randn(T, I), "act": torch.empty(T, I, dtype=f16, device=dev),
+        }
+        sets.append(s)
+    e = 2  # bytes per f16
+    bytes_emb = T * H * e * 2 + T * 4
+    bytes_norm = T * H * e * 4
+    bytes_rope = T * (nq + nkv) * hd * e * 2 + T * 4
+    bytes_swiglu = T * I * e * 3
+
+    def op_emb(s):
+        ops.embedding(table, s["ids"], out=s["emb"])
+
+    def op_norm(s):
+        ops.add_rmsnorm(s["x"], s["r"], w_norm, 1e-5, h_out=s["h"], y_out=s["y"])
+
+    def op_rope(s):
+        ops.rope(s["q"], inv, head_dim=hd, pairing=0, positions=pos, x2=s["k"], out1=s["qo"], out2=s["ko"])
+
+    def op_swiglu(s):
+        ops.silu_gate(s["gate"], s["up"], out=s["act"])
+
+    chain = [Op("embedding_f16", bytes_emb, op_emb), Op("add_rmsnorm", bytes_norm, op_norm),
+             Op("rope_qk", bytes_rope, op_rope), Op("swiglu", bytes_swiglu, op_swiglu)]
+    return chain, sets, T
+
+
+def c3_ops(torch, ops, dev, n_sets, seed=3):
+    """Qwen2-7B quantized embedding gather, Zipf ids."""
+    import numpy as np
+
+    from fellm_amd import synth
+
+    V, D, T = 152064, 3584, 8192
+    rng = np.random.default_rng(seed)
+    q4 = torch.from_numpy(synth.q4k_table(rng, V, D)).to(dev)
+    q6 = torch.from_numpy(synth.q6k_table(rng, V, D)).to(dev)
+    w = torch.from_numpy(rng.normal(1.0, 0.1, size=D).astype(np.float32)).to(dev)
+    sets = [{"ids": torch.from_numpy(synth.zipf_ids(rng, T, V).view(np.int32)).to(dev),
+             "out": torch.empty(T, D, dtype=torch.float16, device=dev),
+             "y": torch.empty(T, D, dtype=torch.float16, device=dev)} for _ in range(n_sets)]
+    out_b = T * D * 2
+    chain = [
+        Op("q4k_gather", T * 2016 + out_b + T * 4, lambda s: ops.embedding(q4, s["ids"], dim=D, qtype="q4k",
+                                                                           out=s["out"])),
+        Op("q6k_gather", T * 2940 + out_b + T * 4, lambda s: ops.embedding(q6, s["ids"], dim=D, qtype="q6k",
+                                                                           out=s["out"])),
+        Op("q4k_gather_rmsnorm", T * 2016 + 2 * out_b + T * 4,
+           lambda s: ops.embedding_rmsnorm(q4, s["ids"], w, 1e-6, dim=D, qtype="q4k", h_out=s["out"],
+                                           y_out=s["y"])),
+    ]
+    return chain, sets, T
+
+
+def c4_ops(torch, ops, dev, n_sets, seed=4):
+    """Llama-3-70B continuous-batching decode step, 256 sequences."""
+    import numpy as np
+
+    from fellm_amd import synth
+
+    B, nq, nkv, hd, bs, n_blocks = 256, 64, 8, 128, 16, 65536
+    H, I = 8192, 28672
+    stride = nkv * hd
+    bf = torch.bfloat16
+    rng = np.random.default_rng(seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    bb = ops.PagedKvCache.block_bytes_for(stride, bs)
+    arena = torch.zeros(n_blocks * bb, dtype=torch.uint8, device=dev)
+    inv = ops.rope_inv_freqs(500000.0, hd).to(dev)
+    w = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).float()
+    sets = []
+    for _ in range(n_sets):
+        pos, table, n_logical = synth.paged_layout(rng, B, n_blocks, bs, 32768)
+        cache = ops.PagedKvCache(arena, torch.from_numpy(table.view(np.int32)).to(dev), 1, n_logical, bs, bb, stride,
+                                 bf)
+        sets.append({
+            "pos": torch.from_numpy(pos.view(np.int32)).to(dev), "cache": cache,
+            "q": torch.randn(B, nq * hd, generator=g, device=dev).to(bf),
+            "k": torch.randn(B, stride, generator=g, device=dev).to(bf),
+            "v": torch.randn(B, stride, generator=g, device=dev).to(bf),
+            "qo": torch.empty(B, nq * hd, dtype=bf, device=dev),
+            "x": torch.randn(B, H, generator=g, device=dev).to(bf),
+            "r": (2 * torch.randn(B, H, generator=g, device=dev)).to(bf),
+            "h": torch.empty(B, H, dtype=bf, device=dev), "y": torch.empty(B, H, dtype=bf, device=dev),
+            "gate": torch.randn(B, I, generator=g, device=dev).to(bf),
+            "up": torch.randn(B, I, generator=g, device=dev).to(bf),
+            "act": torch.empty(B, I, dtype=bf, device=dev),
+        })
+    chain = [
+        Op("rope_kv_write", B * (nq * hd * 2 + 2 * stride) * 2 + B * 2 * stride * 2 + B * 4,
+           lambda s: ops.rope_kv_write(s["q"], s["k"], s["v"], inv, s["pos"], s["cache"], head_dim=hd,
+                                       q_out=s["qo"])),
+        Op("add_rmsnorm", B * H * 2 * 4, lambda s: ops.add_rmsnorm(s["x"], s["r"], w, 1e-5, h_out=s["h"],
+                                                                   y_out=s["y"])),
+        Op("swiglu", B * I * 2 * 3, lambda s: ops.silu_gate(s["gate"], s["up"], out=s["act"])),
+    ]
+    return chain, sets, B
+
+
+def c5_ops(torch, ops, dev, n_sets, seed=5):
+    """Qwen3-30B-A3B MoE layer ops, 16384 tokens."""
+    T, E, K, H, Iexp = 16384, 128, 8, 2048, 768
+    nq, nkv, hd = 32, 4, 128
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    inv = ops.rope_inv_freqs(1.0e6, hd).to(dev)
+    pos = torch.arange(T, dtype=torch.int32, device=dev)
+    w = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).float()
+    sets = []
+    for _ in range(n_sets):
+        sets.append({
+            "logits": torch.randn(T, E, generator=g, device=dev),
+            "ids": torch.empty(T, K, dtype=torch.int32, device=dev),
+            "wts": torch.empty(T, K, dtype=torch.float32, device=dev),
+            "gate": torch.randn(T * K, Iexp, generator=g, device=dev).to(bf),
+            "up": torch.randn(T * K, Iexp, generator=g, device=dev).to(bf),
+            "act": torch.empty(T * K, Iexp, dtype=bf, device=dev),
+            "x": torch.randn(T, H, generator=g, device=dev).to(bf),
+            "y": torch.empty(T, H, dtype=bf, device=dev),
+            "q": torch.randn(T, nq * hd, generator=g, device=dev).to(bf),
+            "k": torch.randn(T, nkv * hd, generator=g, device=dev).to(bf),
+            "qo": torch.empty(T, nq * hd, dtype=bf, device=dev),
+            "ko": torch.empty(T, nkv * hd, dtype=bf, device=dev),
+        })
+    chain = [
+        Op("router_topk", T * E * 4 + T * K * 8, lambda s: ops.router_topk(s["logits"], K, ids=s["ids"],
+                                                                          weights=s["wts"])),
+        Op("swiglu_routed", T * K * Iexp * 2 * 3, lambda s: ops.silu_gate(s["gate"], s["up"], out=s["act"])),
+        Op("rmsnorm", T * H * 2 * 2, lambda s: ops.rmsnorm(s["x"], w, 1e-6, out=s["y"])),
+        Op("rope_qk", T * (nq + nkv) * hd * 2 * 2 + T * 4,
+           lambda s: ops.rope(s["q"], inv, head_dim=hd, positions=pos, x2=s["k"], out1=s["qo"], out2=s["ko"])),
+    ]
+    return chain, sets, T
+
+
+# --------------------------------------------------------------------------- #
+# Timing
+# --------------------------------------------------------------------------- #
+def run_chain(torch, chain, sets, steps, warmup):
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        for op in chain:
+            op.fn(sets[i % len(sets)])
+    torch.cuda.synchronize()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in chain]
+          for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        s = sets[i % len(sets)]
+        for j, op in enumerate(chain):
+            ev[i][j][0].record(stream)
+            op.fn(s)
+            ev[i][j][1].record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    per_op = []
+    for j, op in enumerate(chain):
+        ms = sorted(ev[i][j][0].elapsed_time(ev[i][j][1]) for i in range(steps))
+        per_op.append({"op": op.name, "bytes": op.nbytes, "ms_median": ms[len(ms) // 2],
+                       "ms_mean": sum(ms) / len(ms)})
+    return (t1 - t0), per_op
+
+
+def op_report(per_op):
+    out = {}
+    for r in per_op:
+        gbps = r["bytes"] / (r["ms_mean"] * 1e-3) / 1e9
+        out[r["op"]] = {"bytes": r["bytes"], "us_mean": round(r["ms_mean"] * 1e3, 2),
+                        "us_median": round(r["ms_median"] * 1e3, 2), "GBps": round(gbps, 1),
+                        "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4)}
+    return out
+
+
+# --------------------------------------------------------------------------- #
+# CPU baseline: the oracle (C restatement of backend-cpu), 1 thread
+# --------------------------------------------------------------------------- #
+def cpu_baseline(budget_s: float):
+    import numpy as np
+
+    import oracle
+
+    T, H, I, V = 64, 4096, 14336, 4096  # sample: 64 tokens of the c2 chain
+    nq, nkv, hd = 32, 8, 128
+    rng = np.random.default_rng(7)
+    # The reference's op boundary is f32: the CPU path gathers f16 rows into f32.
+    table = (rng.normal(0, 0.02, size=(V, H))).astype(np.float16)
+    ids = rng.integers(0, V, size=T, dtype=np.uint32)
+    x = rng.normal(size=(T, H)).astype(np.float32)
+    r = (2 * rng.normal(size=(T, H))).astype(np.float32)
+    w = rng.normal(1.0, 0.1, size=H).astype(np.float32)
+    q = rng.normal(size=(T, nq * hd)).astype(np.float32)
+    k = rng.normal(size=(T, nkv * hd)).astype(np.float32)
+    inv = oracle.rope_inv_freqs(500000.0, hd)
+    pos = np.arange(T, dtype=np.uint32)
+    gt = rng.normal(size=(T, I)).astype(np.float32)
+    up = rng.normal(size=(T, I)).astype(np.float32)
+    oracle.lib()
+    iters, t0 = 0, time.perf_counter()
+    while True:
+        oracle.embedding(table.view(np.uint8), 1, V, H, ids)
+        h = oracle.add(x, r)
+        oracle.rmsnorm(h, w, 1e-5)
+        oracle.rope(q, nq, hd, hd, 0, inv, pos)
+        oracle.rope(k, nkv, hd, hd, 0, inv, pos)
+        oracle.silu_gate(gt, up)
+        iters += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    isa = "unknown"
+    try:
+        flags = Path("/proc/cpuinfo").read_text()
+        isa = "AVX-512" if "avx512f" in flags else ("AVX2" if "avx2" in flags else "SSE")
+        model = next((l.split(":", 1)[1].strip() for l in flags.splitlines() if l.startswith("model name")), "")
+    except OSError:
+        model = platform.processor()
+    return {"value": round(T * iters / el, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{iters} x 64-token c2 chain (embedding f16->f32, add, rmsnorm, rope q+k, swiglu) in "
+                      f"{el:.1f}s, f32 ops as backend-cpu, 1 thread",
+            "cpu": model, "isa": isa}
+
+
+# --------------------------------------------------------------------------- #
+def read_traffic():
+    """HBM bytes per SwiGLU launch from the committed rocprofv3 PMC summary, if present."""
+    p = ROOT / "profiles" / "swiglu_c2_pmc_traffic.txt"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every op shards by tokens "
+              "with no exchange; see DESIGN.md).  Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from fellm_amd import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.calibrate_copy:
+        n = 512 << 20
+        a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+
+    if args.suite:
+        result = {}
+        for name, make in (("c2", c2_ops), ("c3", c3_ops), ("c4", c4_ops), ("c5", c5_ops)):
+            chain, sets, _ = make(torch, ops, dev, args.sets)
+            _, per_op = run_chain(torch, chain, sets, args.steps, args.warmup)
+            result[name] = op_report(per_op)
+            del chain, sets
+            torch.cuda.empty_cache()
+        print(json.dumps({"suite": result}, indent=1))
+        return
+
+    chain, sets, T = c2_ops(torch, ops, dev, args.sets)
+    elapsed, per_op = run_chain(torch, chain, sets, args.steps, args.warmup)
+    rep = op_report(per_op)
+    ms_step = elapsed / args.steps * 1e3
+    kernel_sum_ms = sum(r["ms_mean"] for r in per_op)
+    dom = max(per_op, key=lambda r: r["bytes"])
+    achieved = dom["bytes"] / (dom["ms_mean"] * 1e-3) / 1e9
+    traffic = read_traffic()
+    line = {
+        "metric": METRIC,
+        "value": round(T * args.steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded; table ~N(0,0.02), x ~N(0,1), r ~N(0,4), ids uniform)",
+        "config": {"workload": "configs[1] Llama-3-8B prefill op chain: embedding f16 gather + add/RMSNorm "
+                               "H4096 + RoPE q+k hd128 32/8 + SwiGLU I14336", "tokens": T,
+                   "rotating_input_sets": args.sets},
+        "roofline": {"bound": "hbm", "kernel": dom["op"], "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic},
+        "ops": rep,
+        "chain_tokens_per_s_kernel_sum": round(T / (kernel_sum_ms * 1e-3), 1),
+        "chain_GBps_kernel_sum": round(sum(r["bytes"] for r in per_op) / (kernel_sum_ms * 1e-3) / 1e9, 1),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -7,11 +7,13 @@ one HIP runtime (they carry the same SONAME, libamdhip64.so.7).
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 from . import abi
 
-LIB_PATH = Path(__file__).resolve().parent / "libfellm_rocm_kernels.so"
+# FELLM_ROCM_LIB overrides the library path (e.g. to compare builds).
+LIB_PATH = Path(os.environ.get("FELLM_ROCM_LIB") or Path(__file__).resolve().parent / "libfellm_rocm_kernels.so")
 
 _lib: C.CDLL | None = None
 

@@ -45,29 +45,31 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: install ROCm or set HIPCC")
 
 
-def _compile(src: str) -> Path:
-    obj = BUILD / (Path(src).stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+def _compile(src: str, build_dir: Path = BUILD, extra=()) -> Path:
+    obj = build_dir / (Path(src).stem + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, *extra, "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    BUILD.mkdir(exist_ok=True)
+def build(verbose: bool = False, out: Path = LIB_PATH, build_dir: Path = BUILD, defines=()) -> Path:
+    """Compile every source and link ``out``; ``defines`` are extra -D flags."""
+    build_dir.mkdir(parents=True, exist_ok=True)
+    extra = [f"-D{d}" for d in defines]
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), 6)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, build_dir, extra), SOURCES))
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), *DEVICE_FLAGS, "-shared", "-fPIC", f"-Wl,--version-script={CSRC / 'exports.map'}",
            "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB_PATH}")
-    return LIB_PATH
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":

@@ -178,7 +178,7 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
 // exp(x) = 2^(k/32) * p(r), p cubic, all in double, one final rounding.
 // The x86_64 build contracts r = x*InvLn2N - kd and the Horner steps into FMA;
 // this restatement does the same.  Table: tab[i] = bits(2^(i/32)) - (i << 47).
-// Exhaustively equal to glibc expf over every float in (-103.97, 88.73).
+// Checked on the GPU against the host's glibc expf for all 2^32 inputs.
 // ---------------------------------------------------------------------------
 struct ExpfTable {
     uint64_t tab[32];
@@ -209,18 +209,18 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
         if (x < -0x1.9fe368p6f) return 0.0f;          // underflow
     }
     const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
-    const double Shift = 0x1.8p+52;
     const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
     const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
     const double xd = (double)x;
     const double z = InvLn2N * xd;
-    double kd = __dadd_rn(z, Shift);
-    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
-    kd = __dsub_rn(kd, Shift);
+    // glibc rounds z to the nearest integer with the add/subtract-0x1.8p52
+    // trick; |z| < 2^13 here, so rint gives the identical kd in one op.
+    const double kd = __builtin_rint(z);
+    const int32_t ki = (int32_t)kd;
     const double r = __fma_rn(InvLn2N, xd, -kd);
-    uint64_t t = tab[ki % 32];
-    t += ki << 47;
+    uint64_t t = tab[ki & 31];
+    t += (uint64_t)(int64_t)ki << 47;
     const double s = __longlong_as_double((long long)t);
     const double zz = __fma_rn(C0, r, C1);
     const double r2 = __dmul_rn(r, r);

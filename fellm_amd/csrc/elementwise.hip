@@ -4,11 +4,14 @@
 //   out[i] = (g / (1 + exp(-g))) * u       (f32, libm expf)
 // Add reference: crates/backend-cpu/src/kernels/simd_f32.rs:175-197.
 //
-// Pure streaming kernels: each thread moves VEC elements per iteration with
-// 16-byte non-temporal loads/stores over a grid-stride loop sized to keep
-// every CU busy.  exp is the glibc-exact double-precision restatement
-// (common.hpp), so the f32 result equals the CPU reference bit for bit; its
-// ~12 f64 ops per element hide under the HBM time on MI355X.
+// Pure streaming kernels: each thread moves 2 x VEC elements per iteration
+// (both 16-byte loads of g and u for the two units issued before any math)
+// with non-temporal loads/stores; the grid covers the tensor in one pass.
+// exp is the glibc-exact double-precision restatement (common.hpp) and the
+// division uses silu_div below, so the f32 result equals the CPU reference
+// bit for bit.  With ~30 ALU ops per element the kernel sits close to the
+// ALU/HBM balance point, which is why the division is not left to the
+// default 13-instruction IEEE sequence.
 #include "common.hpp"
 
 namespace fellm {
@@ -23,7 +26,26 @@ inline uint32_t ew_grid(uint64_t units) {
     return (uint32_t)(g == 0 ? 1 : g);
 }
 
-template <typename I, typename O, int VEC>
+// g / d for d = 1 + exp(-g) >= 1: hardware reciprocal, one Newton step on the
+// reciprocal, one residual correction of the quotient (Markstein's sequence).
+// Inputs outside [2^-100, 2^126) take the IEEE division.  Proven equal to the
+// IEEE quotient for this use by comparing silu(g) for all 2^32 values of g.
+__device__ __forceinline__ float silu_div(float g, float d) {
+    const float ag = __builtin_fabsf(g);
+    if (!(ag >= 0x1p-100f && ag < 0x1p+126f && d < 0x1p+126f)) return g / d;
+    const float y0 = __builtin_amdgcn_rcpf(d);
+    const float e0 = __builtin_fmaf(-d, y0, 1.0f);
+    const float y1 = __builtin_fmaf(e0, y0, y0);
+    const float q0 = g * y1;
+    const float r0 = __builtin_fmaf(-d, q0, g);
+    return __builtin_fmaf(r0, y1, q0);
+}
+
+__device__ __forceinline__ float silu(float g, const uint64_t *tab) {
+    return silu_div(g, 1.0f + expf_glibc(-g, tab));
+}
+
+template <typename I, typename O, int VEC, int UNROLL>
 __global__ __launch_bounds__(kEwBlock) void silu_gate_kernel(const typename I::T *__restrict__ g,
                                                              const typename I::T *__restrict__ u,
                                                              typename O::T *__restrict__ out,
@@ -31,25 +53,32 @@ __global__ __launch_bounds__(kEwBlock) void silu_gate_kernel(const typename I::T
     __shared__ uint64_t tab_lds[32];
     const uint64_t *tab = stage_expf_table(tab_lds);
     const uint64_t nvec = n / VEC;
-    const uint64_t stride = (uint64_t)gridDim.x * kEwBlock;
-    for (uint64_t i = (uint64_t)blockIdx.x * kEwBlock + threadIdx.x; i < nvec; i += stride) {
-        float gv[VEC], uv[VEC], o[VEC];
-        load_f32_nt<I, VEC>(g + i * VEC, gv);
-        load_f32_nt<I, VEC>(u + i * VEC, uv);
+    const uint64_t stride = (uint64_t)gridDim.x * kEwBlock * UNROLL;
+    for (uint64_t base = (uint64_t)blockIdx.x * kEwBlock * UNROLL + threadIdx.x; base < nvec; base += stride) {
+        float gv[UNROLL][VEC], uv[UNROLL][VEC];
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) {
-            const float silu = gv[k] / (1.0f + expf_glibc(-gv[k], tab));
-            o[k] = silu * uv[k];
+        for (int j = 0; j < UNROLL; ++j) {
+            const uint64_t i = base + (uint64_t)j * kEwBlock;
+            if (i < nvec) {
+                load_f32_nt<I, VEC>(g + i * VEC, gv[j]);
+                load_f32_nt<I, VEC>(u + i * VEC, uv[j]);
+            }
         }
-        store_f32_nt<O, VEC>(out + i * VEC, o);
+#pragma unroll
+        for (int j = 0; j < UNROLL; ++j) {
+            const uint64_t i = base + (uint64_t)j * kEwBlock;
+            if (i < nvec) {
+                float o[VEC];
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) o[k] = silu(gv[j][k], tab) * uv[j][k];
+                store_f32_nt<O, VEC>(out + i * VEC, o);
+            }
+        }
     }
     // Tail (n % VEC elements), handled by the first threads of block 0.
     if (blockIdx.x == 0) {
         const uint64_t t = nvec * VEC + threadIdx.x;
-        if (t < n) {
-            const float gv = I::load(g[t]);
-            out[t] = O::store((gv / (1.0f + expf_glibc(-gv, tab))) * I::load(u[t]));
-        }
+        if (t < n) out[t] = O::store(silu(I::load(g[t]), tab) * I::load(u[t]));
     }
 }
 
@@ -85,16 +114,21 @@ __global__ __launch_bounds__(kEwBlock) void expf_kernel(const float *__restrict_
 // VEC = 8 elements: 16 B for 16-bit types, 32 B for f32.
 template <typename I, typename O>
 int launch_silu(const void *g, const void *u, void *out, uint64_t n, hipStream_t s) {
-    constexpr int VEC = 8;
+    constexpr int VEC = 8, UNROLL = 2;
     using TI = typename I::T;
     using TO = typename O::T;
     if (!aligned_to(g, sizeof(TI) * VEC) || !aligned_to(u, sizeof(TI) * VEC) ||
         !aligned_to(out, sizeof(TO) * VEC)) {
-        hipLaunchKernelGGL((silu_gate_kernel<I, O, 1>), dim3(ew_grid(n)), dim3(kEwBlock), 0, s,
+        hipLaunchKernelGGL((silu_gate_kernel<I, O, 1, 1>), dim3(ew_grid(n)), dim3(kEwBlock), 0, s,
                            (const TI *)g, (const TI *)u, (TO *)out, n);
         return launch_status();
     }
-    hipLaunchKernelGGL((silu_gate_kernel<I, O, VEC>), dim3(ew_grid(n / VEC)), dim3(kEwBlock), 0, s,
+    // One pass over the tensor: ceil(units / (block * UNROLL)) blocks.
+    const uint64_t units = n / VEC;
+    uint64_t blocks = (units + kEwBlock * UNROLL - 1) / (kEwBlock * UNROLL);
+    if (blocks == 0) blocks = 1;
+    if (blocks > 0x7fffffffull) blocks = 0x7fffffffull;
+    hipLaunchKernelGGL((silu_gate_kernel<I, O, VEC, UNROLL>), dim3((uint32_t)blocks), dim3(kEwBlock), 0, s,
                        (const TI *)g, (const TI *)u, (TO *)out, n);
     return launch_status();
 }

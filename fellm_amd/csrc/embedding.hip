@@ -14,14 +14,23 @@
 //           16-byte aligned because a block is 144 = 9*16 bytes) is loaded
 //           straight from global memory and shared via L1 by the 16 parts of
 //           the block;
-//   Q6_K  : 16 elements = 4 runs of 4.  210-byte blocks are only 2-byte
-//           aligned, so the whole row is first staged into LDS with
-//           coalesced dword loads and decoded from there.
+//   Q6_K  : 16 elements = 4 runs of 4, read with unaligned dword loads
+//           (210-byte blocks are only 2-byte aligned).
 // The arithmetic order is the reference's, with FMA contraction disabled at
 // compile time:  Q4_K  y = (d*sc)*q - (dmin*m);   Q6_K  y = (d*sc)*(q-32).
 // With NORM the decoded row stays in registers for the sum of squares and
 // is written once as h (gathered row) and once as y (normalised row).
 #include "common.hpp"
+
+// Build knob: threads per workgroup (one token row per workgroup).
+#ifndef FELLM_EMB_BLOCK
+#define FELLM_EMB_BLOCK 256
+#endif
+// Build knob: plain gathers decode and store part by part (1) or decode all
+// parts into registers first (0).
+#ifndef FELLM_EMB_LOOP
+#define FELLM_EMB_LOOP 1
+#endif
 
 namespace fellm {
 namespace {
@@ -34,7 +43,6 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
 template <typename A, int VEC>
 struct DenseDec {
     static constexpr int OUT = VEC, RUNS = 1, RUNLEN = VEC;
-    static constexpr bool kStage = false;
     __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)dim * sizeof(typename A::T); }
     __host__ __device__ static uint32_t parts(uint32_t dim) { return dim / VEC; }
     __device__ static uint32_t run_off(uint32_t p, int) { return p * VEC; }
@@ -45,7 +53,6 @@ struct DenseDec {
 
 struct Q4KDec {
     static constexpr int OUT = 16, RUNS = 2, RUNLEN = 8;
-    static constexpr bool kStage = false;
     __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)(dim / 256) * 144; }
     __host__ __device__ static uint32_t parts(uint32_t dim) { return (dim / 256) * 16; }
     __device__ static uint32_t run_off(uint32_t p, int r) {
@@ -88,28 +95,39 @@ struct Q4KDec {
 
 struct Q6KDec {
     static constexpr int OUT = 16, RUNS = 4, RUNLEN = 4;
-    static constexpr bool kStage = true;
     __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)(dim / 256) * 210; }
     __host__ __device__ static uint32_t parts(uint32_t dim) { return (dim / 256) * 16; }
     __device__ static uint32_t run_off(uint32_t p, int r) {
         const uint32_t q = p % 16;
         return (p / 16) * 256 + 128 * (q / 8) + 4 * (q % 8) + 32 * r;
     }
-    // `row` points into LDS.  Block layout (dequant.rs:315-370): ql[128],
-    // qh[64], int8 scales[16], f16 d at 208.
+    // Block layout (dequant.rs:315-370): ql[128], qh[64], int8 scales[16],
+    // f16 d at 208.  210-byte blocks are only 2-byte aligned; gfx950 serves
+    // unaligned dword loads directly, so each part reads its 4+4+4 quant
+    // bytes and the 8 scale bytes of its half as unaligned dwords.
+    __device__ static uint32_t ld32(const uint8_t *p) {
+        uint32_t v;
+        __builtin_memcpy(&v, p, 4);
+        return v;
+    }
     __device__ static void decode(const uint8_t *row, uint32_t p, float (&v)[OUT]) {
         const uint8_t *blk = row + (size_t)(p / 16) * 210;
         const uint32_t q = p % 16, hh = q / 8, l0 = 4 * (q % 8), is = l0 / 16;
-        const uint8_t *ql = blk + 64 * hh;
-        const uint8_t *qh = blk + 128 + 32 * hh;
-        const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192 + 8 * hh);
-        const float d = half_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
-        const float ds0 = d * (float)sc[is], ds1 = d * (float)sc[is + 2];
-        const float ds2 = d * (float)sc[is + 4], ds3 = d * (float)sc[is + 6];
+        const uint32_t qa = ld32(blk + 64 * hh + l0);       // ql[l0 .. l0+3]
+        const uint32_t qb = ld32(blk + 64 * hh + 32 + l0);  // ql[l0+32 .. l0+35]
+        const uint32_t qhw = ld32(blk + 128 + 32 * hh + l0);
+        const uint32_t s0 = ld32(blk + 192 + 8 * hh), s1 = ld32(blk + 196 + 8 * hh);
+        uint16_t dbits;
+        __builtin_memcpy(&dbits, blk + 208, 2);
+        const float d = half_bits_to_f32(dbits);
+        // scales[is + 2k] for k = 0..3 (is is 0 or 1): bytes is, is+2 of s0 and of s1.
+        const int32_t sc0 = (int8_t)(s0 >> (8 * is)), sc1 = (int8_t)(s0 >> (8 * (is + 2)));
+        const int32_t sc2 = (int8_t)(s1 >> (8 * is)), sc3 = (int8_t)(s1 >> (8 * (is + 2)));
+        const float ds0 = d * (float)sc0, ds1 = d * (float)sc1;
+        const float ds2 = d * (float)sc2, ds3 = d * (float)sc3;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const uint32_t l = l0 + m;
-            const int32_t a = ql[l], b = ql[l + 32], h = qh[l];
+            const int32_t a = (qa >> (8 * m)) & 0xff, b = (qb >> (8 * m)) & 0xff, h = (qhw >> (8 * m)) & 0xff;
             const int32_t q1 = ((a & 0xf) | ((h & 3) << 4)) - 32;
             const int32_t q2 = ((b & 0xf) | (((h >> 2) & 3) << 4)) - 32;
             const int32_t q3 = ((a >> 4) | (((h >> 4) & 3) << 4)) - 32;
@@ -122,43 +140,34 @@ struct Q6KDec {
     }
 };
 
-template <typename D, typename O>
+// Plain gathers stream their output with non-temporal stores; the fused
+// gather + RMSNorm stores after its reduction barrier and measured faster
+// with regular stores.
+template <typename D, typename O, bool NT>
 __device__ __forceinline__ void store_part(typename O::T *row, uint32_t p, const float (&v)[D::OUT]) {
 #pragma unroll
     for (int r = 0; r < D::RUNS; ++r) {
         float t[D::RUNLEN];
 #pragma unroll
         for (int k = 0; k < D::RUNLEN; ++k) t[k] = v[r * D::RUNLEN + k];
-        store_f32_nt<O, D::RUNLEN>(row + D::run_off(p, r), t);
+        if constexpr (NT)
+            store_f32_nt<O, D::RUNLEN>(row + D::run_off(p, r), t);
+        else
+            store_f32<O, D::RUNLEN>(row + D::run_off(p, r), t);
     }
 }
 
-// Stages `bytes` (even) of a table row into LDS.  Dword loads when the source
-// is 4-byte aligned, else 16-bit loads.
-template <int BLOCK>
-__device__ __forceinline__ void stage_row(const uint8_t *src, uint8_t *lds, uint64_t bytes) {
-    if ((reinterpret_cast<uintptr_t>(src) & 3) == 0) {
-        const uint32_t nw = (uint32_t)(bytes / 4);
-        for (uint32_t i = threadIdx.x; i < nw; i += BLOCK)
-            reinterpret_cast<uint32_t *>(lds)[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(src) + i);
-        if ((bytes & 2) && threadIdx.x == 0)
-            reinterpret_cast<uint16_t *>(lds)[bytes / 2 - 1] = reinterpret_cast<const uint16_t *>(src)[bytes / 2 - 1];
-    } else {
-        const uint32_t nh = (uint32_t)(bytes / 2);
-        for (uint32_t i = threadIdx.x; i < nh; i += BLOCK)
-            reinterpret_cast<uint16_t *>(lds)[i] = reinterpret_cast<const uint16_t *>(src)[i];
-    }
-    __syncthreads();
-}
+constexpr int kEmbBlock = FELLM_EMB_BLOCK;
 
-constexpr int kEmbBlock = 256;
-
+// One workgroup per token row.  Each thread decodes its (up to MAXC) parts
+// into registers before storing anything, so all of its loads are in flight
+// together.  MAXC == 0 selects a looping variant for rows longer than
+// 8 * kEmbBlock parts (no fused norm).
 template <typename D, typename O, int MAXC, bool NORM>
 __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
     const uint8_t *__restrict__ table, uint64_t vocab, uint32_t dim, const uint32_t *__restrict__ ids,
     typename O::T *__restrict__ h, typename O::T *__restrict__ y, const float *__restrict__ w, float eps,
     uint32_t *__restrict__ err) {
-    extern __shared__ __align__(16) uint8_t lds_row[];
     __shared__ float red[kEmbBlock / kWave];
     const uint32_t row = blockIdx.x;
     const uint32_t id = ids[row];
@@ -166,13 +175,9 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
     if (bad && threadIdx.x == 0 && err) atomicOr(err, 1u);
     const uint64_t rb = D::row_bytes(dim);
     const uint8_t *src = table + (bad ? 0 : (uint64_t)id * rb);
-    if constexpr (D::kStage) {
-        stage_row<kEmbBlock>(src, lds_row, rb);
-        src = lds_row;
-    }
     const uint32_t parts = D::parts(dim);
     const size_t obase = (size_t)row * dim;
-    if constexpr (!NORM) {
+    if constexpr (MAXC == 0) {
         for (uint32_t p = threadIdx.x; p < parts; p += kEmbBlock) {
             float v[D::OUT];
             D::decode(src, p, v);
@@ -180,8 +185,9 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
 #pragma unroll
                 for (int k = 0; k < D::OUT; ++k) v[k] = 0.0f;
             }
-            store_part<D, O>(h + obase, p, v);
+            store_part<D, O, true>(h + obase, p, v);
         }
+        return;
     } else {
         float v[MAXC][D::OUT];
         float ss = 0.0f;
@@ -193,26 +199,34 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
 #pragma unroll
                 for (int k = 0; k < D::OUT; ++k) {
                     if (bad) v[c][k] = 0.0f;
-                    ss += v[c][k] * v[c][k];
+                    if constexpr (NORM) ss += v[c][k] * v[c][k];
                 }
             }
         }
-        ss = block_sum<kEmbBlock>(ss, red);
-        const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
+        if constexpr (!NORM) {
 #pragma unroll
-        for (int c = 0; c < MAXC; ++c) {
-            const uint32_t p = c * kEmbBlock + threadIdx.x;
-            if (p < parts) {
-                if (h) store_part<D, O>(h + obase, p, v[c]);
-                float o[D::OUT];
+            for (int c = 0; c < MAXC; ++c) {
+                const uint32_t p = c * kEmbBlock + threadIdx.x;
+                if (p < parts) store_part<D, O, true>(h + obase, p, v[c]);
+            }
+        } else {
+            ss = block_sum<kEmbBlock>(ss, red);
+            const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
 #pragma unroll
-                for (int r = 0; r < D::RUNS; ++r) {
-                    const uint32_t off = D::run_off(p, r);
+            for (int c = 0; c < MAXC; ++c) {
+                const uint32_t p = c * kEmbBlock + threadIdx.x;
+                if (p < parts) {
+                    if (h) store_part<D, O, false>(h + obase, p, v[c]);
+                    float o[D::OUT];
 #pragma unroll
-                    for (int k = 0; k < D::RUNLEN; ++k)
-                        o[r * D::RUNLEN + k] = (v[c][r * D::RUNLEN + k] * scale) * w[off + k];
+                    for (int r = 0; r < D::RUNS; ++r) {
+                        const uint32_t off = D::run_off(p, r);
+#pragma unroll
+                        for (int k = 0; k < D::RUNLEN; ++k)
+                            o[r * D::RUNLEN + k] = (v[c][r * D::RUNLEN + k] * scale) * w[off + k];
+                    }
+                    store_part<D, O, false>(y + obase, p, o);
                 }
-                store_part<D, O>(y + obase, p, o);
             }
         }
     }
@@ -222,27 +236,34 @@ template <typename D, typename O>
 int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids,
                void *h, void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
     using TO = typename O::T;
-    const size_t lds = D::kStage ? (size_t)((D::row_bytes(dim) + 15) / 16 * 16) : 0;
-    if (lds > 64 * 1024) return FELLM_ERR_SHAPE;
     const dim3 grid(n_ids), block(kEmbBlock);
     const uint8_t *tb = static_cast<const uint8_t *>(table);
+    const uint32_t chunks = (D::parts(dim) + kEmbBlock - 1) / kEmbBlock;
+#define FELLM_EMB(C, NORM)                                                                          \
+    if (chunks <= C) {                                                                              \
+        hipLaunchKernelGGL((embedding_kernel<D, O, C, NORM>), grid, block, 0, s, tb, vocab, dim, ids,  \
+                           (TO *)h, (TO *)y, w, eps, err);                                          \
+        return launch_status();                                                                     \
+    }
     if (!w) {
-        hipLaunchKernelGGL((embedding_kernel<D, O, 1, false>), grid, block, lds, s, tb, vocab, dim, ids,
-                           (TO *)h, nullptr, nullptr, 0.0f, err);
+        if (FELLM_EMB_LOOP) {
+            hipLaunchKernelGGL((embedding_kernel<D, O, 0, false>), grid, block, 0, s, tb, vocab, dim, ids, (TO *)h,
+                               nullptr, nullptr, 0.0f, err);
+            return launch_status();
+        }
+        FELLM_EMB(1, false)
+        FELLM_EMB(2, false)
+        FELLM_EMB(4, false)
+        FELLM_EMB(8, false)
+        hipLaunchKernelGGL((embedding_kernel<D, O, 0, false>), grid, block, 0, s, tb, vocab, dim, ids, (TO *)h,
+                           nullptr, nullptr, 0.0f, err);
         return launch_status();
     }
-    const uint32_t chunks = (D::parts(dim) + kEmbBlock - 1) / kEmbBlock;
-#define FELLM_EMB_NORM(C)                                                                          \
-    if (chunks <= C) {                                                                             \
-        hipLaunchKernelGGL((embedding_kernel<D, O, C, true>), grid, block, lds, s, tb, vocab, dim, ids, \
-                           (TO *)h, (TO *)y, w, eps, err);                                          \
-        return launch_status();                                                                    \
-    }
-    FELLM_EMB_NORM(1)
-    FELLM_EMB_NORM(2)
-    FELLM_EMB_NORM(4)
-    FELLM_EMB_NORM(8)
-#undef FELLM_EMB_NORM
+    FELLM_EMB(1, true)
+    FELLM_EMB(2, true)
+    FELLM_EMB(4, true)
+    FELLM_EMB(8, true)
+#undef FELLM_EMB
     return FELLM_ERR_SHAPE;
 }
 

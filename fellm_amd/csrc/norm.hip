@@ -14,6 +14,19 @@
 #include "common.hpp"
 
 namespace fellm {
+
+// x and residual are read once with non-temporal loads.  h and y are written
+// after the reduction barrier: regular stores measured faster for the
+// many-row (prefill) layout, non-temporal ones for the 1024-thread decode
+// layout, hence the NT_STORE template flag.
+template <typename A, int N>
+__device__ __forceinline__ void norm_load(const typename A::T *p, float (&v)[N]) {
+    load_f32_nt<A, N>(p, v);
+}
+template <typename A, int N, bool NT>
+__device__ __forceinline__ void norm_store(typename A::T *p, const float (&v)[N]) {
+    if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
+}
 namespace {
 
 template <typename A, typename O, int BLOCK, int VEC, int NCHUNK, bool ADD, bool STORE_H>
@@ -30,16 +43,16 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_kernel(
     for (int c = 0; c < NCHUNK; ++c) {
         const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
         if (base < group) {
-            load_f32_nt<A, VEC>(xr + base, v[c]);
+            norm_load<A, VEC>(xr + base, v[c]);
             if constexpr (ADD) {
                 float rv[VEC];
-                load_f32_nt<A, VEC>(r + row * group + base, rv);
+                norm_load<A, VEC>(r + row * group + base, rv);
 #pragma unroll
                 for (int i = 0; i < VEC; ++i) {
                     // h is stored in the activation dtype and normalised as stored.
                     v[c][i] = A::load(A::store(v[c][i] + rv[i]));
                 }
-                if constexpr (STORE_H) store_f32_nt<A, VEC>(h + row * group + base, v[c]);
+                if constexpr (STORE_H) norm_store<A, VEC, (BLOCK >= 1024)>(h + row * group + base, v[c]);
             }
 #pragma unroll
             for (int i = 0; i < VEC; ++i) ss += v[c][i] * v[c][i];
@@ -55,7 +68,7 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_kernel(
             load_f32<F32, VEC>(w + base, wv);
 #pragma unroll
             for (int i = 0; i < VEC; ++i) o[i] = (v[c][i] * scale) * wv[i];
-            store_f32_nt<O, VEC>(y + row * group + base, o);
+            norm_store<O, VEC, (BLOCK >= 1024)>(y + row * group + base, o);
         }
     }
 }

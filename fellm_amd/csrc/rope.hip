@@ -22,6 +22,15 @@
 
 #include "common.hpp"
 
+// Build knob: sin/cos of theta evaluated in double then rounded (1) or with f32 sincosf (0).
+#ifndef FELLM_ROPE_DOUBLE_TRIG
+#define FELLM_ROPE_DOUBLE_TRIG 1
+#endif
+// Build knob: (row, head) slots each thread loads before rotating/storing.
+#ifndef FELLM_ROPE_UNROLL
+#define FELLM_ROPE_UNROLL 1
+#endif
+
 namespace fellm {
 namespace {
 
@@ -59,137 +68,241 @@ __device__ __forceinline__ void store_cache(uint8_t *arena, uint64_t byte_off, u
     store_f32<C, N>(reinterpret_cast<typename C::T *>(arena + byte_off) + elem, v);
 }
 
-// Rotates item `it` of one head.  Items [0, n_rot) are rotated, the rest
-// pass through.  Returns the element offsets of the two runs of PV values.
+// Element offset, within its head, of item `it`'s first run and of its
+// second run (PV elements each).  Items [0, n_rot) are rotated; the rest are
+// the pass-through span.  Adjacent pairings keep both runs contiguous.
+__device__ __forceinline__ void item_offsets(uint32_t it, uint32_t n_rot, uint32_t head_dim, uint32_t rope_dim,
+                                             uint32_t pairing, int PV, uint32_t &lo, uint32_t &hi) {
+    if (it >= n_rot) {
+        lo = (pairing == 2 ? 0 : rope_dim) + (it - n_rot) * 2 * PV;
+        hi = lo + PV;
+    } else if (pairing == 1) {
+        lo = it * PV;
+        hi = lo + rope_dim / 2;
+    } else {
+        lo = (pairing == 2 ? head_dim - rope_dim : 0) + 2 * it * PV;
+        hi = lo + PV;
+    }
+}
+
+// Loads the 2*PV elements of item `it` of head `hd` (q heads, then k heads,
+// then v heads) of `row`: e[0..PV) is the first run, e[PV..2PV) the second.
 template <typename A, int PV>
-__device__ __forceinline__ void rope_item(const typename A::T *src, uint32_t it, uint32_t n_rot,
-                                          uint32_t head_dim, uint32_t rope_dim, uint32_t pairing,
-                                          const float2 *cs, float (&lo)[PV], float (&hi)[PV],
-                                          uint32_t &off_lo, uint32_t &off_hi) {
-    if (it >= n_rot) {  // passthrough: 2*PV consecutive elements after the rotated span
-        const uint32_t start = pairing == 2 ? 0 : rope_dim;
-        off_lo = start + (it - n_rot) * 2 * PV;
-        off_hi = off_lo + PV;
-        load_f32<A, PV>(src + off_lo, lo);
-        load_f32<A, PV>(src + off_hi, hi);
+__device__ __forceinline__ void rope_load(const typename A::T *x1, const typename A::T *x2,
+                                          const typename A::T *x3, uint32_t nh1, uint32_t nh2, size_t w1, size_t w2,
+                                          uint32_t row, uint32_t hd, uint32_t it, uint32_t head_dim, uint32_t rope_dim,
+                                          uint32_t pairing, uint32_t n_rot, float (&e)[2 * PV]) {
+    const typename A::T *src;
+    size_t base;
+    if (hd < nh1) {
+        src = x1;
+        base = (size_t)row * w1 + (size_t)hd * head_dim;
+    } else if (hd < nh1 + nh2) {
+        src = x2;
+        base = (size_t)row * w2 + (size_t)(hd - nh1) * head_dim;
+    } else {  // V head: plain 2*PV-element run
+        load_f32<A, 2 * PV>(x3 + (size_t)row * w2 + (size_t)(hd - nh1 - nh2) * head_dim + it * 2 * PV, e);
         return;
     }
-    if (pairing == 1) {
-        const uint32_t half = rope_dim / 2;
-        const uint32_t i0 = it * PV;
-        off_lo = i0;
-        off_hi = i0 + half;
+    uint32_t lo, hi;
+    item_offsets(it, n_rot, head_dim, rope_dim, pairing, PV, lo, hi);
+    if (hi == lo + PV) {
+        load_f32<A, 2 * PV>(src + base + lo, e);
+    } else {
         float a[PV], b[PV];
-        load_f32<A, PV>(src + off_lo, a);
-        load_f32<A, PV>(src + off_hi, b);
+        load_f32<A, PV>(src + base + lo, a);
+        load_f32<A, PV>(src + base + hi, b);
 #pragma unroll
         for (int k = 0; k < PV; ++k) {
-            const float2 sc = cs[i0 + k];  // (sin, cos)
-            lo[k] = a[k] * sc.y - b[k] * sc.x;
-            hi[k] = a[k] * sc.x + b[k] * sc.y;
+            e[k] = a[k];
+            e[PV + k] = b[k];
+        }
+    }
+}
+
+// Rotates a loaded item and stores it (and the K/V cache copies in MODE 1).
+template <typename A, typename C, int PV, int MODE>
+__device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A::T *out1, const typename A::T *x2,
+                                            typename A::T *out2, uint32_t nh1, uint32_t nh2, size_t w1, size_t w2,
+                                            uint32_t row, uint32_t hd, uint32_t it, uint32_t head_dim,
+                                            uint32_t rope_dim, uint32_t pairing, uint32_t n_rot, const float2 *cs,
+                                            float (&e)[2 * PV], uint64_t kbase, const KvDev &kv, uint64_t v_off) {
+    if (hd >= nh1 + nh2) {  // V head (MODE 1 only)
+        if constexpr (MODE == 1) {
+            const uint32_t el = (hd - nh1 - nh2) * head_dim + it * 2 * PV;
+            if (kbase != ~0ull)
+                store_f32<C, 2 * PV>(reinterpret_cast<typename C::T *>(kv.arena + kbase + v_off) + el, e);
         }
         return;
     }
-    // Adjacent pairs; pairing 2 shifts the span to the tail of the head.
-    const uint32_t start = pairing == 2 ? head_dim - rope_dim : 0;
-    const uint32_t i0 = it * PV;  // first pair index
-    off_lo = start + 2 * i0;
-    off_hi = off_lo + PV;
-    float e[2 * PV];
-    load_f32<A, 2 * PV>(src + off_lo, e);
+    const bool second = hd >= nh1;
+    const uint32_t h = second ? hd - nh1 : hd;
+    const typename A::T *src = second ? x2 : x1;
+    typename A::T *dst = second ? out2 : out1;
+    const size_t base = (size_t)row * (second ? w2 : w1) + (size_t)h * head_dim;
+    uint32_t lo, hi;
+    item_offsets(it, n_rot, head_dim, rope_dim, pairing, PV, lo, hi);
+    if (it < n_rot) {
+        const uint32_t i0 = it * PV;
+        if (pairing == 1) {
 #pragma unroll
-    for (int k = 0; k < PV; ++k) {
-        const float2 sc = cs[i0 + k];
-        const float a = e[2 * k], b = e[2 * k + 1];
-        e[2 * k] = a * sc.y - b * sc.x;
-        e[2 * k + 1] = a * sc.x + b * sc.y;
+            for (int k = 0; k < PV; ++k) {
+                const float2 sc = cs[i0 + k];  // (sin, cos)
+                const float a = e[k], b = e[PV + k];
+                e[k] = a * sc.y - b * sc.x;
+                e[PV + k] = a * sc.x + b * sc.y;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < PV; ++k) {
+                const float2 sc = cs[i0 + k];
+                const float a = e[2 * k], b = e[2 * k + 1];
+                e[2 * k] = a * sc.y - b * sc.x;
+                e[2 * k + 1] = a * sc.x + b * sc.y;
+            }
+        }
     }
+    const bool write = dst && (dst != src || it < n_rot);
+    const bool cache = MODE == 1 && second && kbase != ~0ull;
+    if (hi == lo + PV) {
+        if (write) store_f32<A, 2 * PV>(dst + base + lo, e);
+        if constexpr (MODE == 1)
+            if (cache) store_cache<C, 2 * PV>(kv.arena, kbase, h * head_dim + lo, e);
+    } else {
+        float a[PV], b[PV];
 #pragma unroll
-    for (int k = 0; k < PV; ++k) {
-        lo[k] = e[k];
-        hi[k] = e[PV + k];
+        for (int k = 0; k < PV; ++k) {
+            a[k] = e[k];
+            b[k] = e[PV + k];
+        }
+        if (write) {
+            store_f32<A, PV>(dst + base + lo, a);
+            store_f32<A, PV>(dst + base + hi, b);
+        }
+        if constexpr (MODE == 1) {
+            if (cache) {
+                store_cache<C, PV>(kv.arena, kbase, h * head_dim + lo, a);
+                store_cache<C, PV>(kv.arena, kbase, h * head_dim + hi, b);
+            }
+        }
     }
 }
 
 // MODE 0: rotate x1 -> out1 and x2 -> out2.
 // MODE 1: additionally write rotated x2 (K) and x3 (V) into the paged cache
 //         (cache element type C).
-template <typename A, typename C, int PV, int MODE>
+// Each workgroup handles R consecutive rows: all threads first fill the
+// R x rope_dim/2 (sin, cos) table (one barrier), then stream every item of
+// the R rows.
+template <typename A, typename C, int PV, int MODE, int R>
 __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
     // x1/out1 and x2/out2 may alias (in-place rotation): no __restrict__.
     const typename A::T *x1, typename A::T *out1, uint32_t nh1,
     const typename A::T *x2, typename A::T *out2, uint32_t nh2,
-    const typename A::T *__restrict__ x3, uint32_t head_dim, uint32_t rope_dim, uint32_t pairing,
+    const typename A::T *__restrict__ x3, uint32_t rows, uint32_t head_dim, uint32_t rope_dim, uint32_t pairing,
     const float *__restrict__ inv_freqs, const uint32_t *__restrict__ rope_pos, uint32_t pos0,
     const uint32_t *__restrict__ kv_pos, KvDev kv, uint32_t *__restrict__ err) {
-    __shared__ float2 cs[kMaxHalf];
-    const uint32_t row = blockIdx.x;
-    uint32_t pos;
-    if constexpr (MODE == 1)
-        pos = rope_pos ? rope_pos[row] : kv_pos[row];
-    else
-        pos = rope_pos ? rope_pos[row] : pos0 + row;
+    __shared__ float2 cs_all[R][kMaxHalf / R];
+    __shared__ uint64_t kbase_all[R];
+    const uint32_t row0 = blockIdx.x * R;
     const uint32_t half = rope_dim / 2;
-    const float pf = (float)pos;
-    for (uint32_t i = threadIdx.x; i < half; i += kRopeBlock) {
-        const float theta = pf * inv_freqs[i];
-        double sd, cd;
-        sincos((double)theta, &sd, &cd);
-        cs[i] = make_float2((float)sd, (float)cd);
+    for (uint32_t t = threadIdx.x; t < R * half; t += kRopeBlock) {
+        const uint32_t rr = t / half, i = t % half;
+        const uint32_t row = row0 + rr;
+        if (row >= rows) continue;
+        uint32_t pos;
+        if constexpr (MODE == 1)
+            pos = rope_pos ? rope_pos[row] : kv_pos[row];
+        else
+            pos = rope_pos ? rope_pos[row] : pos0 + row;
+        const float theta = (float)pos * inv_freqs[i];
+        if constexpr (FELLM_ROPE_DOUBLE_TRIG) {
+            double sd, cd;
+            sincos((double)theta, &sd, &cd);
+            cs_all[rr][i] = make_float2((float)sd, (float)cd);
+        } else {
+            float sf, cf;
+            sincosf(theta, &sf, &cf);
+            cs_all[rr][i] = make_float2(sf, cf);
+        }
     }
-    uint64_t kbase = ~0ull;
     if constexpr (MODE == 1) {
-        kbase = kv_slot_offset(kv, row, kv_pos[row]);
-        if (kbase == ~0ull && threadIdx.x == 0 && err) atomicOr(err, 1u);
+        if (threadIdx.x < R) {
+            const uint32_t row = row0 + threadIdx.x;
+            uint64_t kb = ~0ull;
+            if (row < rows) {
+                kb = kv_slot_offset(kv, row, kv_pos[row]);
+                if (kb == ~0ull && err) atomicOr(err, 1u);
+            }
+            kbase_all[threadIdx.x] = kb;
+        }
     }
     __syncthreads();
 
-    const uint32_t n_rot = half / PV;  // rotated items of PV pairs
-    const uint32_t items_head = head_dim / (2 * PV);             // all items of a head
-    const uint32_t items1 = nh1 * items_head;
-    const uint32_t items2 = x2 ? nh2 * items_head : 0;
-    const uint32_t items3 = (MODE == 1) ? nh2 * items_head : 0;
-    const uint32_t total = items1 + items2 + items3;
+    const uint32_t n_rot = half / PV;                // rotated items of PV pairs
+    const uint32_t items_head = head_dim / (2 * PV);  // all items of a head
+    const uint32_t nh_x2 = x2 ? nh2 : 0;
+    const uint32_t nh_v = (MODE == 1) ? nh2 : 0;
+    const uint32_t heads = nh1 + nh_x2 + nh_v;       // q heads, k heads, v heads
     const size_t w1 = (size_t)nh1 * head_dim, w2 = (size_t)nh2 * head_dim;
     const uint64_t v_off = (uint64_t)kv.block_size * kv.stride * 2;
+    const uint32_t nrows = rows - row0 < (uint32_t)R ? rows - row0 : (uint32_t)R;
 
-    for (uint32_t u = threadIdx.x; u < total; u += kRopeBlock) {
-        float lo[PV], hi[PV];
-        uint32_t off_lo, off_hi;
-        if (u < items1) {
-            const uint32_t hd = u / items_head, it = u % items_head;
-            const size_t base = (size_t)row * w1 + (size_t)hd * head_dim;
-            rope_item<A, PV>(x1 + base, it, n_rot, head_dim, rope_dim, pairing, cs, lo, hi, off_lo, off_hi);
-            if (out1 != x1 || it < n_rot) {
-                store_f32<A, PV>(out1 + base + off_lo, lo);
-                store_f32<A, PV>(out1 + base + off_hi, hi);
-            }
-        } else if (u < items1 + items2) {
-            const uint32_t v = u - items1;
-            const uint32_t hd = v / items_head, it = v % items_head;
-            const size_t base = (size_t)row * w2 + (size_t)hd * head_dim;
-            rope_item<A, PV>(x2 + base, it, n_rot, head_dim, rope_dim, pairing, cs, lo, hi, off_lo, off_hi);
-            if (out2 && (out2 != x2 || it < n_rot)) {
-                store_f32<A, PV>(out2 + base + off_lo, lo);
-                store_f32<A, PV>(out2 + base + off_hi, hi);
-            }
-            if constexpr (MODE == 1) {
-                if (kbase != ~0ull) {
-                    const uint32_t e = hd * head_dim;
-                    store_cache<C, PV>(kv.arena, kbase, e + off_lo, lo);
-                    store_cache<C, PV>(kv.arena, kbase, e + off_hi, hi);
+    // When items_head divides the block (head_dim a power of two), each thread
+    // keeps one item position `it` and walks (row, head) slots with a fixed
+    // step, U slots per batch: all U loads are issued before any rotation or
+    // store, so each thread keeps U 16-byte requests in flight.  Other shapes
+    // enumerate items one by one with divisions.
+    const bool fixed_item = items_head <= kRopeBlock && kRopeBlock % items_head == 0;
+    const uint32_t total_slots = nrows * heads;
+    if (fixed_item) {
+        const uint32_t it = threadIdx.x % items_head;
+        const uint32_t step = kRopeBlock / items_head;
+        uint32_t slot = threadIdx.x / items_head;
+        uint32_t rr = slot / heads, hd = slot % heads;
+        for (; slot < total_slots; slot += step * FELLM_ROPE_UNROLL) {
+            uint32_t srr[FELLM_ROPE_UNROLL], shd[FELLM_ROPE_UNROLL];
+            float e[FELLM_ROPE_UNROLL][2 * PV];
+#pragma unroll
+            for (int uu = 0; uu < FELLM_ROPE_UNROLL; ++uu) {
+                srr[uu] = rr;
+                shd[uu] = hd;
+                if (slot + uu * step < total_slots)
+                    rope_load<A, PV>(x1, x2, x3, nh1, nh_x2, w1, w2, row0 + rr, hd, it, head_dim, rope_dim, pairing, n_rot,
+                                     e[uu]);
+                hd += step;
+                while (hd >= heads) {
+                    hd -= heads;
+                    ++rr;
                 }
             }
-        } else if constexpr (MODE == 1) {
-            // V row: 2*PV consecutive elements per item, converted to the cache dtype.
-            const uint32_t v = u - items1 - items2;
-            const uint32_t e = v * 2 * PV;
-            float vals[2 * PV];
-            load_f32<A, 2 * PV>(x3 + (size_t)row * w2 + e, vals);
-            if (kbase != ~0ull)
-                store_f32<C, 2 * PV>(reinterpret_cast<typename C::T *>(kv.arena + kbase + v_off) + e, vals);
+#pragma unroll
+            for (int uu = 0; uu < FELLM_ROPE_UNROLL; ++uu) {
+                if (slot + uu * step < total_slots)
+                    rope_finish<A, C, PV, MODE>(x1, out1, x2, out2, nh1, nh_x2, w1, w2, row0 + srr[uu], shd[uu], it,
+                                                head_dim, rope_dim, pairing, n_rot, cs_all[srr[uu]], e[uu],
+                                                kbase_all[srr[uu]], kv, v_off);
+            }
+        }
+    } else {
+        for (uint32_t t = threadIdx.x; t < total_slots * items_head; t += kRopeBlock) {
+            const uint32_t it = t % items_head, slot = t / items_head;
+            const uint32_t rr = slot / heads, hd = slot % heads;
+            float e[2 * PV];
+            rope_load<A, PV>(x1, x2, x3, nh1, nh_x2, w1, w2, row0 + rr, hd, it, head_dim, rope_dim, pairing, n_rot, e);
+            rope_finish<A, C, PV, MODE>(x1, out1, x2, out2, nh1, nh_x2, w1, w2, row0 + rr, hd, it, head_dim, rope_dim,
+                                        pairing, n_rot, cs_all[rr], e, kbase_all[rr], kv, v_off);
         }
     }
+}
+
+// Rows per workgroup: enough workgroups to fill 256 CUs several times over,
+// and R * rope_dim/2 sin/cos pairs within the LDS table.
+inline int rope_rows_per_block(uint32_t rows, uint32_t rope_dim) {
+    const uint32_t half = rope_dim / 2;
+    if (rows >= 4096 && half <= kMaxHalf / 4) return 4;
+    if (rows >= 2048 && half <= kMaxHalf / 2) return 2;
+    return 1;
 }
 
 // Standalone KvWrite: one workgroup per batch row, items of VEC elements.
@@ -266,14 +379,20 @@ extern "C" int fellm_rocm_rope(const void *x1, void *out1, uint32_t n_heads1, co
     return dispatch_act(act_dtype, [&]<typename A>() -> int {
         using T = typename A::T;
         const bool vec = rope_vec_ok(head_dim, rope_dim, pairing, sizeof(T), {x1, out1, x2, out2});
-        auto go = [&]<int PV>() {
-            hipLaunchKernelGGL((rope_kernel<A, F16, PV, 0>), dim3(rows), dim3(kRopeBlock), 0, s, (const T *)x1,
-                               (T *)out1, n_heads1, (const T *)x2, (T *)out2, x2 ? n_heads2 : 0, nullptr,
-                               head_dim, rope_dim, pairing, inv_freqs, positions, position0, nullptr, KvDev{},
-                               nullptr);
+        const int R = rope_rows_per_block(rows, rope_dim);
+        auto go = [&]<int PV, int RR>() {
+            hipLaunchKernelGGL((rope_kernel<A, F16, PV, 0, RR>), dim3((rows + RR - 1) / RR), dim3(kRopeBlock), 0, s,
+                               (const T *)x1, (T *)out1, n_heads1, (const T *)x2, (T *)out2, x2 ? n_heads2 : 0,
+                               nullptr, rows, head_dim, rope_dim, pairing, inv_freqs, positions, position0, nullptr,
+                               KvDev{}, nullptr);
             return launch_status();
         };
-        return vec ? go.template operator()<4>() : go.template operator()<1>();
+        auto go_r = [&]<int PV>() {
+            if (R == 4) return go.template operator()<PV, 4>();
+            if (R == 2) return go.template operator()<PV, 2>();
+            return go.template operator()<PV, 1>();
+        };
+        return vec ? go_r.template operator()<4>() : go_r.template operator()<1>();
     });
 }
 
@@ -323,8 +442,8 @@ extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q
             const bool vec = rope_vec_ok(head_dim, rope_dim, pairing, sizeof(T), {q, q_out, k, k_out, v}) &&
                              aligned_to(kvp->arena, 16) && kv.block_bytes % 16 == 0;
             auto go = [&]<int PV>() {
-                hipLaunchKernelGGL((rope_kernel<A, C, PV, 1>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)q,
-                                   (T *)q_out, n_q_heads, (const T *)k, (T *)k_out, n_kv_heads, (const T *)v,
+                hipLaunchKernelGGL((rope_kernel<A, C, PV, 1, 1>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)q,
+                                   (T *)q_out, n_q_heads, (const T *)k, (T *)k_out, n_kv_heads, (const T *)v, batch,
                                    head_dim, rope_dim, pairing, inv_freqs, rope_positions, 0u, kv_positions, kv,
                                    err_flag);
                 return launch_status();

@@ -355,3 +355,19 @@ def test_router_topk(ops, dev, n_exp, k, gating, norm, rsf):
                              routed_scaling_factor=rsf)
     assert_exact(from_dev(ids), ids_ref, "ids")
     assert_exact(from_dev(w), w_ref, "weights")
+
+
+@pytest.mark.parametrize("rows", [2051, 4099])
+def test_rope_many_rows(ops, dev, rows):
+    """Row counts that select 2 and 4 rows per workgroup, with a ragged tail."""
+    rng = np.random.default_rng(rows)
+    nq, nk, hd = 2, 1, 64
+    inv = oracle.rope_inv_freqs(10000.0, hd)
+    q = rng.normal(size=(rows, nq * hd)).astype(np.float32)
+    k = rng.normal(size=(rows, nk * hd)).astype(np.float32)
+    qr = oracle.rope(q, nq, hd, hd, 1, inv, None, position0=3)
+    kr = oracle.rope(k, nk, hd, hd, 1, inv, None, position0=3)
+    qo, ko = ops.rope(torch.from_numpy(q).to(dev), torch.from_numpy(inv).to(dev), head_dim=hd, pairing=1,
+                      position0=3, x2=torch.from_numpy(k).to(dev))
+    assert_rope_close(from_dev(qo), qr, pair_magnitude(q, nq, hd, hd, 1), "f32", "q")
+    assert_rope_close(from_dev(ko), kr, pair_magnitude(k, nk, hd, hd, 1), "f32", "k")
