@@ -616,12 +616,13 @@ int launch_router_topk(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint
     });
 }
 
-// Cast [x f32] -> host f32: materialise a device-valid mirror into host
-// storage (launchers.rs:140-170).
+// Cast [x] -> host x of the same dtype: materialise a device-valid mirror into
+// host storage (launchers.rs:140-170).
 int launch_materialize(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
                        uint32_t n_out, FellmStreamHandle) {
     return guarded(attrs, in, n_in, out, n_out, 1, 1, false, [&](State &st) {
         if (in[0].byte_len != out[0].byte_len || !out[0].data) fail(FELLM_ERR_SHAPE);
+        if (in[0].dtype != out[0].dtype) fail(FELLM_ERR_DTYPE);
         void *src = ensure_input(st, in[0]);
         hip_check(hipMemcpyAsync(out[0].data, src, out[0].byte_len, hipMemcpyDeviceToHost, stream_locked(st)));
         hip_check(hipStreamSynchronize(stream_locked(st)), FELLM_ERR_ALLOC);
@@ -682,6 +683,10 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
         const R regs[] = {
             // Reference keys (plugins/cuda_kernels/src/lib.rs:337-720).
             {FELLM_OP_CAST, {F32}, F32, launch_materialize},
+            // Same-dtype Cast = materialise a device-valid mirror into host memory.
+            {FELLM_OP_CAST, {F16}, F16, launch_materialize},
+            {FELLM_OP_CAST, {BF16}, BF16, launch_materialize},
+            {FELLM_OP_CAST, {U32}, U32, launch_materialize},
             {FELLM_OP_RMSNORM, {F32, F32}, F32, launch_rmsnorm},
             {FELLM_OP_SILU_GATE, {F32, F32}, F32, launch_silu_gate},
             {FELLM_OP_ROPE, {F32, F32}, F32, launch_rope},

@@ -1,0 +1,293 @@
+"""GPU tests through the plugin C ABI with host buffers, as FeLLM's plugin host
+drives it (crates/fellm-plugin-host/tests/load_cuda_kernels.rs pattern):
+dlopen + ABI check + registration, then registry launches with TensorRef /
+TensorMut over host memory.  Outputs stay device-valid; a same-dtype Cast
+launch materialises them into host memory (launchers.rs:140-170).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")  # load torch's HIP runtime before the plugin
+
+import oracle  # noqa: E402
+from fellm_amd import abi, synth  # noqa: E402
+from fellm_amd.plugin_host import PagedKvContext, PluginHost  # noqa: E402
+from parity_util import assert_close, assert_exact, assert_rope_close, ordered16, pair_magnitude  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+D = abi.DType
+
+
+@pytest.fixture(scope="module")
+def host():
+    torch.cuda.init()
+    h = PluginHost()
+    yield h
+    h.set_paged_context(None)
+
+
+# The plugin keys device mirrors by (host pointer, byte length), like the
+# reference (plugins/cuda_kernels/src/buffers.rs:341-394): a freed host buffer
+# whose address numpy hands out again would alias a stale mirror.  FeLLM's host
+# owns long-lived buffers and invalidates after CPU writes; these tests keep
+# every host buffer alive for the module instead.
+_KEEP = []
+
+
+def tref(a: np.ndarray, dt, dims=None, logical_id=0):
+    _KEEP.append(a)
+    return abi.tensor_ref(a.ctypes.data, a.nbytes, dt, dims or [a.size], logical_id)
+
+
+def tmut(a: np.ndarray, dt, dims=None):
+    _KEEP.append(a)
+    return abi.tensor_mut(a.ctypes.data, a.nbytes, dt, dims or [a.size])
+
+
+def run(host, op, ins_dt, out_dt, attrs, ins, outs):
+    h = host.lookup(op, ins_dt, out_dt)
+    assert h is not None, (op, ins_dt, out_dt)
+    host.launch(h, attrs, ins, outs)
+
+
+def materialize(host, buf: np.ndarray, dt):
+    """Cast launch: copy buf's device mirror into a fresh host array."""
+    out = np.empty_like(buf)
+    run(host, abi.OpKind.CAST, [dt], dt, abi.OpAttrs(), [tref(buf, dt)], [tmut(out, dt)])
+    return out
+
+
+def test_rmsnorm_f32(host):
+    rng = np.random.default_rng(0)
+    x = rng.normal(size=(64, 2048)).astype(np.float32)
+    w = rng.normal(1, 0.1, 2048).astype(np.float32)
+    y = np.zeros_like(x)
+    run(host, abi.OpKind.RMSNORM, [D.F32, D.F32], D.F32, abi.OpAttrs(eps=1e-5),
+        [tref(x, D.F32, [64, 2048]), tref(w, D.F32, logical_id=101)], [tmut(y, D.F32, [64, 2048])])
+    got = materialize(host, y, D.F32)
+    assert_close(got, oracle.rmsnorm(x, w, 1e-5), "f32", what="plugin rmsnorm")
+
+
+def test_silu_gate_f16_and_chain_stays_on_device(host):
+    rng = np.random.default_rng(1)
+    g = rng.normal(size=4096).astype(np.float16)
+    u = rng.normal(size=4096).astype(np.float16)
+    a = np.zeros(4096, np.float16)
+    b = np.zeros(4096, np.float16)
+    sg = (abi.OpKind.SILU_GATE, [D.F16, D.F16], D.F16)
+    run(host, *sg, abi.OpAttrs(), [tref(g, D.F16), tref(u, D.F16)], [tmut(a, D.F16)])
+    # `a` is only device-valid: feeding it back must use the device copy, not the zero host bytes
+    run(host, *sg, abi.OpAttrs(), [tref(a, D.F16), tref(u, D.F16)], [tmut(b, D.F16)])
+    ref_a = oracle.narrow(oracle.silu_gate(g.astype(np.float32), u.astype(np.float32)), "f16")
+    ref_b = oracle.narrow(oracle.silu_gate(oracle.widen(ref_a, "f16"), u.astype(np.float32)), "f16")
+    assert np.all(a == 0), "host copy of a device-valid output must not be written without a Cast"
+    assert_exact(materialize(host, b, D.F16).view(np.uint16), ref_b, "chained silu")
+
+
+def test_invalidate_refreshes_mirror(host):
+    x = np.ones(1024, np.float32)
+    z = np.zeros(1024, np.float32)
+    out = np.zeros(1024, np.float32)
+    add = (abi.OpKind.ADD, [D.F32, D.F32], D.F32)
+    run(host, *add, abi.OpAttrs(), [tref(x, D.F32), tref(z, D.F32)], [tmut(out, D.F32)])
+    x[:] = 5.0  # host write; the device mirror is now stale
+    run(host, *add, abi.OpAttrs(), [tref(x, D.F32), tref(z, D.F32)], [tmut(out, D.F32)])
+    assert np.all(materialize(host, out, D.F32) == 1.0)  # mirror reused, as in the reference cache
+    host.invalidate(x.ctypes.data, x.nbytes)
+    run(host, *add, abi.OpAttrs(), [tref(x, D.F32), tref(z, D.F32)], [tmut(out, D.F32)])
+    assert np.all(materialize(host, out, D.F32) == 5.0)
+
+
+def test_register_device_tensor(host):
+    dev = torch.arange(256, dtype=torch.float32, device="cuda")
+    shadow = np.zeros(256, np.float32)  # host view that is never read
+    _KEEP.append((dev, shadow))  # the binding lives as long as the plugin
+    assert host.register_device_tensor(shadow.ctypes.data, shadow.nbytes, dev.data_ptr()) == 0
+    ones = np.ones(256, np.float32)
+    out = np.zeros(256, np.float32)
+    run(host, abi.OpKind.ADD, [D.F32, D.F32], D.F32, abi.OpAttrs(), [tref(shadow, D.F32), tref(ones, D.F32)],
+        [tmut(out, D.F32)])
+    assert np.array_equal(materialize(host, out, D.F32), np.arange(256, dtype=np.float32) + 1)
+
+
+@pytest.mark.parametrize("qt,out_dt", [(D.Q4K, D.F32), (D.Q6K, D.F16), (D.Q4K, D.F16)])
+def test_embedding_quant(host, qt, out_dt):
+    rng = np.random.default_rng(int(qt) + int(out_dt))
+    vocab, dim = 200, 1024
+    table = synth.q4k_table(rng, vocab, dim) if qt == D.Q4K else synth.q6k_table(rng, vocab, dim)
+    ids = rng.integers(0, vocab, size=50, dtype=np.uint32)
+    out = np.zeros((50, dim), np.float32 if out_dt == D.F32 else np.float16)
+    run(host, abi.OpKind.EMBEDDING, [qt, D.U32], out_dt, abi.OpAttrs(),
+        [tref(table, qt, [vocab, dim], logical_id=2000 + int(qt) * 10 + int(out_dt)), tref(ids, D.U32)],
+        [tmut(out, out_dt, [50, dim])])
+    got = materialize(host, out, out_dt)
+    ref = oracle.embedding(table, int(qt), vocab, dim, ids)
+    if out_dt == D.F32:
+        assert_exact(got, ref, "plugin q-embedding")
+    else:
+        assert_exact(got.view(np.uint16), oracle.narrow(ref, "f16"), "plugin q-embedding f16")
+
+
+def test_embedding_weight_cached_by_logical_id(host):
+    vocab, dim = 16, 64
+    t = np.full((vocab, dim), 2.0, np.float32)
+    ids = np.array([3], np.uint32)
+    out = np.zeros((1, dim), np.float32)
+    key = (abi.OpKind.EMBEDDING, [D.F32, D.U32], D.F32)
+    run(host, *key, abi.OpAttrs(), [tref(t, D.F32, [vocab, dim], logical_id=777), tref(ids, D.U32)],
+        [tmut(out, D.F32, [1, dim])])
+    t[:] = 9.0  # weights are immutable per logical id: no re-upload
+    run(host, *key, abi.OpAttrs(), [tref(t, D.F32, [vocab, dim], logical_id=777), tref(ids, D.U32)],
+        [tmut(out, D.F32, [1, dim])])
+    assert np.all(materialize(host, out, D.F32) == 2.0)
+
+
+def _paged(rng, batch, nkv, hd, n_blocks, bs, max_pos, kv_dtype):
+    stride = nkv * hd
+    kv_pos, table, n_logical = synth.paged_layout(rng, batch, n_blocks, bs, max_pos)
+    bb = (2 * bs * stride * 2 + 63) // 64 * 64
+    arena = torch.zeros(n_blocks * bb, dtype=torch.uint8, device="cuda")
+    host_arena = np.zeros(8, np.uint8)  # host mirror unused by the ROCm path
+    rope_pos = (kv_pos + 3).astype(np.uint32)
+    ctx = PagedKvContext(arena_ptr=host_arena.ctypes.data, arena_len=host_arena.size, block_table=table,
+                         n_logical_blocks=n_logical, n_layers=1, tokens_stride=stride, block_bytes=bb,
+                         block_size=bs, row_positions=kv_pos, row_rope_positions=rope_pos,
+                         device_arena_ptr=arena.data_ptr(), device_arena_len=arena.numel())
+    ctx._keep = (host_arena,)
+    return ctx, arena, kv_pos, rope_pos, table, n_logical, bb, stride
+
+
+def test_rope_uses_paged_row_positions(host):
+    rng = np.random.default_rng(3)
+    batch, nh, hd = 6, 4, 64
+    ctx, arena, kv_pos, rope_pos, *_ = _paged(rng, batch, 1, hd, 16, 16, 256, "f16")
+    host.set_paged_context(ctx)
+    try:
+        x = rng.normal(size=(batch, nh * hd)).astype(np.float32)
+        inv = oracle.rope_inv_freqs(500000.0, hd)
+        y = np.zeros_like(x)
+        run(host, abi.OpKind.ROPE, [D.F32, D.F32], D.F32,
+            abi.OpAttrs(n_heads=nh, head_dim=hd, rope_dim=hd, rope_pairing=0, position=99),
+            [tref(x, D.F32), tref(inv, D.F32)], [tmut(y, D.F32)])
+        got = materialize(host, y, D.F32)
+        ref = oracle.rope(x, nh, hd, hd, 0, inv, rope_pos)
+        assert_rope_close(got, ref, pair_magnitude(x, nh, hd, hd, 0), "f32", "plugin rope paged")
+    finally:
+        host.set_paged_context(None)
+    # without a paged context: attrs.position + row
+    x = rng.normal(size=(3, nh * hd)).astype(np.float32)
+    y = np.zeros_like(x)
+    run(host, abi.OpKind.ROPE, [D.F32, D.F32], D.F32, abi.OpAttrs(n_heads=nh, head_dim=hd, rope_dim=hd, position=40),
+        [tref(x, D.F32), tref(inv, D.F32)], [tmut(y, D.F32)])
+    assert_rope_close(materialize(host, y, D.F32), oracle.rope(x, nh, hd, hd, 0, inv, None, position0=40),
+                      pair_magnitude(x, nh, hd, hd, 0), "f32", "plugin rope pos0")
+
+
+def test_kv_write_paged(host):
+    rng = np.random.default_rng(4)
+    batch, nkv, hd, bs, n_blocks = 9, 2, 64, 16, 32
+    ctx, arena, kv_pos, _, table, n_logical, bb, stride = _paged(rng, batch, nkv, hd, n_blocks, bs, 500, "f16")
+    host.set_paged_context(ctx)
+    try:
+        rows = rng.normal(size=(batch, stride)).astype(np.float32)
+        cache_view = np.zeros(4, np.float32)
+        for slot in (0, 1):
+            run(host, abi.OpKind.KV_WRITE, [D.F32, D.F32], D.F32,
+                abi.OpAttrs(block_size=bs, kv_slot=slot, layer_ord=0), [tref(rows, D.F32)],
+                [tmut(cache_view, D.F32)])
+        torch.cuda.synchronize()
+        ref = np.zeros(arena.numel(), np.uint8)
+        for slot in (0, 1):
+            oracle.kv_write_paged(rows, stride, kv_pos, table, n_logical, 1, 0, bs, bb, ref, bool(slot))
+        assert_exact(arena.cpu().numpy(), ref, "plugin paged kv")
+    finally:
+        host.set_paged_context(None)
+
+
+def test_kv_write_contiguous(host):
+    row = np.arange(32, dtype=np.float32)
+    cache = np.full((8, 32), -1.0, np.float32)
+    run(host, abi.OpKind.KV_WRITE, [D.F32, D.F32], D.F32, abi.OpAttrs(position=5),
+        [tref(row, D.F32)], [tmut(cache, D.F32, [8, 32])])
+    got = materialize(host, cache, D.F32)
+    want = np.full((8, 32), -1.0, np.float32)
+    want[5] = row
+    assert np.array_equal(got, want)
+
+
+def test_custom_add_rmsnorm_f16(host):
+    rng = np.random.default_rng(5)
+    x = rng.normal(size=(33, 4096)).astype(np.float16)
+    r = (2 * rng.normal(size=(33, 4096))).astype(np.float16)
+    w = rng.normal(1, 0.1, 4096).astype(np.float32)
+    h = np.zeros_like(x)
+    y = np.zeros_like(x)
+    run(host, abi.OP_ADD_RMSNORM, [D.F16, D.F16, D.F32], D.F16, abi.OpAttrs(eps=1e-5),
+        [tref(x, D.F16), tref(r, D.F16), tref(w, D.F32)], [tmut(h, D.F16), tmut(y, D.F16)])
+    h_ref, y_ref = oracle.add_rmsnorm(x.view(np.uint16), r.view(np.uint16), w, 1e-5, "f16")
+    assert_exact(materialize(host, h, D.F16).view(np.uint16), h_ref, "plugin h")
+    assert_close(materialize(host, y, D.F16).view(np.uint16), y_ref, "f16", what="plugin y")
+
+
+def test_custom_router(host):
+    rng = np.random.default_rng(6)
+    logits = rng.normal(size=(300, 128)).astype(np.float32)
+    ids = np.zeros((300, 8), np.uint32)
+    w = np.zeros((300, 8), np.float32)
+    run(host, abi.OP_ROUTER_TOPK, [D.F32], D.U32,
+        abi.OpAttrs(n_experts=128, n_expert_used=8, expert_gating_func=1, norm_topk_prob=1),
+        [tref(logits, D.F32)], [tmut(ids, D.U32), tmut(w, D.F32)])
+    ids_r, w_r = oracle.router(logits, 8, 1, True, 0.0)
+    assert_exact(materialize(host, ids, D.U32), ids_r, "plugin router ids")
+    assert_exact(materialize(host, w, D.F32), w_r, "plugin router weights")
+
+
+def test_custom_rope_kv_write_bf16(host):
+    rng = np.random.default_rng(7)
+    batch, nq, nkv, hd, bs, n_blocks = 12, 8, 2, 128, 16, 64
+    ctx, arena, kv_pos, rope_pos, table, n_logical, bb, stride = _paged(rng, batch, nkv, hd, n_blocks, bs, 900,
+                                                                         "bf16")
+    host.set_paged_context(ctx)
+    try:
+        bits = lambda a: oracle.f32_to_bf16_bits(a)
+        q = bits(rng.normal(size=(batch, nq * hd)).astype(np.float32))
+        k = bits(rng.normal(size=(batch, stride)).astype(np.float32))
+        v = bits(rng.normal(size=(batch, stride)).astype(np.float32))
+        inv = oracle.rope_inv_freqs(500000.0, hd)
+        qo = np.zeros_like(q)
+        run(host, abi.OP_ROPE_KV_WRITE, [D.BF16, D.BF16, D.BF16, D.F32], D.BF16,
+            abi.OpAttrs(n_heads=nq, n_kv_heads=nkv, head_dim=hd, rope_dim=hd, rope_pairing=0, layer_ord=0,
+                        cast_to=int(D.BF16), block_size=bs),
+            [tref(q, D.BF16), tref(k, D.BF16), tref(v, D.BF16), tref(inv, D.F32)], [tmut(qo, D.BF16)])
+        qf = oracle.widen(q, "bf16")
+        q_ref = oracle.narrow(oracle.rope(qf, nq, hd, hd, 0, inv, rope_pos), "bf16")
+        assert_rope_close(materialize(host, qo, D.BF16), q_ref, pair_magnitude(qf, nq, hd, hd, 0), "bf16", "q")
+        torch.cuda.synchronize()
+        ref = np.zeros(arena.numel(), np.uint8)
+        oracle.kv_write_paged(oracle.widen(v, "bf16"), stride, kv_pos, table, n_logical, 1, 0, bs, bb, ref, True,
+                              "bf16")
+        got = arena.cpu().numpy()
+        for b in range(batch):
+            vb = table[kv_pos[b] // bs] * bb + bs * stride * 2 + (kv_pos[b] % bs) * stride * 2
+            assert_exact(got[vb:vb + stride * 2], ref[vb:vb + stride * 2], f"V row {b}")
+    finally:
+        host.set_paged_context(None)
+
+
+def test_custom_embedding_rmsnorm(host):
+    rng = np.random.default_rng(8)
+    vocab, dim = 100, 3584
+    table = synth.q4k_table(rng, vocab, dim)
+    ids = synth.zipf_ids(rng, 64, vocab)
+    w = rng.normal(1, 0.1, dim).astype(np.float32)
+    h = np.zeros((64, dim), np.float16)
+    y = np.zeros((64, dim), np.float16)
+    run(host, abi.OP_EMBEDDING_RMSNORM, [D.Q4K, D.U32, D.F32], D.F16, abi.OpAttrs(eps=1e-6),
+        [tref(table, D.Q4K, [vocab, dim], logical_id=4242), tref(ids, D.U32), tref(w, D.F32)],
+        [tmut(h, D.F16, [64, dim]), tmut(y, D.F16, [64, dim])])
+    e = oracle.embedding(table, 12, vocab, dim, ids)
+    assert_exact(materialize(host, h, D.F16).view(np.uint16), oracle.narrow(e, "f16"), "fused h")
+    assert_close(materialize(host, y, D.F16).view(np.uint16), oracle.narrow(oracle.rmsnorm(e, w, 1e-6), "f16"),
+                 "f16", what="fused y")
