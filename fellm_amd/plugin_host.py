@@ -85,6 +85,30 @@ class KernelRegistry:
         return None
 
 
+def validate_manifest(m: dict) -> None:
+    """V1 manifest rules of crates/fellm-plugin-host/src/manifest.rs:110-165."""
+    schema = m.get("schema", m.get("schema_version"))
+    if schema is None:
+        raise PluginError("plugin manifest is missing schema/schema_version")
+    if "schema" in m and "schema_version" in m and m["schema"] != m["schema_version"]:
+        raise PluginError("plugin manifest schema fields disagree")
+    if schema != 1:
+        raise PluginError(f"unsupported plugin manifest schema {schema}")
+    if not str(m.get("id", "")).strip():
+        raise PluginError("plugin manifest id is empty")
+    if not str(m.get("version", "")).strip():
+        raise PluginError("plugin has an empty version")
+    provides = m.get("provides") or []
+    if not provides:
+        raise PluginError("plugin declares no provided components")
+    for c in provides:
+        kind = c.get("type")
+        if kind in ("backend", "architecture", "capability", "capabilities") and not c.get("id"):
+            raise PluginError(f"component {kind} is missing id")
+        if kind in ("kernels", "kernel-provider") and not (c.get("id") or c.get("backend")):
+            raise PluginError("kernels component needs id or backend")
+
+
 class PluginHost:
     """Loads one kernel plugin and launches its ops."""
 
@@ -152,7 +176,9 @@ class PluginHost:
         raw = fn()
         if not raw.ptr or raw.len == 0:
             raise PluginError("empty plugin manifest")
-        return json.loads(C.string_at(raw.ptr, raw.len).decode())
+        manifest = json.loads(C.string_at(raw.ptr, raw.len).decode())
+        validate_manifest(manifest)
+        return manifest
 
     def _register(self, _registry, reg_ptr) -> int:
         return self.registry.register(reg_ptr.contents)

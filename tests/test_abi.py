@@ -83,6 +83,17 @@ def host():
     h.shutdown()
 
 
+def test_manifest_validation_rules():
+    from fellm_amd.plugin_host import PluginError, validate_manifest
+
+    good = {"schema": 1, "id": "x", "version": "1", "provides": [{"type": "kernels", "backend": "rocm"}]}
+    validate_manifest(good)
+    for bad in ({**good, "schema": 2}, {**good, "id": " "}, {**good, "version": ""}, {**good, "provides": []},
+                {**good, "provides": [{"type": "backend"}]}, {**good, "schema_version": 3}):
+        with pytest.raises(PluginError):
+            validate_manifest(bad)
+
+
 def test_plugin_activation(host):
     assert host.manifest["schema"] == 1
     assert host.manifest["id"] == "fellm.rocm"
