@@ -10,10 +10,11 @@ One step = one pass of the four kernels over one batch of synthetic inputs
 already resident in HBM.  Three input sets rotate between steps (> 1.8 GB
 touched per rotation) so the 256 MB MALL cannot serve repeated reads.
 
-Per-op kernel time comes from HIP events recorded on the stream the kernels
-run on; achieved GB/s = algorithmic bytes / kernel time (bytes each op must
-read and write once).  `value` = tokens per second of the whole timed
-region (wall clock, K steps).  The CPU baseline times the C restatement of
+`value` = tokens per second over K uninstrumented steps (wall clock between
+two synchronisations).  Per-op kernel time comes from a second pass of K steps
+with HIP events recorded around each launch on the stream the kernels run on;
+achieved GB/s = algorithmic bytes / kernel time (bytes each op must read and
+write once).  The CPU baseline times the C restatement of
 backend-cpu (oracle/, 1 thread) on a bounded sample of the same chain.
 
 --suite measures every BASELINE config's ops (per-op GB/s table) instead.
@@ -221,15 +222,27 @@ def c5_ops(torch, ops, dev, n_sets, seed=5):
 # Timing
 # --------------------------------------------------------------------------- #
 def run_chain(torch, chain, sets, steps, warmup):
+    """Two timed passes over `steps` steps of the chain.
+
+    Pass 1 (whole job): no instrumentation, wall clock between two device
+    synchronisations -> elapsed seconds.  Pass 2 (per op): a HIP event pair
+    around every launch on the launch stream -> per-op kernel times.  Event
+    records between launches cost ~1-3 us each, so they stay out of pass 1.
+    """
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         for op in chain:
             op.fn(sets[i % len(sets)])
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        s = sets[i % len(sets)]
+        for op in chain:
+            op.fn(s)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in chain]
           for _ in range(steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for i in range(steps):
         s = sets[i % len(sets)]
         for j, op in enumerate(chain):
@@ -237,7 +250,6 @@ def run_chain(torch, chain, sets, steps, warmup):
             op.fn(s)
             ev[i][j][1].record(stream)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
     per_op = []
     for j, op in enumerate(chain):
         ms = sorted(ev[i][j][0].elapsed_time(ev[i][j][1]) for i in range(steps))

@@ -151,6 +151,45 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
+// ---- DPP row permutes: intra-row data movement at VALU latency -------------
+// dpp_ctrl encodings (GCN/CDNA DPP): quad_perm [1,0,3,2] = 0xB1 (lane ^ 1),
+// quad_perm [2,3,0,1] = 0x4E (lane ^ 2), row_half_mirror = 0x141 (i <-> 7-i in
+// each half-row of 8), row_mirror = 0x140 (i <-> 15-i in each row of 16),
+// row_shr:1 = 0x111 (lane i reads lane i-1 of its row).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
+}
+
+// Max over aligned groups of G lanes (G = 1, 2, 4, 8 or 16); every lane of the
+// group gets the result.  Mirrors pair up halves, then quad xor 2 and xor 1.
+template <int G>
+__device__ __forceinline__ float group_max_f32(float v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "group size");
+    if constexpr (G >= 16) v = fmaxf(v, dpp_f32<0x140>(v));
+    if constexpr (G >= 8) v = fmaxf(v, dpp_f32<0x141>(v));
+    if constexpr (G >= 4) v = fmaxf(v, dpp_f32<0x4E>(v));
+    if constexpr (G >= 2) v = fmaxf(v, dpp_f32<0xB1>(v));
+    return v;
+}
+template <int G>
+__device__ __forceinline__ uint64_t group_max_u64(uint64_t v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "group size");
+    if constexpr (G >= 16) { const uint64_t o = dpp_u64<0x140>(v); v = o > v ? o : v; }
+    if constexpr (G >= 8) { const uint64_t o = dpp_u64<0x141>(v); v = o > v ? o : v; }
+    if constexpr (G >= 4) { const uint64_t o = dpp_u64<0x4E>(v); v = o > v ? o : v; }
+    if constexpr (G >= 2) { const uint64_t o = dpp_u64<0xB1>(v); v = o > v ? o : v; }
+    return v;
+}
+
 // Block-wide f32 sum; every thread gets the result.  `scratch` holds one
 // float per wave.  Contains __syncthreads, so all threads must call it.
 template <int BLOCK>

@@ -11,10 +11,10 @@
 //       routed_scaling_factor, 0 meaning 1)
 //   batched variant :820-855 (same ranking and arithmetic).
 //
-// One wavefront per token (n_experts <= 512: EPL experts per lane).  exp is
-// the glibc-exact restatement and the denominator is summed serially in
-// expert order by lane 0 (through LDS), so scores, ranking and weights are
-// bit-exact with the CPU.  Ranking uses 64-bit keys
+// A group of G lanes per token (n_experts <= 512, EPL experts per lane).  exp
+// is the glibc-exact restatement and the denominator is folded serially in
+// expert order lane to lane, so scores, ranking and weights are bit-exact with
+// the CPU.  Ranking uses 64-bit keys
 // (total-order(score) << 32 | ~expert): k wavefront max-reductions pick the
 // winners in rank order, ties resolved towards the lower expert id exactly as
 // the CPU's comparator does.
@@ -22,6 +22,11 @@
 
 namespace fellm {
 namespace {
+
+// Build knob: experts per lane in the grouped kernel (8, 16 or 32).
+#ifndef FELLM_ROUTER_EPL
+#define FELLM_ROUTER_EPL 16
+#endif
 
 constexpr int kRouterBlock = 256;
 constexpr int kRouterWaves = kRouterBlock / kWave;
@@ -37,90 +42,138 @@ __device__ __forceinline__ float total_order_inv(uint32_t o) {
     return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
 }
 
-template <int EPL>
-__global__ __launch_bounds__(kRouterBlock) void router_topk_kernel(
+// Grouped path: G = 64 / TPW lanes per token, each lane owning EPL
+// consecutive experts (expert e lives in lane e / EPL of its group, slot
+// e % EPL), so expert order is (lane, slot) order.
+//  * max: per-lane max, then an xor-shuffle reduction inside the group;
+//  * denominator: the f32 fold in expert order runs lane to lane through the
+//    group (lane q adds its EPL values to the running sum, then hands it to
+//    lane q+1), i.e. exactly the CPU's left-to-right accumulation;
+//  * top-k: k rounds; each lane scans its own candidates for the best
+//    (score desc, expert asc) key, the group takes the 64-bit max, the owner
+//    marks it taken.  Rank r's expert and raw score go straight to ids/weights
+//    and the rank-order sum is folded on the way; a final pass rescales.
+template <int EPL, int G>
+__global__ __launch_bounds__(kRouterBlock) void router_topk_grouped(
     const float *__restrict__ logits, uint32_t tokens, uint32_t n_exp, uint32_t k, uint32_t gating,
     uint32_t norm, float rsf, uint32_t *__restrict__ ids, float *__restrict__ weights) {
     __shared__ uint64_t tab_lds[32];
-    __shared__ float ex_lds[kRouterWaves][kMaxExperts];
-    __shared__ float denom_lds[kRouterWaves];
-    __shared__ uint64_t sel_lds[kRouterWaves][kMaxTopK];
     const uint64_t *tab = stage_expf_table(tab_lds);
-
-    const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t token = blockIdx.x * kRouterWaves + wave;
+    constexpr int TPW = kWave / G;  // tokens per wavefront
+    const uint32_t lane = threadIdx.x % kWave, sub = lane % G;
+    const uint32_t token = (blockIdx.x * kRouterWaves + threadIdx.x / kWave) * TPW + lane / G;
     const bool active = token < tokens;
     const float *lg = logits + (size_t)(active ? token : 0) * n_exp;
+    const uint32_t e0 = sub * EPL;
 
-    float l[EPL], s[EPL];
+    float s[EPL];
+    if (EPL % 4 == 0 && n_exp % EPL == 0 && (reinterpret_cast<uintptr_t>(lg) & 15) == 0) {
+        if (active && e0 < n_exp) {
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-        const uint32_t e = lane + kWave * j;
-        l[j] = (active && e < n_exp) ? lg[e] : -__builtin_inff();
+            for (int j = 0; j < EPL; j += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(lg + e0 + j);
+                s[j] = v.x;
+                s[j + 1] = v.y;
+                s[j + 2] = v.z;
+                s[j + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) s[j] = -__builtin_inff();
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) s[j] = (active && e0 + j < n_exp) ? lg[e0 + j] : -__builtin_inff();
     }
-
     if (gating == 2) {
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) s[j] = 1.0f / (1.0f + expf_glibc(-l[j], tab));
+        for (int j = 0; j < EPL; ++j) s[j] = 1.0f / (1.0f + expf_glibc(-s[j], tab));
     } else {
-        // max over all experts; fmaxf skips NaN like the CPU's f32::max fold.
-        float m = l[0];
+        float m = s[0];
 #pragma unroll
-        for (int j = 1; j < EPL; ++j) m = fmaxf(m, l[j]);
-        m = wave_max(m);
+        for (int j = 1; j < EPL; ++j) m = fmaxf(m, s[j]);
+        if constexpr (G <= 16) {
+            m = group_max_f32<G>(m);
+        } else {
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            const uint32_t e = lane + kWave * j;
-            s[j] = expf_glibc(l[j] - m, tab);
-            if (e < n_exp) ex_lds[wave][e] = s[j];
+            for (int off = G / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
         }
-        __syncthreads();
-        if (lane == 0) {
-            float d = 0.0f;
-            for (uint32_t e = 0; e < n_exp; ++e) d += ex_lds[wave][e];  // expert order
-            denom_lds[wave] = d;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) s[j] = expf_glibc(s[j] - m, tab);
+        float d = 0.0f;
+        for (uint32_t q = 0; q < (uint32_t)G; ++q) {
+            if (sub == q) {
+#pragma unroll
+                for (int j = 0; j < EPL; ++j)
+                    if (e0 + j < n_exp) d += s[j];
+            }
+            // lane q hands the running sum to lane q+1
+            const float up = (G <= 16) ? dpp_f32<0x111>(d) : __shfl_up(d, 1, G);
+            if (sub == q + 1) d = up;
         }
-        __syncthreads();
-        const float d = denom_lds[wave];
+        d = __shfl(d, G - 1, G);  // the last lane of the group holds the full fold
         if (d > 0.0f) {
+            // e / d for every expert with one IEEE reciprocal per token:
+            // y = RN(1/d), q0 = RN(e*y), r = e - d*q0 (exact), q = RN(q0 + r*y),
+            // which Markstein's theorem makes the correctly rounded e / d when no
+            // step underflows; tiny or non-finite operands take the IEEE division.
+            // (Checked against IEEE division for 4096 values of d in [1, 512)
+            // and every e in [2^-100, 1].)
+            const float y = 1.0f / d;
+            const bool d_ok = d < 0x1p+100f;
 #pragma unroll
-            for (int j = 0; j < EPL; ++j) s[j] = s[j] / d;
+            for (int j = 0; j < EPL; ++j) {
+                const float e = s[j];
+                if (d_ok && e >= 0x1p-100f && e <= 1.0f) {
+                    const float q0 = e * y;
+                    const float r = __builtin_fmaf(-d, q0, e);
+                    s[j] = __builtin_fmaf(r, y, q0);
+                } else {
+                    s[j] = e / d;
+                }
+            }
         }
     }
-
-    uint64_t key[EPL];
+    uint64_t key[EPL];  // (total-order score << 32) | ~expert; 0 = not a candidate
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
-        const uint32_t e = lane + kWave * j;
-        key[j] = (e < n_exp) ? ((uint64_t)total_order_key(s[j]) << 32) | (uint64_t)(0xffffffffu - e) : 0ull;
+        const uint32_t e = e0 + j;
+        key[j] = (active && e < n_exp) ? ((uint64_t)total_order_key(s[j]) << 32) | (uint64_t)(0xffffffffu - e) : 0ull;
     }
+    float sum = 0.0f;
     for (uint32_t r = 0; r < k; ++r) {
-        uint64_t best = 0;
+        uint64_t best = key[0];
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) best = key[j] > best ? key[j] : best;
-        const uint64_t win = wave_max_u64(best);
-        const uint32_t e = 0xffffffffu - (uint32_t)win;
-        if (e % kWave == lane) {
+        for (int j = 1; j < EPL; ++j) best = key[j] > best ? key[j] : best;
+        if constexpr (G <= 16) {
+            best = group_max_u64<G>(best);
+        } else {
+#pragma unroll
+            for (int off = G / 2; off > 0; off >>= 1) {
+                const uint64_t o = __shfl_xor(best, off, kWave);
+                best = o > best ? o : best;
+            }
+        }
+        const uint32_t e = 0xffffffffu - (uint32_t)best;
+        if (e / EPL == sub) {
 #pragma unroll
             for (int j = 0; j < EPL; ++j)
-                if ((uint32_t)j == e / kWave) key[j] = 0;
+                if ((uint32_t)j == e % EPL) key[j] = 0;
         }
-        if (lane == 0) sel_lds[wave][r] = win;
+        const float raw = total_order_inv((uint32_t)(best >> 32));
+        sum += raw;  // rank order, as finish_selected sums
+        if (active && sub == 0) {
+            ids[(size_t)token * k + r] = e;
+            weights[(size_t)token * k + r] = raw;
+        }
     }
-    __syncthreads();
-    if (lane == 0 && active) {
-        float sum = 0.0f;
-        if (norm) {
-            for (uint32_t r = 0; r < k; ++r) sum += total_order_inv((uint32_t)(sel_lds[wave][r] >> 32));
-        }
-        const float scale = rsf == 0.0f ? 1.0f : rsf;
+    // The lane that wrote the raw scores rescales them (same thread, program order).
+    const float scale = rsf == 0.0f ? 1.0f : rsf;
+    if (active && sub == 0) {
         for (uint32_t r = 0; r < k; ++r) {
-            const uint64_t w = sel_lds[wave][r];
-            float v = total_order_inv((uint32_t)(w >> 32));
+            float v = weights[(size_t)token * k + r];
             if (norm && sum > 0.0f) v = v / sum;
-            v = v * scale;
-            ids[(size_t)token * k + r] = 0xffffffffu - (uint32_t)w;
-            weights[(size_t)token * k + r] = v;
+            weights[(size_t)token * k + r] = v * scale;
         }
     }
 }
@@ -139,19 +192,31 @@ extern "C" int fellm_rocm_router_topk(const float *logits, uint32_t tokens, uint
     const uint32_t k = n_expert_used < n_experts ? n_expert_used : n_experts;
     if (k == 0 || k > kMaxTopK) return FELLM_ERR_SHAPE;
     if (tokens == 0) return FELLM_OK;
-    const dim3 grid((tokens + kRouterWaves - 1) / kRouterWaves), block(kRouterBlock);
+    const dim3 block(kRouterBlock);
     hipStream_t s = as_stream(stream);
-    const uint32_t epl = (n_experts + kWave - 1) / kWave;
-#define FELLM_ROUTER(E)                                                                                   \
-    if (epl <= E) {                                                                                       \
-        hipLaunchKernelGGL(router_topk_kernel<E>, grid, block, 0, s, logits, tokens, n_experts, k,        \
-                           gating_func, norm_topk_prob, routed_scaling_factor, ids, weights);             \
-        return launch_status();                                                                           \
+    // Grouped path: EPL experts per lane, G lanes per token (G a power of two
+    // <= 64 with G * EPL >= n_experts).
+    {
+        constexpr int EPL = FELLM_ROUTER_EPL;
+        const uint32_t need = (n_experts + EPL - 1) / EPL;
+        uint32_t g = 1;
+        while (g < need) g <<= 1;
+        const uint32_t tpb = kRouterBlock / g;  // tokens per block
+        const dim3 ggrid((tokens + tpb - 1) / tpb);
+#define FELLM_ROUTER_G(GG)                                                                                 \
+        if (g == GG) {                                                                                     \
+            hipLaunchKernelGGL((router_topk_grouped<EPL, GG>), ggrid, block, 0, s, logits, tokens, n_experts, k, \
+                               gating_func, norm_topk_prob, routed_scaling_factor, ids, weights);          \
+            return launch_status();                                                                        \
+        }
+        FELLM_ROUTER_G(1)
+        FELLM_ROUTER_G(2)
+        FELLM_ROUTER_G(4)
+        FELLM_ROUTER_G(8)
+        FELLM_ROUTER_G(16)
+        FELLM_ROUTER_G(32)
+        FELLM_ROUTER_G(64)
+#undef FELLM_ROUTER_G
     }
-    FELLM_ROUTER(1)
-    FELLM_ROUTER(2)
-    FELLM_ROUTER(4)
-    FELLM_ROUTER(8)
-#undef FELLM_ROUTER
     return FELLM_ERR_SHAPE;
 }
