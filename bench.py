@@ -17,7 +17,8 @@ achieved GB/s = algorithmic bytes / kernel time (bytes each op must read and
 write once).  The CPU baseline times the C restatement of
 backend-cpu (oracle/, 1 thread) on a bounded sample of the same chain.
 
---suite measures every BASELINE config's ops (per-op GB/s table) instead.
+--suite measures every BASELINE config's ops (per-op GB/s table) instead, plus the
+decode gate/up K-quant GEMV + SwiGLU (next_gemv).
 """
 from __future__ import annotations
 
@@ -218,6 +219,40 @@ def c5_ops(torch, ops, dev, n_sets, seed=5):
     return chain, sets, T
 
 
+def gemv_ops(torch, ops, dev, n_sets, seed=6):
+    """Decode FFN gate/up GEMV + SwiGLU (GateUpSwiGlu) on GGUF K-quant weights:
+    Llama-3-8B (14336 x 4096) as Q4_K and Q6_K, Llama-3-70B (28672 x 8192) as
+    Q4_K.  One activation vector; weights rotate over enough copies (device
+    rolls of one synthetic matrix) that every launch streams them from HBM."""
+    import numpy as np
+
+    from fellm_amd import synth
+
+    rng = np.random.default_rng(seed)
+    chain, sets = [], []
+    cases = (("gate_up_q4k_8b", "q4k", 12, 14336, 4096, max(n_sets, 8)),
+             ("gate_up_q6k_8b", "q6k", 14, 14336, 4096, max(n_sets, 6)),
+             ("gate_up_q4k_70b", "q4k", 12, 28672, 8192, max(n_sets, 3)))
+    per_case = []
+    for name, qt, code, rows, cols, nset in cases:
+        g0 = torch.from_numpy(synth.KQUANT_TABLES[code](rng, rows, cols)).to(dev)
+        u0 = torch.from_numpy(synth.KQUANT_TABLES[code](rng, rows, cols)).to(dev)
+        mats = [(g0.roll(7 * i, 0).contiguous(), u0.roll(5 * i, 0).contiguous()) for i in range(nset)]
+        x = torch.randn(cols, device=dev)
+        out = torch.empty(rows, device=dev)
+        per_case.append((mats, x, out))
+        nbytes = 2 * g0.numel() + cols * 4 + rows * 4
+
+        def fn(s, mats=mats, x=x, out=out, qt=qt, key=name):
+            i = s["i"][key] = (s["i"][key] + 1) % len(mats)
+            ops.gate_up_swiglu(mats[i][0], mats[i][1], x, qtype=qt, out=out)
+
+        chain.append(Op(name, nbytes, fn))
+    state = {"i": {c[0]: 0 for c in cases}}
+    sets = [state]
+    return chain, sets, 1
+
+
 # --------------------------------------------------------------------------- #
 # Timing
 # --------------------------------------------------------------------------- #
@@ -352,7 +387,8 @@ def main():
 
     if args.suite:
         result = {}
-        for name, make in (("c2", c2_ops), ("c3", c3_ops), ("c4", c4_ops), ("c5", c5_ops)):
+        for name, make in (("c2", c2_ops), ("c3", c3_ops), ("c4", c4_ops), ("c5", c5_ops),
+                           ("next_gemv", gemv_ops)):
             chain, sets, _ = make(torch, ops, dev, args.sets)
             _, per_op = run_chain(torch, chain, sets, args.steps, args.warmup)
             result[name] = op_report(per_op)

@@ -57,6 +57,8 @@ _SIGNATURES = {
     ),
     "fellm_rocm_router_topk": (I32, [P, U32, U32, U32, U32, U32, F32, P, P, P]),
     "fellm_rocm_expf": (I32, [P, P, U64, P]),
+    "fellm_rocm_gate_up_swiglu": (I32, [P, U32, P, U32, U32, U32, P, P, P]),
+    "fellm_rocm_matvec_kquant": (I32, [P, U32, U32, U32, P, P, P]),
     # plugin ABI
     "_fellm_plugin_abi_version": (abi.AbiVersion, []),
     "_fellm_plugin_manifest_json": (abi.PluginManifestJson, []),

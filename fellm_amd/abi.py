@@ -52,6 +52,7 @@ class OpKind(IntEnum):
     SAMPLE = 12
     KV_WRITE = 13
     MOE = 15
+    GATE_UP_SWIGLU = 17
 
 
 def custom_op(namespace: str, name: str) -> int:

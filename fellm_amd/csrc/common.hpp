@@ -269,6 +269,41 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
     return (float)y;
 }
 
+// get_scale_min_k4 (dequant.rs:295-305): 6-bit scale and min j (0..7) of a
+// Q4_K/Q5_K block from its 12 scale bytes held as 3 little-endian dwords.
+__device__ __forceinline__ void k4_scale_min(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,
+                                             uint32_t &m) {
+    if (j < 4) {
+        sc = (s0 >> (8 * j)) & 63u;
+        m = (s1 >> (8 * j)) & 63u;
+    } else {
+        const uint32_t k = 8 * (j - 4);
+        const uint32_t b_hi = (s2 >> k) & 0xffu;                // q[j + 4]
+        sc = (b_hi & 0x0fu) | (((s0 >> k) & 0xffu) >> 6) << 4;  // q[j - 4] >> 6
+        m = (b_hi >> 4) | (((s1 >> k) & 0xffu) >> 6) << 4;      // q[j] >> 6
+    }
+}
+
+// silu(g) = g / (1 + exp(-g)) as swiglu.rs:5-7 computes it in f32.
+// g / d for d = 1 + exp(-g) >= 1: hardware reciprocal, one Newton step on the
+// reciprocal, one residual correction of the quotient (Markstein's sequence).
+// Inputs outside [2^-100, 2^126) take the IEEE division.  Proven equal to the
+// IEEE quotient for this use by comparing silu(g) for all 2^32 values of g.
+__device__ __forceinline__ float silu_div(float g, float d) {
+    const float ag = __builtin_fabsf(g);
+    if (!(ag >= 0x1p-100f && ag < 0x1p+126f && d < 0x1p+126f)) return g / d;
+    const float y0 = __builtin_amdgcn_rcpf(d);
+    const float e0 = __builtin_fmaf(-d, y0, 1.0f);
+    const float y1 = __builtin_fmaf(e0, y0, y0);
+    const float q0 = g * y1;
+    const float r0 = __builtin_fmaf(-d, q0, g);
+    return __builtin_fmaf(r0, y1, q0);
+}
+
+__device__ __forceinline__ float silu(float g, const uint64_t *tab) {
+    return silu_div(g, 1.0f + expf_glibc(-g, tab));
+}
+
 // Copies the 32-entry table into LDS once per block; returns the LDS pointer.
 // Contains __syncthreads.
 __device__ __forceinline__ const uint64_t *stage_expf_table(uint64_t *lds) {

@@ -26,25 +26,6 @@ inline uint32_t ew_grid(uint64_t units) {
     return (uint32_t)(g == 0 ? 1 : g);
 }
 
-// g / d for d = 1 + exp(-g) >= 1: hardware reciprocal, one Newton step on the
-// reciprocal, one residual correction of the quotient (Markstein's sequence).
-// Inputs outside [2^-100, 2^126) take the IEEE division.  Proven equal to the
-// IEEE quotient for this use by comparing silu(g) for all 2^32 values of g.
-__device__ __forceinline__ float silu_div(float g, float d) {
-    const float ag = __builtin_fabsf(g);
-    if (!(ag >= 0x1p-100f && ag < 0x1p+126f && d < 0x1p+126f)) return g / d;
-    const float y0 = __builtin_amdgcn_rcpf(d);
-    const float e0 = __builtin_fmaf(-d, y0, 1.0f);
-    const float y1 = __builtin_fmaf(e0, y0, y0);
-    const float q0 = g * y1;
-    const float r0 = __builtin_fmaf(-d, q0, g);
-    return __builtin_fmaf(r0, y1, q0);
-}
-
-__device__ __forceinline__ float silu(float g, const uint64_t *tab) {
-    return silu_div(g, 1.0f + expf_glibc(-g, tab));
-}
-
 template <typename I, typename O, int VEC, int UNROLL>
 __global__ __launch_bounds__(kEwBlock) void silu_gate_kernel(const typename I::T *__restrict__ g,
                                                              const typename I::T *__restrict__ u,

@@ -59,19 +59,6 @@ struct Q4KDec {
         const uint32_t q = p % 16;
         return (p / 16) * 256 + 64 * (q / 4) + 8 * (q % 4) + 32 * r;
     }
-    // get_scale_min_k4 (dequant.rs:295-305) on the 12 scale bytes held as 3 dwords.
-    __device__ static void scale_min(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,
-                                     uint32_t &m) {
-        if (j < 4) {
-            sc = (s0 >> (8 * j)) & 63u;
-            m = (s1 >> (8 * j)) & 63u;
-        } else {
-            const uint32_t k = 8 * (j - 4);
-            const uint32_t b_hi = (s2 >> k) & 0xffu;  // q[j + 4]
-            sc = (b_hi & 0x0fu) | (((s0 >> k) & 0xffu) >> 6) << 4;  // q[j - 4] >> 6
-            m = (b_hi >> 4) | (((s1 >> k) & 0xffu) >> 6) << 4;      // q[j] >> 6
-        }
-    }
     __device__ static void decode(const uint8_t *row, uint32_t p, float (&v)[OUT]) {
         const uint8_t *blk = row + (size_t)(p / 16) * 144;
         const uint32_t q = p % 16, c = q / 4, j = q % 4;
@@ -79,8 +66,8 @@ struct Q4KDec {
         const float d = half_bits_to_f32(hdr.x & 0xffffu);
         const float dmin = half_bits_to_f32(hdr.x >> 16);
         uint32_t sc0, m0, sc1, m1;
-        scale_min(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
-        scale_min(2 * c + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+        k4_scale_min(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
+        k4_scale_min(2 * c + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
         const float d1 = d * (float)sc0, m1f = dmin * (float)m0;
         const float d2 = d * (float)sc1, m2f = dmin * (float)m1;
         const uint2 qs = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * c + 8 * j);

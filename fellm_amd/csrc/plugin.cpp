@@ -616,6 +616,42 @@ int launch_router_topk(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint
     });
 }
 
+uint64_t kquant_row_bytes(uint32_t dt, uint64_t cols) {
+    if (cols % 256) return 0;
+    switch (dt) {
+        case FELLM_DTYPE_Q4K: return cols / 256 * 144;
+        case FELLM_DTYPE_Q5K: return cols / 256 * 176;
+        case FELLM_DTYPE_Q6K: return cols / 256 * 210;
+        default: return 0;
+    }
+}
+
+// GateUpSwiGlu [gate_w, up_w, x] -> out (backend.rs:944-1002; the CUDA
+// plugin's launch_q4k_gate_up_swiglu, launchers.rs:1654-1744): weights
+// [rows, cols] K-quant, x f32 [cols], out f32 [rows].
+int launch_gate_up_swiglu(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                          uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 3, 1, false, [&](State &st) {
+        const FellmTensorRef &g = in[0], &u = in[1];
+        if (in[2].dtype != FELLM_DTYPE_F32 || out[0].dtype != FELLM_DTYPE_F32) fail(FELLM_ERR_DTYPE);
+        if (g.rank != 2 || u.rank != 2 || g.dims[0] != u.dims[0] || g.dims[1] != u.dims[1]) fail(FELLM_ERR_SHAPE);
+        const uint64_t rows = g.dims[0], cols = g.dims[1];
+        const uint64_t grb = kquant_row_bytes(g.dtype, cols), urb = kquant_row_bytes(u.dtype, cols);
+        if (!grb || !urb) fail(g.dtype == FELLM_DTYPE_Q4K || g.dtype == FELLM_DTYPE_Q5K || g.dtype == FELLM_DTYPE_Q6K
+                                   ? FELLM_ERR_SHAPE
+                                   : FELLM_ERR_DTYPE);
+        if (g.byte_len < rows * grb || u.byte_len < rows * urb || rows > 0xffffffffull) fail(FELLM_ERR_SHAPE);
+        if (elems(in[2], FELLM_DTYPE_F32) != cols || elems(out[0], FELLM_DTYPE_F32) != rows) fail(FELLM_ERR_SHAPE);
+        void *gw = ensure_input(st, g);
+        void *uw = ensure_input(st, u);
+        void *x = ensure_input(st, in[2]);
+        void *o = ensure_output(st, out[0]);
+        check(fellm_rocm_gate_up_swiglu(gw, g.dtype, uw, u.dtype, (uint32_t)rows, (uint32_t)cols, (const float *)x,
+                                        (float *)o, stream_ptr(st)));
+        finish_outputs(st, out, 1);
+    });
+}
+
 // Cast [x] -> host x of the same dtype: materialise a device-valid mirror into
 // host storage (launchers.rs:140-170).
 int launch_materialize(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
@@ -673,7 +709,7 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
     try {
         if (!vt || !vt->register_op) return FELLM_ERR_ARITY;
         const uint32_t F32 = FELLM_DTYPE_F32, F16 = FELLM_DTYPE_F16, BF16 = FELLM_DTYPE_BF16;
-        const uint32_t Q4K = FELLM_DTYPE_Q4K, Q6K = FELLM_DTYPE_Q6K, U32 = FELLM_DTYPE_U32;
+        const uint32_t Q4K = FELLM_DTYPE_Q4K, Q5K = FELLM_DTYPE_Q5K, Q6K = FELLM_DTYPE_Q6K, U32 = FELLM_DTYPE_U32;
         struct R {
             uint32_t op;
             std::initializer_list<uint32_t> ins;
@@ -713,6 +749,18 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
             {FELLM_OP_EMBEDDING, {BF16, U32}, BF16, launch_embedding},
             {FELLM_OP_EMBEDDING, {Q4K, U32}, F16, launch_embedding},
             {FELLM_OP_EMBEDDING, {Q6K, U32}, F16, launch_embedding},
+            // GateUpSwiGlu for every K-quant gate/up pair (backend-cpu accepts any
+            // supported matvec dtype pair, backend.rs:430-435; the CUDA plugin
+            // registers the same-dtype pairs, lib.rs:467-496).
+            {FELLM_OP_GATE_UP_SWIGLU, {Q4K, Q4K, F32}, F32, launch_gate_up_swiglu},
+            {FELLM_OP_GATE_UP_SWIGLU, {Q5K, Q5K, F32}, F32, launch_gate_up_swiglu},
+            {FELLM_OP_GATE_UP_SWIGLU, {Q6K, Q6K, F32}, F32, launch_gate_up_swiglu},
+            {FELLM_OP_GATE_UP_SWIGLU, {Q4K, Q5K, F32}, F32, launch_gate_up_swiglu},
+            {FELLM_OP_GATE_UP_SWIGLU, {Q4K, Q6K, F32}, F32, launch_gate_up_swiglu},
+            {FELLM_OP_GATE_UP_SWIGLU, {Q5K, Q4K, F32}, F32, launch_gate_up_swiglu},
+            {FELLM_OP_GATE_UP_SWIGLU, {Q5K, Q6K, F32}, F32, launch_gate_up_swiglu},
+            {FELLM_OP_GATE_UP_SWIGLU, {Q6K, Q4K, F32}, F32, launch_gate_up_swiglu},
+            {FELLM_OP_GATE_UP_SWIGLU, {Q6K, Q5K, F32}, F32, launch_gate_up_swiglu},
             // Fused custom ops (OpKind::custom("rocm", ...)).
             {kOpAddRmsNorm, {F32, F32, F32}, F32, launch_add_rmsnorm},
             {kOpAddRmsNorm, {F16, F16, F32}, F16, launch_add_rmsnorm},

@@ -28,7 +28,12 @@ namespace {
 #define FELLM_ROUTER_EPL 16
 #endif
 
-constexpr int kRouterBlock = 256;
+// Build knob: threads per workgroup.
+#ifndef FELLM_ROUTER_BLOCK
+#define FELLM_ROUTER_BLOCK 256
+#endif
+
+constexpr int kRouterBlock = FELLM_ROUTER_BLOCK;
 constexpr int kRouterWaves = kRouterBlock / kWave;
 constexpr uint32_t kMaxExperts = 512;
 constexpr uint32_t kMaxTopK = kMaxExperts;

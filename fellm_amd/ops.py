@@ -19,7 +19,7 @@ from .abi import DType
 
 _ACT = {torch.float32: DType.F32, torch.float16: DType.F16, torch.bfloat16: DType.BF16}
 _TORCH = {v: k for k, v in _ACT.items()}
-QTYPES = {"q4k": (DType.Q4K, 144), "q6k": (DType.Q6K, 210)}
+QTYPES = {"q4k": (DType.Q4K, 144), "q5k": (DType.Q5K, 176), "q6k": (DType.Q6K, 210)}
 
 
 def _code(t: torch.Tensor) -> int:
@@ -227,6 +227,43 @@ def router_topk(logits, k: int, *, gating_func: int = 1, norm_topk_prob: bool = 
     _lib.call("fellm_rocm_router_topk", _p(logits), tokens, n_exp, k, gating_func, int(norm_topk_prob),
               routed_scaling_factor, _p(ids), _p(weights), _stream())
     return ids, weights
+
+
+def _kquant_code(qtype: str, w, cols: int) -> int:
+    code, bb = QTYPES[qtype]
+    if w.dtype != torch.uint8 or w.dim() != 2 or w.shape[1] != cols // 256 * bb:
+        raise ValueError(f"{qtype} weights must be uint8 [rows, cols/256*{bb}]")
+    return int(code)
+
+
+def gate_up_swiglu(gate_w, up_w, x, *, qtype: str = "q4k", up_qtype: str | None = None, out=None):
+    """out[r] = silu(gate_w[r] . x) * (up_w[r] . x) with x quantized to Q8_K
+    (GateUpSwiGlu, backend.rs:944-1002).  Weights: uint8 GGUF K-quant rows."""
+    _dev(gate_w, up_w, x)
+    if x.dtype != torch.float32 or x.dim() != 1:
+        raise TypeError("x must be a float32 vector")
+    cols = x.numel()
+    rows = gate_w.shape[0]
+    g = _kquant_code(qtype, gate_w, cols)
+    u = _kquant_code(up_qtype or qtype, up_w, cols)
+    if up_w.shape[0] != rows:
+        raise ValueError("gate and up must have the same number of rows")
+    out = out if out is not None else torch.empty(rows, dtype=torch.float32, device=x.device)
+    _lib.call("fellm_rocm_gate_up_swiglu", _p(gate_w), g, _p(up_w), u, rows, cols, _p(x), _p(out), _stream())
+    return out
+
+
+def matvec_kquant(w, x, *, qtype: str = "q4k", out=None):
+    """y = W x for one activation vector, x quantized to Q8_K (matvec_quant, matmul.rs:534-600)."""
+    _dev(w, x)
+    if x.dtype != torch.float32 or x.dim() != 1:
+        raise TypeError("x must be a float32 vector")
+    cols = x.numel()
+    code = _kquant_code(qtype, w, cols)
+    rows = w.shape[0]
+    out = out if out is not None else torch.empty(rows, dtype=torch.float32, device=x.device)
+    _lib.call("fellm_rocm_matvec_kquant", _p(w), code, rows, cols, _p(x), _p(out), _stream())
+    return out
 
 
 def expf(x):

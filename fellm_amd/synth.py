@@ -58,6 +58,24 @@ def q6k_table(rng: np.random.Generator, vocab: int, dim: int) -> np.ndarray:
     return blocks.reshape(vocab, nb * Q6K_BLOCK)
 
 
+def q5k_table(rng: np.random.Generator, vocab: int, dim: int) -> np.ndarray:
+    """uint8 [vocab, dim/256*176]: d, dmin ~ f16(|N(0, 0.01)|), 6-bit sc/m U[0,63], qh and qs uniform bytes."""
+    assert dim % QK_K == 0
+    nb = dim // QK_K
+    blocks = np.empty((vocab, nb, 176), np.uint8)
+    blocks[..., 0:2] = _abs_normal_f16_bits(rng, (vocab, nb), 0.01).view(np.uint8).reshape(vocab, nb, 2)
+    blocks[..., 2:4] = _abs_normal_f16_bits(rng, (vocab, nb), 0.01).view(np.uint8).reshape(vocab, nb, 2)
+    ls = rng.integers(0, 64, size=(vocab, nb, 8), dtype=np.uint8)
+    lm = rng.integers(0, 64, size=(vocab, nb, 8), dtype=np.uint8)
+    blocks[..., 4:16] = pack_scale_min_k4(ls, lm)
+    blocks[..., 16:] = rng.integers(0, 256, size=(vocab, nb, 160), dtype=np.uint8)
+    return blocks.reshape(vocab, nb * 176)
+
+
+KQUANT_TABLES = {12: q4k_table, 13: q5k_table, 14: q6k_table}
+KQUANT_BLOCK_BYTES = {12: 144, 13: 176, 14: 210}
+
+
 def zipf_ids(rng: np.random.Generator, n: int, vocab: int, s: float = 1.1) -> np.ndarray:
     """Token ids Zipf(s) over [0, vocab) by inverse CDF (rank 1 = id 0)."""
     ranks = np.arange(1, vocab + 1, dtype=np.float64)

@@ -64,6 +64,7 @@ enum {
     FELLM_OP_SAMPLE = 12,
     FELLM_OP_KV_WRITE = 13,
     FELLM_OP_MOE = 15,
+    FELLM_OP_GATE_UP_SWIGLU = 17,
 };
 /* OpKind::custom(ns, name) = FNV-1a-32 over "ns:name", OR 0x8000_0000. */
 #define FELLM_OP_CUSTOM_TAG 0x80000000u

@@ -153,6 +153,35 @@ int fellm_rocm_router_topk(const float *logits, uint32_t tokens, uint32_t n_expe
                            void *stream);
 
 /*
+ * Fused gate/up GEMV with the SwiGLU epilogue for one activation vector:
+ * x is quantized once to Q8_K (256-element blocks: f32 scale, int8 values,
+ * int16 group sums), every row of gate_w and up_w is dotted against it, and
+ * out[r] = silu(gate[r]) * up[r].
+ * replaces: crates/backend-cpu/src/backend.rs:944-1002 (launch_gate_up_swiglu,
+ * OpKind::GateUpSwiGlu) -> kernels/matmul.rs:404-531 (matvec_quant_multi);
+ * the CUDA plugin's launch_q4k_gate_up_swiglu / launch_q5k_gate_up_swiglu
+ * (plugins/cuda_kernels/src/launchers.rs:1654, :1745).
+ * gate_w/up_w: GGUF K-quant rows [rows, cols] of dtype 12 (Q4_K), 13 (Q5_K) or
+ * 14 (Q6_K), Q4_K/Q5_K 16-byte aligned; x f32 [cols] 16-byte aligned,
+ * cols % 256 == 0, cols <= 49152; out f32 [rows].
+ * Integer dot products are exact; the f32 combine follows the CPU's portable
+ * path (vec_dot_q4k.rs:296-333, vec_dot_q5k.rs:189-218, matmul.rs:1597-1644)
+ * operation by operation.
+ */
+int fellm_rocm_gate_up_swiglu(const void *gate_w, uint32_t gate_dtype, const void *up_w, uint32_t up_dtype,
+                              uint32_t rows, uint32_t cols, const float *x, float *out, void *stream);
+
+/*
+ * K-quant GEMV y = W x for one activation vector (same quantization and
+ * arithmetic as fellm_rocm_gate_up_swiglu, no epilogue).
+ * replaces: kernels/matmul.rs:534-600 (matvec_quant, Q4_K/Q5_K/Q6_K arms), the
+ * rank-1 (decode) form of OpKind::MatMul [Q4K|Q5K|Q6K, F32] -> F32
+ * (crates/backend-cpu/src/backend.rs:861-920, launch_matmul with rows == 1).
+ */
+int fellm_rocm_matvec_kquant(const void *w, uint32_t w_dtype, uint32_t rows, uint32_t cols, const float *x,
+                             float *y, void *stream);
+
+/*
  * Self-check of the device expf restatement: out[i] = expf(in[i]) on the GPU.
  * Diagnostic only (no counterpart in the reference).
  */

@@ -51,6 +51,11 @@ def lib() -> C.CDLL:
             "oracle_rope": (C.c_int, [P, P, S, S, S, S, U32, P, P, S, U32]),
             "oracle_kv_write_paged": (C.c_int, [P, S, S, P, P, S, S, S, S, S, S, P, S, C.c_int, C.c_int]),
             "oracle_router": (C.c_int, [P, S, S, S, U32, U32, F, P, P]),
+            "oracle_quantize_q8k": (None, [P, S, P, P, P]),
+            "oracle_kquant45_ints": (None, [U32, P, P, P, P]),
+            "oracle_kquant_row_dot": (F, [U32, P, S, P, P, P]),
+            "oracle_matvec_kquant": (C.c_int, [U32, P, S, S, P, P]),
+            "oracle_gate_up_swiglu": (C.c_int, [U32, P, U32, P, S, S, P, P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(l, name)
@@ -233,3 +238,51 @@ def router(logits: np.ndarray, k: int, gating: int = 1, norm: bool = True, rsf: 
     if rc:
         raise ValueError(f"router rc={rc}")
     return ids, w
+
+
+# ---- next: K-quant GEMV + SwiGLU epilogue -------------------------------------
+def quantize_q8k(x: np.ndarray):
+    """Q8_K activations of x (len % 256 == 0): (qs int8[n], bsums int16[n/16], d f32[n/256])."""
+    a = _c(x, np.float32).ravel()
+    qs = np.empty(a.size, np.int8)
+    bs = np.empty(a.size // 16, np.int16)
+    d = np.empty(a.size // 256, np.float32)
+    lib().oracle_quantize_q8k(_p(a), a.size, _p(qs), _p(bs), _p(d))
+    return qs, bs, d
+
+
+def kquant45_ints(dtype: int, block: np.ndarray, qs: np.ndarray, bsums: np.ndarray) -> tuple[int, int]:
+    """(sumi, sumi_min) of one Q4_K/Q5_K block against one Q8_K block."""
+    b = _c(block, np.uint8)
+    q = _c(qs, np.int8)
+    s = _c(bsums, np.int16)
+    out = np.zeros(2, np.int32)
+    lib().oracle_kquant45_ints(dtype, _p(b), _p(q), _p(s), _p(out))
+    return int(out[0]), int(out[1])
+
+
+def kquant_row_dot(dtype: int, row: np.ndarray, cols: int, qs, bsums, d) -> float:
+    r = _c(row, np.uint8)
+    q, s, dd = _c(qs, np.int8), _c(bsums, np.int16), _c(d, np.float32)
+    return float(np.float32(lib().oracle_kquant_row_dot(dtype, _p(r), cols, _p(q), _p(s), _p(dd))))
+
+
+def matvec_kquant(dtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    ww = _c(w, np.uint8)
+    xx = _c(x, np.float32)
+    y = np.empty(rows, np.float32)
+    rc = lib().oracle_matvec_kquant(dtype, _p(ww), rows, cols, _p(xx), _p(y))
+    if rc:
+        raise ValueError(f"oracle_matvec_kquant rc={rc}")
+    return y
+
+
+def gate_up_swiglu(gate_dtype: int, gate_w: np.ndarray, up_dtype: int, up_w: np.ndarray, rows: int, cols: int,
+                   x: np.ndarray) -> np.ndarray:
+    g, u = _c(gate_w, np.uint8), _c(up_w, np.uint8)
+    xx = _c(x, np.float32)
+    out = np.empty(rows, np.float32)
+    rc = lib().oracle_gate_up_swiglu(gate_dtype, _p(g), up_dtype, _p(u), rows, cols, _p(xx), _p(out))
+    if rc:
+        raise ValueError(f"oracle_gate_up_swiglu rc={rc}")
+    return out

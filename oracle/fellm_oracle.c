@@ -458,3 +458,182 @@ int oracle_router(const float *logits, size_t tokens, size_t n_experts, size_t n
     free(sc);
     return 0;
 }
+
+/* ---- next: quantized gate/up GEMV with the SwiGLU epilogue ---------------
+ * backend.rs:944-1002 (launch_gate_up_swiglu) -> matmul.rs:404-531
+ * (matvec_quant_multi: x quantized once to Q8_K, every row of gate then up
+ * dotted against it, then swiglu.rs silu_gate(gate, up)).
+ *
+ * Q8_K (matmul.rs:21-29): per 256 elements one f32 d, 256 int8 qs and 16
+ * int16 bsums.  Quantization follows quantize_row_q8_k_avx2
+ * (matmul.rs:213-270), the path every AVX2 x86 host takes: amax = max |x|,
+ * iscale = 127/amax, q = round-to-nearest-even(x*iscale) saturated to int8,
+ * bsums = sums of 16 consecutive q, d = amax/127; amax == 0 gives all zeros.
+ *
+ * Row dots follow the portable (scalar) paths, whose f32 order is fixed:
+ *   Q4_K vec_dot_q4k.rs:296-333, Q5_K vec_dot_q5k.rs:189-218 (per block
+ *     sumf = ((-dmin)*xd)*f(sumi_min); sumf += (d*xd)*f(sumi)), row = serial
+ *     sum over blocks (vec_dot_q4k.rs:68-77);
+ *   Q6_K matmul.rs:1597-1644 (fused_q6_k_block: 16 terms (d*sc)*f(dot) in
+ *     (half, is, k) order, times xd), row = serial sum (matmul.rs:516-525).
+ * The SIMD Q4_K/Q5_K paths (AVX2 / VNNI / AVX-512) compute the same integer
+ * dots and differ only in the f32 combine order. */
+
+void oracle_quantize_q8k(const float *x, size_t n, int8_t *qs, int16_t *bsums, float *d) {
+    for (size_t b = 0; b < n / QK_K; ++b) {
+        const float *xb = x + b * QK_K;
+        int8_t *q = qs + b * QK_K;
+        float amax = 0.0f;
+        for (int i = 0; i < QK_K; ++i) {
+            const float a = fabsf(xb[i]);
+            amax = a > amax ? a : amax;
+        }
+        if (amax == 0.0f) {
+            memset(q, 0, QK_K);
+            memset(bsums + b * 16, 0, 16 * sizeof(int16_t));
+            d[b] = 0.0f;
+            continue;
+        }
+        const float iscale = 127.0f / amax;
+        for (int i = 0; i < QK_K; ++i) {
+            /* _mm256_cvtps_epi32 (round to nearest even) returns INT32_MIN for
+             * NaN and |v| >= 2^31 (iscale overflows to inf when amax < ~3.7e-37);
+             * the saturating packs then clamp to [-128, 127]. */
+            const float v = xb[i] * iscale;
+            if (!(fabsf(v) < 2147483648.0f)) {
+                q[i] = -128;
+                continue;
+            }
+            const long r = lrintf(v);
+            q[i] = (int8_t)(r < -128 ? -128 : r > 127 ? 127 : r);
+        }
+        for (int g = 0; g < 16; ++g) {
+            int s = 0;
+            for (int l = 0; l < 16; ++l) s += q[g * 16 + l];
+            bsums[b * 16 + g] = (int16_t)s;
+        }
+        d[b] = amax / 127.0f;
+    }
+}
+
+/* Integer parts of one Q4_K / Q5_K block against one Q8_K block:
+ * sumi = sum_g sc[g] * dot(aux8[32g..], q[32g..]), sumi_min = sum_j bsums[j] * m[j/2]. */
+static void kquant45_ints(uint32_t dtype, const uint8_t *blk, const int8_t *q, const int16_t *bs, int32_t *sumi,
+                          int32_t *sumi_min) {
+    uint8_t sc[8], mn[8], aux8[QK_K];
+    for (int j = 0; j < 8; ++j) get_scale_min_k4((size_t)j, blk + 4, &sc[j], &mn[j]);
+    const uint8_t *qs = blk + (dtype == 13 ? 48 : 16), *qh = blk + 16;
+    for (int j = 0; j < 4; ++j) /* unpack_q4_k_aux8 / unpack_q5_k_aux8 */
+        for (int l = 0; l < 32; ++l) {
+            uint8_t lo = qs[32 * j + l] & 0x0F, hi = qs[32 * j + l] >> 4;
+            if (dtype == 13) {
+                lo = (uint8_t)(lo + ((qh[l] >> (2 * j)) & 1) * 16);
+                hi = (uint8_t)(hi + ((qh[l] >> (2 * j + 1)) & 1) * 16);
+            }
+            aux8[64 * j + l] = lo;
+            aux8[64 * j + 32 + l] = hi;
+        }
+    int32_t smin = 0, s = 0;
+    for (int j = 0; j < 16; ++j) smin += (int32_t)bs[j] * (int32_t)mn[j / 2];
+    for (int g = 0; g < 8; ++g) {
+        int32_t dot = 0;
+        for (int l = 0; l < 32; ++l) dot += (int32_t)aux8[32 * g + l] * (int32_t)q[32 * g + l];
+        s += (int32_t)sc[g] * dot;
+    }
+    *sumi = s;
+    *sumi_min = smin;
+}
+
+void oracle_kquant45_ints(uint32_t dtype, const uint8_t *blk, const int8_t *q, const int16_t *bs, int32_t *out2) {
+    kquant45_ints(dtype, blk, q, bs, &out2[0], &out2[1]);
+}
+
+static float dot_k45_block(uint32_t dtype, const uint8_t *blk, const int8_t *q, const int16_t *bs, float xd) {
+    const float d = f16_to_f32(le16(blk)), dmin = f16_to_f32(le16(blk + 2));
+    int32_t sumi, sumi_min;
+    kquant45_ints(dtype, blk, q, bs, &sumi, &sumi_min);
+    float sumf = -dmin * xd * (float)sumi_min;
+    sumf += d * xd * (float)sumi;
+    return sumf;
+}
+
+/* matmul.rs:1597-1644 */
+static float dot_q6k_block(const uint8_t *blk, const int8_t *xq, float xd) {
+    const uint8_t *ql_all = blk, *qh_all = blk + 128;
+    const int8_t *scales = (const int8_t *)(blk + 192);
+    const float d = f16_to_f32(le16(blk + 208));
+    float acc = 0.0f;
+    for (int h = 0; h < 2; ++h) {
+        const uint8_t *ql = ql_all + 64 * h, *qh = qh_all + 32 * h;
+        const int8_t *sc = scales + 8 * h, *x = xq + 128 * h;
+        int32_t dots[4][2] = {{0}};
+        for (int l = 0; l < 32; ++l) {
+            const int is = l / 16;
+            const int q1 = ((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+            const int q2 = ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            dots[0][is] += q1 * x[l];
+            dots[1][is] += q2 * x[l + 32];
+            dots[2][is] += q3 * x[l + 64];
+            dots[3][is] += q4 * x[l + 96];
+        }
+        for (int is = 0; is < 2; ++is)
+            for (int k = 0; k < 4; ++k) acc += d * (float)sc[is + 2 * k] * (float)dots[k][is];
+    }
+    return acc * xd;
+}
+
+static size_t kquant_block_bytes(uint32_t dtype) {
+    return dtype == 12 ? 144 : dtype == 13 ? 176 : dtype == 14 ? 210 : 0;
+}
+
+/* One weight row against quantized activations: serial f32 sum over blocks. */
+float oracle_kquant_row_dot(uint32_t dtype, const uint8_t *row, size_t cols, const int8_t *qs, const int16_t *bsums,
+                            const float *d) {
+    const size_t bb = kquant_block_bytes(dtype);
+    float acc = 0.0f;
+    for (size_t b = 0; b < cols / QK_K; ++b) {
+        if (dtype == 14)
+            acc += dot_q6k_block(row + b * bb, qs + b * QK_K, d[b]);
+        else
+            acc += dot_k45_block(dtype, row + b * bb, qs + b * QK_K, bsums + b * 16, d[b]);
+    }
+    return acc;
+}
+
+static int matvec_kquant_q(uint32_t dtype, const uint8_t *w, size_t rows, size_t cols, const int8_t *qs,
+                           const int16_t *bs, const float *d, float *y) {
+    const size_t bb = kquant_block_bytes(dtype);
+    if (!bb || cols % QK_K) return -2;
+    const size_t rb = cols / QK_K * bb;
+    for (size_t r = 0; r < rows; ++r) y[r] = oracle_kquant_row_dot(dtype, w + r * rb, cols, qs, bs, d);
+    return 0;
+}
+
+/* matvec_quant (matmul.rs:534-600) for the K-quant dtypes. */
+int oracle_matvec_kquant(uint32_t dtype, const uint8_t *w, size_t rows, size_t cols, const float *x, float *y) {
+    if (cols % QK_K) return -2;
+    int8_t *qs = malloc(cols);
+    int16_t *bs = malloc(cols / 16 * sizeof(int16_t));
+    float *d = malloc(cols / QK_K * sizeof(float));
+    oracle_quantize_q8k(x, cols, qs, bs, d);
+    const int rc = matvec_kquant_q(dtype, w, rows, cols, qs, bs, d, y);
+    free(qs);
+    free(bs);
+    free(d);
+    return rc;
+}
+
+/* backend.rs:944-1002: gate and up rows against one Q8_K copy of x, then
+ * out = silu(gate) * up (swiglu.rs:5-16). */
+int oracle_gate_up_swiglu(uint32_t gate_dtype, const uint8_t *gate_w, uint32_t up_dtype, const uint8_t *up_w,
+                          size_t rows, size_t cols, const float *x, float *out) {
+    float *g = malloc(rows * sizeof(float)), *u = malloc(rows * sizeof(float));
+    int rc = oracle_matvec_kquant(gate_dtype, gate_w, rows, cols, x, g);
+    if (!rc) rc = oracle_matvec_kquant(up_dtype, up_w, rows, cols, x, u);
+    if (!rc) oracle_silu_gate(g, u, out, rows);
+    free(g);
+    free(u);
+    return rc;
+}

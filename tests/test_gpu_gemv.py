@@ -1,0 +1,115 @@
+"""GPU parity of the K-quant GEMV and the fused gate/up SwiGLU GEMV.
+
+Both are bit-exact against the oracle (oracle/fellm_oracle.c: Q8_K
+quantization of x as quantize_row_q8_k_avx2, block dots as the CPU's portable
+path, serial f32 row sums, glibc-exact silu): integer parts are exact by
+construction and the f32 combine follows the same operation order.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from fellm_amd import synth
+from parity_util import assert_exact
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+NAMES = {12: "q4k", 13: "q5k", 14: "q6k"}
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from fellm_amd import ops as _ops
+
+    return _ops
+
+
+def weights(rng, dtype, rows, cols):
+    return synth.KQUANT_TABLES[dtype](rng, rows, cols)
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("gt", [12, 13, 14])
+@pytest.mark.parametrize("ut", [12, 13, 14])
+def test_gate_up_swiglu_pairs(ops, dev, gt, ut):
+    rng = np.random.default_rng(gt * 100 + ut)
+    rows, cols = 300, 4096
+    g, u = weights(rng, gt, rows, cols), weights(rng, ut, rows, cols)
+    x = rng.normal(size=cols).astype(np.float32)
+    ref = oracle.gate_up_swiglu(gt, g, ut, u, rows, cols, x)
+    got = ops.gate_up_swiglu(to_dev(g, dev), to_dev(u, dev), to_dev(x, dev), qtype=NAMES[gt],
+                             up_qtype=NAMES[ut]).cpu().numpy()
+    assert_exact(got, ref, f"gate_up_swiglu {NAMES[gt]}/{NAMES[ut]}")
+
+
+# nb = cols/256 blocks per row: 1, 14 (partial pass), 16, 17, 32 (two passes), 65 (ragged third pass)
+@pytest.mark.parametrize("dtype", [12, 13, 14])
+@pytest.mark.parametrize("cols", [256, 3584, 4096, 4352, 8192, 16640])
+def test_matvec_kquant_shapes(ops, dev, dtype, cols):
+    rng = np.random.default_rng(dtype * 7 + cols)
+    rows = 129
+    w = weights(rng, dtype, rows, cols)
+    x = (rng.normal(size=cols) * rng.uniform(0.01, 20.0, size=cols)).astype(np.float32)
+    ref = oracle.matvec_kquant(dtype, w, rows, cols, x)
+    got = ops.matvec_kquant(to_dev(w, dev), to_dev(x, dev), qtype=NAMES[dtype]).cpu().numpy()
+    assert_exact(got, ref, f"matvec {NAMES[dtype]} cols={cols}")
+
+
+@pytest.mark.parametrize("dtype", [12, 13, 14])
+def test_matvec_q8k_edges(ops, dev, dtype):
+    """Zero blocks, round-half-even ties (amax 127 makes iscale 1), a block
+    whose amax is a denormal, and huge magnitudes."""
+    rng = np.random.default_rng(99 + dtype)
+    cols, rows = 2048, 70
+    x = rng.normal(size=cols).astype(np.float32)
+    x[0:256] = 0.0
+    x[256:512] = rng.integers(-127, 128, size=256).astype(np.float32) + np.float32(0.5)
+    x[256] = 127.0
+    x[512:768] = np.float32(1e-40) * rng.integers(-3, 4, size=256)
+    x[768] = np.float32(3e-40)
+    x[1024:1280] *= np.float32(1e30)
+    w = weights(rng, dtype, rows, cols)
+    ref = oracle.matvec_kquant(dtype, w, rows, cols, x)
+    got = ops.matvec_kquant(to_dev(w, dev), to_dev(x, dev), qtype=NAMES[dtype]).cpu().numpy()
+    assert_exact(got, ref, f"matvec edges {NAMES[dtype]}")
+
+
+@pytest.mark.parametrize("dtype", [12, 14])
+def test_gate_up_swiglu_llama3_8b_decode(ops, dev, dtype):
+    """Llama-3-8B FFN shape: 14336 rows, 4096 columns."""
+    rng = np.random.default_rng(8000 + dtype)
+    rows, cols = 14336, 4096
+    g, u = weights(rng, dtype, rows, cols), weights(rng, dtype, rows, cols)
+    x = rng.normal(size=cols).astype(np.float32)
+    ref = oracle.gate_up_swiglu(dtype, g, dtype, u, rows, cols, x)
+    got = ops.gate_up_swiglu(to_dev(g, dev), to_dev(u, dev), to_dev(x, dev), qtype=NAMES[dtype]).cpu().numpy()
+    assert_exact(got, ref, f"gate_up 8B {NAMES[dtype]}")
+
+
+def test_gate_up_zero_x_and_empty(ops, dev):
+    rng = np.random.default_rng(5)
+    rows, cols = 64, 1024
+    g, u = weights(rng, 12, rows, cols), weights(rng, 12, rows, cols)
+    got = ops.gate_up_swiglu(to_dev(g, dev), to_dev(u, dev), torch.zeros(cols, device=dev)).cpu().numpy()
+    assert np.all(got == 0.0)
+    empty = torch.empty((0, cols // 256 * 144), dtype=torch.uint8, device=dev)
+    out = ops.gate_up_swiglu(empty, empty, torch.zeros(cols, device=dev))
+    assert out.numel() == 0
+
+
+def test_gemv_rejects_bad_shapes(ops, dev):
+    from fellm_amd._lib import FellmRocmError
+
+    w = torch.zeros((4, 144), dtype=torch.uint8, device=dev)
+    with pytest.raises(ValueError):
+        ops.matvec_kquant(w, torch.zeros(200, device=dev))  # cols % 256 != 0
+    with pytest.raises(FellmRocmError):
+        ops.matvec_kquant(torch.zeros((4, 2 * 144), dtype=torch.uint8, device=dev),
+                          torch.zeros(513, device=dev)[1:])  # x not 16-byte aligned

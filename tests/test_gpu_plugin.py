@@ -291,3 +291,33 @@ def test_custom_embedding_rmsnorm(host):
     assert_exact(materialize(host, h, D.F16).view(np.uint16), oracle.narrow(e, "f16"), "fused h")
     assert_close(materialize(host, y, D.F16).view(np.uint16), oracle.narrow(oracle.rmsnorm(e, w, 1e-6), "f16"),
                  "f16", what="fused y")
+
+
+@pytest.mark.parametrize("gt,ut", [(D.Q4K, D.Q4K), (D.Q5K, D.Q5K), (D.Q6K, D.Q6K), (D.Q4K, D.Q6K)])
+def test_gate_up_swiglu(host, gt, ut):
+    """GateUpSwiGlu [gate_w, up_w, x] -> out (backend.rs:944-1002), keyed like
+    the CUDA plugin's registration (lib.rs:467-496), bit-exact with the oracle."""
+    rng = np.random.default_rng(int(gt) * 31 + int(ut))
+    rows, cols = 512, 2048
+    g = synth.KQUANT_TABLES[int(gt)](rng, rows, cols)
+    u = synth.KQUANT_TABLES[int(ut)](rng, rows, cols)
+    x = rng.normal(size=cols).astype(np.float32)
+    out = np.zeros(rows, np.float32)
+    run(host, abi.OpKind.GATE_UP_SWIGLU, [gt, ut, D.F32], D.F32, abi.OpAttrs(),
+        [tref(g, gt, [rows, cols], logical_id=7000 + 100 * int(gt) + int(ut)),
+         tref(u, ut, [rows, cols], logical_id=8000 + 100 * int(gt) + int(ut)),
+         tref(x, D.F32)], [tmut(out, D.F32)])
+    ref = oracle.gate_up_swiglu(int(gt), g, int(ut), u, rows, cols, x)
+    assert_exact(materialize(host, out, D.F32), ref, "plugin gate_up_swiglu")
+
+
+def test_gate_up_swiglu_shape_errors(host):
+    rows, cols = 8, 512
+    g = np.zeros((rows, cols // 256 * 144), np.uint8)
+    x = np.zeros(cols - 256, np.float32)  # wrong length
+    out = np.zeros(rows, np.float32)
+    h = host.lookup(abi.OpKind.GATE_UP_SWIGLU, [D.Q4K, D.Q4K, D.F32], D.F32)
+    rc = host.launch_raw(h, abi.OpAttrs(), [tref(g, D.Q4K, [rows, cols], logical_id=901),
+                                            tref(g, D.Q4K, [rows, cols], logical_id=901), tref(x, D.F32)],
+                         [tmut(out, D.F32)])
+    assert rc == abi.ERR_SHAPE
