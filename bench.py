@@ -18,7 +18,8 @@ write once).  The CPU baseline times the C restatement of
 backend-cpu (oracle/, 1 thread) on a bounded sample of the same chain.
 
 --suite measures every BASELINE config's ops (per-op GB/s table) instead, plus the
-decode gate/up K-quant GEMV + SwiGLU (next_gemv).
+decode gate/up K-quant GEMV + SwiGLU (next_gemv) and paged decode attention
+(next_attention).
 """
 from __future__ import annotations
 
@@ -253,6 +254,40 @@ def gemv_ops(torch, ops, dev, n_sets, seed=6):
     return chain, sets, 1
 
 
+def attention_ops(torch, ops, dev, n_sets, seed=7):
+    """Paged decode attention over an f16 cache in FeLLM's layout:
+    configs[3]-shaped (Llama-3-70B heads 64/8/128, 256 sequences x 4096 keys,
+    the whole 4.29 GB arena) and one Llama-3-8B sequence of 32768 keys (the
+    split-key path).  Physical blocks are a random permutation."""
+    chain = []
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    for name, B, seq, nh, nkv, hd in (("attn_decode_70b_b256_s4096", 256, 4096, 64, 8, 128),
+                                      ("attn_decode_8b_b1_s32768", 1, 32768, 32, 8, 128)):
+        stride = nkv * hd
+        bb = ops.PagedKvCache.block_bytes_for(stride)
+        n_logical = (seq + 15) // 16
+        nblk = B * n_logical
+        arena = torch.empty(nblk * bb, dtype=torch.uint8, device=dev)
+        arena.view(torch.float16).copy_((torch.randn(arena.numel() // 2, device=dev) * 0.5).half())
+        table = torch.randperm(nblk, generator=g).to(torch.int32).to(dev)
+        cache = ops.PagedKvCache(arena=arena, block_table=table, n_layers=1, n_logical_blocks=n_logical,
+                                 block_size=16, block_bytes=bb, stride=stride)
+        q = torch.randn(B, nh * hd, device=dev).half()
+        lens = torch.full((B,), seq, dtype=torch.int32, device=dev)
+        out = torch.empty(B, nh * hd, device=dev, dtype=torch.half)
+        ws_bytes = ops._lib.lib().fellm_rocm_paged_attention_workspace(B, nh, nkv, hd, seq)
+        ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev)
+        nbytes = B * seq * stride * 2 * 2 + 2 * B * nh * hd * 2 + B * 4
+
+        def fn(s, q=q, lens=lens, cache=cache, out=out, ws=ws, nh=nh, nkv=nkv, hd=hd, seq=seq):
+            ops.paged_attention(q, lens, cache, n_heads=nh, n_kv_heads=nkv, head_dim=hd, max_seq=seq, out=out,
+                                workspace=ws)
+
+        chain.append(Op(name, nbytes, fn))
+    return chain, [{}], 1
+
+
 # --------------------------------------------------------------------------- #
 # Timing
 # --------------------------------------------------------------------------- #
@@ -388,7 +423,7 @@ def main():
     if args.suite:
         result = {}
         for name, make in (("c2", c2_ops), ("c3", c3_ops), ("c4", c4_ops), ("c5", c5_ops),
-                           ("next_gemv", gemv_ops)):
+                           ("next_gemv", gemv_ops), ("next_attention", attention_ops)):
             chain, sets, _ = make(torch, ops, dev, args.sets)
             _, per_op = run_chain(torch, chain, sets, args.steps, args.warmup)
             result[name] = op_report(per_op)

@@ -59,6 +59,9 @@ _SIGNATURES = {
     "fellm_rocm_expf": (I32, [P, P, U64, P]),
     "fellm_rocm_gate_up_swiglu": (I32, [P, U32, P, U32, U32, U32, P, P, P]),
     "fellm_rocm_matvec_kquant": (I32, [P, U32, U32, U32, P, P, P]),
+    "fellm_rocm_paged_attention_workspace": (U64, [U32, U32, U32, U32, U32]),
+    "fellm_rocm_paged_attention": (I32, [P, U32, P, U32, U32, U32, U32, U32, P, U32, F32, U32, U32,
+                                         C.POINTER(FellmRocmPagedKv), P, U64, P]),
     # plugin ABI
     "_fellm_plugin_abi_version": (abi.AbiVersion, []),
     "_fellm_plugin_manifest_json": (abi.PluginManifestJson, []),

@@ -21,7 +21,7 @@ LIB_NAME = "libfellm_rocm_kernels.so"
 LIB_PATH = PKG / LIB_NAME
 ARCH = os.environ.get("FELLM_ROCM_ARCH", "gfx950")
 
-SOURCES = ["norm.hip", "elementwise.hip", "embedding.hip", "rope.hip", "router.hip", "gemv.hip", "plugin.cpp"]
+SOURCES = ["norm.hip", "elementwise.hip", "embedding.hip", "rope.hip", "router.hip", "gemv.hip", "attention.hip", "plugin.cpp"]
 
 # -ffp-contract=off keeps the reference's operation order (no silent FMA);
 # the packed-fp32 feature is disabled for every HIP translation unit.
@@ -58,7 +58,7 @@ def build(verbose: bool = False, out: Path = LIB_PATH, build_dir: Path = BUILD, 
     """Compile every source and link ``out``; ``defines`` are extra -D flags."""
     build_dir.mkdir(parents=True, exist_ok=True)
     extra = [f"-D{d}" for d in defines]
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), 7)) as ex:
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as ex:
         objs = list(ex.map(lambda src: _compile(src, build_dir, extra), SOURCES))
     tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), *DEVICE_FLAGS, "-shared", "-fPIC", f"-Wl,--version-script={CSRC / 'exports.map'}",

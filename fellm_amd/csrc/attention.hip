@@ -1,0 +1,499 @@
+// Paged decode attention over the KV cache the fused RoPE + KV append writes.
+//
+// Reference: crates/fellm-plugin-abi/src/attention_provider.rs:391-459
+//   (reference_attention_paged_f32: per query head, online softmax over the
+//   keys 0 .. seq-1, score = (q . k) * scale, keys older than the window
+//   skipped when causal; out = sum p v / sum p), driven per batch row as
+//   crates/backend-cpu/src/backend.rs:1286-1323 does (seq = row_lengths[row],
+//   causal, window = attention_window) and as the CUDA plugin's
+//   attention_paged_batch_heads launch (plugins/cuda_kernels/src/launchers.rs
+//   :3394-3446) is fed; K/V rows as crates/fellm-plugin-abi/src/paged_ctx.rs
+//   :138-174 address them.
+//
+// Work split.  One wavefront per (batch row b, KV head g, key split s); the
+// G = n_heads / n_kv query heads that share KV head g are processed together,
+// so every K/V byte is read once.  Keys go in cache blocks of 16 tokens:
+//  * Q.K^T on the matrix cores: v_mfma_f32_16x16x16f16 with A = the block's K
+//    rows (16 tokens x 16 dims per step) and B = q^T (16 dims x 16 head slots).
+//    q is split into f16 high and low parts (two MFMAs per step), so the
+//    products with the f16 cache are exact and the f32 accumulation carries
+//    q to ~2^-22 relative; a bf16 cache uses bf16 MFMAs with a three-way split.
+//    The contraction order over dims is a permutation shared by A and B: lane
+//    group i = lane / 16 holds dims 32(s/2) + 8i + 4(s%2) .. +3 of step s.
+//  * Online softmax in f32 per head (block max across the 64 lanes, exp,
+//    rescale by exp(m_old - m_new)), probabilities exchanged through LDS.
+//  * P.V on the vector ALUs: lane (token group tg = lane / 16, dim slice
+//    ds = lane % 16) accumulates HD/16 dims of all G heads over tokens
+//    4i + tg, in f32; the four token groups are summed at the end.
+// Splits (several wavefronts per (b, g) when b * n_kv is small) write
+// unnormalised partial sums with their running max and denominator; a second
+// kernel combines them.  Tokens outside [lo, seq) are masked with -inf and
+// their V rows read as zero, so stale cache bytes never reach the output.
+#include "common.hpp"
+#include "fellm_rocm.h"
+
+namespace fellm {
+namespace {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+using Rsrc = __amdgpu_buffer_rsrc_t;
+
+constexpr uint32_t kBlockTokens = 16;  // tokens per cache block handled by one MFMA tile
+
+struct PagedGeom {
+    const uint8_t *arena;
+    uint64_t arena_len;
+    const uint32_t *table;
+    uint64_t n_table;
+    uint32_t n_logical, n_layers, layer, block_size;
+    uint64_t block_bytes;
+    uint32_t stride;  // elements per token row (n_kv * head_dim)
+};
+
+// Cache element policies: MFMA operand split of q and widening of V.
+struct CacheF16 {
+    static constexpr int kParts = 2;
+    using Op = half4_t;
+    __device__ static Op part(const float (&v)[4], int p, float (&rem)[4]) {
+        Op o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const _Float16 h = (_Float16)rem[e];
+            o[e] = h;
+            rem[e] = rem[e] - (float)h;
+        }
+        (void)v;
+        (void)p;
+        return o;
+    }
+    __device__ static Op from_bits(uint32_t lo, uint32_t hi) {
+        Op o;
+        o[0] = __builtin_bit_cast(_Float16, (uint16_t)(lo & 0xffffu));
+        o[1] = __builtin_bit_cast(_Float16, (uint16_t)(lo >> 16));
+        o[2] = __builtin_bit_cast(_Float16, (uint16_t)(hi & 0xffffu));
+        o[3] = __builtin_bit_cast(_Float16, (uint16_t)(hi >> 16));
+        return o;
+    }
+    __device__ static f32x4 mfma(Op a, Op b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+    __device__ static float widen(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
+};
+
+struct CacheBF16 {
+    static constexpr int kParts = 3;
+    using Op = short4_t;
+    __device__ static Op part(const float (&v)[4], int p, float (&rem)[4]) {
+        Op o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // round to nearest even bf16, keep the remainder for the next part
+            const uint32_t u = __float_as_uint(rem[e]);
+            const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+            o[e] = (short)(r >> 16);
+            rem[e] = rem[e] - __uint_as_float(r);
+        }
+        (void)v;
+        (void)p;
+        return o;
+    }
+    __device__ static Op from_bits(uint32_t lo, uint32_t hi) {
+        Op o;
+        o[0] = (short)(lo & 0xffffu);
+        o[1] = (short)(lo >> 16);
+        o[2] = (short)(hi & 0xffffu);
+        o[3] = (short)(hi >> 16);
+        return o;
+    }
+    __device__ static f32x4 mfma(Op a, Op b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    }
+    __device__ static float widen(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+};
+
+// Keys of split s for a row of length seq: blocks [b0, b1) of the range
+// [lo, seq) (lo > 0 only for a causal window), in chunks of bps blocks.
+__device__ __forceinline__ void split_range(uint32_t seq, uint32_t lo, uint32_t s, uint32_t bps, uint32_t &b0,
+                                            uint32_t &b1) {
+    const uint32_t first = lo / kBlockTokens, last = (seq + kBlockTokens - 1) / kBlockTokens;
+    b0 = first + s * bps;
+    b1 = b0 + bps < last ? b0 + bps : last;
+    if (b0 > last) b0 = last;
+}
+
+// Q: query activation policy, O: output policy, C: cache policy, HD: head
+// dim (64, 128 or 256), GM: maximum query heads per KV head (8 or 16).
+template <typename Q, typename O, typename C, int HD, int GM>
+__global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T *__restrict__ q,
+                                                             typename O::T *__restrict__ out,
+                                                             float *__restrict__ part, const uint32_t *__restrict__ lens,
+                                                             const uint32_t *__restrict__ table, PagedGeom geo,
+                                                             uint32_t n_heads, uint32_t n_kv, float scale,
+                                                             uint32_t causal, uint32_t window, uint32_t splits,
+                                                             uint32_t bps) {
+    constexpr int NS = HD / 16;  // MFMA k-steps
+    constexpr int NKL = HD / 32; // 16-byte K loads per lane per block
+    constexpr int DP = HD / 16;  // dims per lane in P.V
+    __shared__ __align__(16) float lds_p[kBlockTokens * 16];
+    __shared__ __align__(16) float lds_h[16];
+
+    const uint32_t lane = threadIdx.x;
+    const uint32_t col = lane % 16, grp = lane / 16;  // MFMA column (head slot) / lane group
+    const uint32_t s = blockIdx.x % splits;
+    const uint32_t bg = blockIdx.x / splits;
+    const uint32_t g = bg % n_kv, b = bg / n_kv;
+    const uint32_t G = n_heads / n_kv;
+    const uint32_t seq = lens[b];
+    const uint32_t lo = (causal && window && seq > window) ? seq - window : 0;
+    uint32_t blk0, blk1;
+    split_range(seq, lo, s, bps, blk0, blk1);
+
+    // q^T as the B operand: head slot col (= query head g*G + col), dims of step st.
+    typename C::Op qb[NS][C::kParts];
+    {
+        const bool hv = col < G;
+        const typename Q::T *qh = q + ((size_t)b * n_heads + (size_t)g * G + (hv ? col : 0)) * HD;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            float v[4], rem[4];
+            const uint32_t d0 = 32 * (st / 2) + 8 * grp + 4 * (st % 2);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rem[e] = v[e] = hv ? Q::load(qh[d0 + e]) : 0.0f;
+#pragma unroll
+            for (int p = 0; p < C::kParts; ++p) qb[st][p] = C::part(v, p, rem);
+        }
+    }
+
+    float acc[GM][DP];
+#pragma unroll
+    for (int h = 0; h < GM; ++h)
+#pragma unroll
+        for (int d = 0; d < DP; ++d) acc[h][d] = 0.0f;
+    float m = -__builtin_inff(), l = 0.0f;  // running max / denominator of head slot col
+
+    const size_t row_bytes = (size_t)geo.stride * 2;
+    const size_t table_base = ((size_t)b * geo.n_layers + geo.layer) * geo.n_logical;
+    // One cache block's K and V slices for this lane, fetched through a
+    // buffer resource spanning the block: an absent or out-of-range block has
+    // range 0 and reads as zeros without memory traffic, so the next block is
+    // requested unconditionally while the current one is reduced.
+    struct BlockRegs {
+        uint4 kr[NKL];         // K: token col, dims 32c + 8 grp .. +7 of load c
+        uint32_t vr[4][DP / 2]; // V: token 4i + grp, dims col*DP .. +DP-1
+        bool ok;
+    };
+    auto fetch = [&](uint32_t blk, BlockRegs &R) {
+        const size_t ti = table_base + blk;
+        const uint64_t phys =
+            (blk < blk1 && blk < geo.n_logical && ti < geo.n_table) ? (uint64_t)table[ti] : ~0ull;
+        const bool ok = phys != ~0ull && (phys + 1) * geo.block_bytes <= geo.arena_len;
+        const uint8_t *base = geo.arena + (ok ? phys * geo.block_bytes : 0);
+        const Rsrc rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0,
+                                                          ok ? (int)geo.block_bytes : 0, 0x00020000);
+        const uint32_t koff = g * HD * 2 + col * (uint32_t)row_bytes + 16 * grp;
+#pragma unroll
+        for (int c = 0; c < NKL; ++c) {
+            const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rs, koff + 64 * c, 0, 2);
+            R.kr[c] = make_uint4(t.x, t.y, t.z, t.w);
+        }
+        const uint32_t voff = geo.block_size * (uint32_t)row_bytes + g * HD * 2 + col * DP * 2;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t o = voff + (4 * i + grp) * (uint32_t)row_bytes;
+            if constexpr (DP == 4) {  // 8 bytes per lane
+                const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, 2);
+                R.vr[i][0] = t.x;
+                R.vr[i][1] = t.y;
+            } else {  // 16 or 32 bytes per lane
+#pragma unroll
+                for (int w = 0; w < DP / 2; w += 4) {
+                    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 4 * w, 0, 2);
+                    R.vr[i][w] = t.x;
+                    R.vr[i][w + 1] = t.y;
+                    R.vr[i][w + 2] = t.z;
+                    R.vr[i][w + 3] = t.w;
+                }
+            }
+        }
+        R.ok = ok;
+    };
+    auto process = [&](uint32_t blk, const BlockRegs &R) {
+        const bool blk_ok = R.ok;
+        const uint4(&kr)[NKL] = R.kr;
+        const uint32_t(&vr)[4][DP / 2] = R.vr;
+        const uint32_t t0 = blk * kBlockTokens;
+        // S^T[token 4 grp + e][head slot col]
+        f32x4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const uint4 &k4 = kr[st / 2];
+            const typename C::Op a = (st % 2) ? C::from_bits(k4.z, k4.w) : C::from_bits(k4.x, k4.y);
+#pragma unroll
+            for (int p = 0; p < C::kParts; ++p) sacc = C::mfma(a, qb[st][p], sacc);
+        }
+        float sc[4];
+        float bmax = -__builtin_inff();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t t = t0 + 4 * grp + e;
+            const bool valid = blk_ok && t >= lo && t < seq;
+            sc[e] = valid ? sacc[e] * scale : -__builtin_inff();
+            bmax = fmaxf(bmax, sc[e]);
+        }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+        const float m_new = fmaxf(m, bmax);
+        const float alpha = (m > -__builtin_inff()) ? __expf(m - m_new) : 0.0f;
+        float psum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float p = sc[e] > -__builtin_inff() ? __expf(sc[e] - m_new) : 0.0f;
+            lds_p[(4 * grp + e) * 16 + col] = p;
+            psum += p;
+        }
+        psum += __shfl_xor(psum, 16, kWave);
+        psum += __shfl_xor(psum, 32, kWave);
+        // a head with no valid key yet keeps m = -inf, l = 0, alpha = 0
+        if (m_new > -__builtin_inff()) {
+            l = l * alpha + psum;
+            m = m_new;
+        }
+        if (grp == 0) lds_h[col] = m_new > -__builtin_inff() ? alpha : 1.0f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+
+        float al[GM];
+#pragma unroll
+        for (int h = 0; h < GM; h += 4) {
+            const float4 t = *reinterpret_cast<const float4 *>(&lds_h[h]);
+            al[h] = t.x;
+            al[h + 1] = t.y;
+            al[h + 2] = t.z;
+            al[h + 3] = t.w;
+        }
+#pragma unroll
+        for (int h = 0; h < GM; ++h)
+#pragma unroll
+            for (int d = 0; d < DP; ++d) acc[h][d] *= al[h];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t t = 4 * i + grp;
+            const bool tv = blk_ok && t0 + t >= lo && t0 + t < seq;
+            float v[DP];
+#pragma unroll
+            for (int w = 0; w < DP / 2; ++w) {
+                v[2 * w] = tv ? C::widen(vr[i][w] & 0xffffu) : 0.0f;
+                v[2 * w + 1] = tv ? C::widen(vr[i][w] >> 16) : 0.0f;
+            }
+            float p[GM];
+#pragma unroll
+            for (int h = 0; h < GM; h += 4) {
+                const float4 t4 = *reinterpret_cast<const float4 *>(&lds_p[t * 16 + h]);
+                p[h] = t4.x;
+                p[h + 1] = t4.y;
+                p[h + 2] = t4.z;
+                p[h + 3] = t4.w;
+            }
+#pragma unroll
+            for (int h = 0; h < GM; ++h)
+#pragma unroll
+                for (int d = 0; d < DP; ++d) acc[h][d] = __builtin_fmaf(p[h], v[d], acc[h][d]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        };
+    BlockRegs ra, rb;
+    fetch(blk0, ra);
+    for (uint32_t blk = blk0; blk < blk1; blk += 2) {
+        fetch(blk + 1, rb);
+        process(blk, ra);
+        if (blk + 1 >= blk1) break;
+        fetch(blk + 2, ra);
+        process(blk + 1, rb);
+    }
+
+    // Sum the four token groups; lanes 0..15 then hold dims col*DP .. of every head.
+#pragma unroll
+    for (int h = 0; h < GM; ++h)
+#pragma unroll
+        for (int d = 0; d < DP; ++d) {
+            acc[h][d] += __shfl_xor(acc[h][d], 16, kWave);
+            acc[h][d] += __shfl_xor(acc[h][d], 32, kWave);
+        }
+    if (grp == 0) lds_h[col] = l;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    if (splits == 1) {
+        if (grp == 0) {
+#pragma unroll
+            for (int h = 0; h < GM; ++h) {
+                if ((uint32_t)h >= G) break;
+                const float lh = lds_h[h];
+                const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+                typename O::T *o = out + ((size_t)b * n_heads + (size_t)g * G + h) * HD + col * DP;
+                float r[DP];
+#pragma unroll
+                for (int d = 0; d < DP; ++d) r[d] = lh > 0.0f ? acc[h][d] * inv : 0.0f;
+                store_f32<O, DP>(o, r);
+            }
+        }
+    } else {
+        // partial record per (b, g, s, head slot): HD sums, then m, l
+        float *rec = part + ((size_t)bg * splits + s) * GM * (HD + 2);
+        if (grp == 0) {
+#pragma unroll
+            for (int h = 0; h < GM; ++h) {
+                if ((uint32_t)h >= G) break;
+#pragma unroll
+                for (int d = 0; d < DP; ++d) rec[h * (HD + 2) + col * DP + d] = acc[h][d];
+            }
+            if (col < G) {
+                rec[col * (HD + 2) + HD] = m;
+                rec[col * (HD + 2) + HD + 1] = l;
+            }
+        }
+    }
+}
+
+// Combine the splits of one (b, query head): M = max m_s, w_s = exp(m_s - M),
+// out = sum w_s acc_s / sum w_s l_s.  256 threads: the split maxima and
+// weights are formed in parallel through LDS, then thread d sums dimension d.
+constexpr int kCombineThreads = 256;
+constexpr uint32_t kMaxSplits = 128;
+
+template <typename O, int HD, int GM>
+__global__ __launch_bounds__(kCombineThreads) void paged_decode_combine(const float *__restrict__ part,
+                                                                        typename O::T *__restrict__ out,
+                                                                        uint32_t n_heads, uint32_t n_kv,
+                                                                        uint32_t splits) {
+    __shared__ float w_lds[kMaxSplits];
+    __shared__ float red[kCombineThreads / kWave];
+    const uint32_t bh = blockIdx.x, h = bh % n_heads, b = bh / n_heads;
+    const uint32_t G = n_heads / n_kv, g = h / G, slot = h % G;
+    constexpr uint32_t kRec = GM * (HD + 2);
+    const float *base = part + ((size_t)(b * n_kv + g) * splits) * kRec + slot * (HD + 2);
+    const uint32_t t = threadIdx.x;
+    const float ms = t < splits ? base[(size_t)t * kRec + HD] : -__builtin_inff();
+    float M = wave_max(ms);
+    if (t % kWave == 0) red[t / kWave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float w = (t < splits && ms > -__builtin_inff()) ? __expf(ms - M) : 0.0f;
+    if (t < splits) w_lds[t] = w;
+    const float lw = t < splits ? w * base[(size_t)t * kRec + HD + 1] : 0.0f;
+    __syncthreads();
+    float L = wave_sum(lw);
+    __syncthreads();
+    if (t % kWave == 0) red[t / kWave] = L;
+    __syncthreads();
+    L = (red[0] + red[1]) + (red[2] + red[3]);
+    if (t < (uint32_t)HD) {
+        float o = 0.0f;
+        for (uint32_t s = 0; s < splits; ++s) o += w_lds[s] * base[(size_t)s * kRec + t];
+        out[((size_t)b * n_heads + h) * HD + t] = O::store(L > 0.0f ? o * (1.0f / L) : 0.0f);
+    }
+}
+
+// Split count: enough wavefronts to cover the chip (~8 per CU) when batch * n_kv is small,
+// at least 16 blocks (256 keys) per split, at most kMaxSplits.
+uint32_t choose_splits(uint32_t batch, uint32_t n_kv, uint32_t max_seq) {
+    const uint32_t pairs = batch * n_kv;
+    const uint32_t blocks = (max_seq + kBlockTokens - 1) / kBlockTokens;
+    uint32_t s = pairs >= 2048 ? 1 : (2048 + pairs - 1) / pairs;
+    const uint32_t cap = blocks / 16 > 0 ? blocks / 16 : 1;
+    if (s > cap) s = cap;
+    if (s > kMaxSplits) s = kMaxSplits;
+    return s ? s : 1;
+}
+
+template <typename Q, typename O, typename C, int HD, int GM>
+int launch_decode(const void *q, void *out, uint32_t batch, uint32_t n_heads, uint32_t n_kv, const uint32_t *lens,
+                  uint32_t max_seq, float scale, uint32_t causal, uint32_t window, const PagedGeom &geo,
+                  float *ws, uint64_t ws_bytes, hipStream_t st) {
+    uint32_t splits = choose_splits(batch, n_kv, max_seq);
+    const uint64_t need = (uint64_t)batch * n_kv * splits * GM * (HD + 2) * 4;
+    if (splits > 1 && (!ws || ws_bytes < need)) splits = 1;
+    const uint32_t blocks = (max_seq + kBlockTokens - 1) / kBlockTokens;
+    const uint32_t bps = (blocks + splits - 1) / splits;
+    hipLaunchKernelGGL((paged_decode_kernel<Q, O, C, HD, GM>), dim3(batch * n_kv * splits), dim3(kWave), 0, st,
+                       static_cast<const typename Q::T *>(q), static_cast<typename O::T *>(out), ws, lens, geo.table, geo,
+                       n_heads, n_kv, scale, causal, window, splits, bps > 0 ? bps : 1);
+    int rc = launch_status();
+    if (rc != FELLM_OK || splits == 1) return rc;
+    hipLaunchKernelGGL((paged_decode_combine<O, HD, GM>), dim3(batch * n_heads), dim3(kCombineThreads), 0, st, ws,
+                       static_cast<typename O::T *>(out), n_heads, n_kv, splits);
+    return launch_status();
+}
+
+template <typename Q, typename O, typename C>
+int dispatch_hd(uint32_t hd, uint32_t G, const void *q, void *out, uint32_t batch, uint32_t n_heads, uint32_t n_kv,
+                const uint32_t *lens, uint32_t max_seq, float scale, uint32_t causal, uint32_t window,
+                const PagedGeom &geo, float *ws, uint64_t ws_bytes, hipStream_t st) {
+#define FELLM_ATT(HDV, GMV)                                                                                    \
+    if (hd == HDV && G <= GMV)                                                                                 \
+        return launch_decode<Q, O, C, HDV, GMV>(q, out, batch, n_heads, n_kv, lens, max_seq, scale, causal, window, \
+                                                 geo, ws, ws_bytes, st);
+    FELLM_ATT(64, 8)
+    FELLM_ATT(64, 16)
+    FELLM_ATT(128, 8)
+    FELLM_ATT(128, 16)
+    FELLM_ATT(256, 8)
+    FELLM_ATT(256, 16)
+#undef FELLM_ATT
+    return FELLM_ERR_SHAPE;
+}
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" uint64_t fellm_rocm_paged_attention_workspace(uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads,
+                                                         uint32_t head_dim, uint32_t max_seq) {
+    using namespace fellm;
+    if (!n_kv_heads || n_heads % n_kv_heads) return 0;
+    const uint32_t splits = choose_splits(batch, n_kv_heads, max_seq);
+    if (splits <= 1) return 0;
+    const uint32_t gm = n_heads / n_kv_heads <= 8 ? 8 : 16;
+    return (uint64_t)batch * n_kv_heads * splits * gm * (head_dim + 2) * 4;
+}
+
+extern "C" int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void *out, uint32_t out_dtype,
+                                          uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                                          const uint32_t *row_lengths, uint32_t max_seq, float scale,
+                                          uint32_t causal, uint32_t window, const FellmRocmPagedKv *kv,
+                                          float *workspace, uint64_t workspace_bytes, void *stream) {
+    using namespace fellm;
+    if (!q || !out || !row_lengths || !kv || !kv->arena || !kv->block_table) return FELLM_ERR_ARITY;
+    if (!n_kv_heads || n_heads % n_kv_heads || n_heads / n_kv_heads > 16) return FELLM_ERR_SHAPE;
+    if (kv->stride != n_kv_heads * head_dim || kv->block_size != kBlockTokens) return FELLM_ERR_SHAPE;
+    if (kv->block_bytes < 2ull * kv->block_size * kv->stride * 2 || kv->block_bytes % 16) return FELLM_ERR_SHAPE;
+    if (kv->layer >= kv->n_layers) return FELLM_ERR_SHAPE;
+    if (!aligned_to(kv->arena, 16) || !aligned_to(q, 16) || !aligned_to(out, 16)) return FELLM_ERR_SHAPE;
+    if (batch == 0) return FELLM_OK;
+    if (!(scale > 0.0f)) scale = 1.0f / sqrtf((float)head_dim);
+    const PagedGeom geo{static_cast<const uint8_t *>(kv->arena), kv->arena_len, kv->block_table, kv->n_block_table,
+                        kv->n_logical_blocks, kv->n_layers, kv->layer, kv->block_size, kv->block_bytes, kv->stride};
+    hipStream_t st = as_stream(stream);
+    const uint32_t G = n_heads / n_kv_heads;
+    if (kv->kv_dtype != FELLM_DTYPE_F16 && kv->kv_dtype != FELLM_DTYPE_BF16) return FELLM_ERR_DTYPE;
+    const bool bf = kv->kv_dtype == FELLM_DTYPE_BF16;
+#define FELLM_ATT_QO(QD, QT, OD, OT)                                                                              \
+    if (q_dtype == QD && out_dtype == OD)                                                                         \
+        return bf ? dispatch_hd<QT, OT, CacheBF16>(head_dim, G, q, out, batch, n_heads, n_kv_heads, row_lengths,  \
+                                                   max_seq, scale, causal, window, geo, workspace, workspace_bytes, \
+                                                   st)                                                            \
+                  : dispatch_hd<QT, OT, CacheF16>(head_dim, G, q, out, batch, n_heads, n_kv_heads, row_lengths,   \
+                                                  max_seq, scale, causal, window, geo, workspace, workspace_bytes,  \
+                                                  st);
+    FELLM_ATT_QO(FELLM_DTYPE_F32, F32, FELLM_DTYPE_F32, F32)
+    FELLM_ATT_QO(FELLM_DTYPE_F16, F16, FELLM_DTYPE_F16, F16)
+    FELLM_ATT_QO(FELLM_DTYPE_BF16, BF16, FELLM_DTYPE_BF16, BF16)
+    FELLM_ATT_QO(FELLM_DTYPE_F16, F16, FELLM_DTYPE_F32, F32)
+    FELLM_ATT_QO(FELLM_DTYPE_BF16, BF16, FELLM_DTYPE_F32, F32)
+#undef FELLM_ATT_QO
+    return FELLM_ERR_DTYPE;
+}

@@ -82,6 +82,7 @@ struct State {
     std::map<std::pair<uintptr_t, size_t>, uint64_t> external;   // registered device tensors
     Mirror step_params;
     Mirror scratch;                                              // per-launch small uploads
+    Mirror attn_ws;                                              // split-key attention partial sums
     void *pinned = nullptr;                                      // host staging for `scratch`
     size_t pinned_bytes = 0;
     bool host_reads_pending = false;  // an H2D copy may still read caller memory
@@ -409,9 +410,11 @@ int launch_rope(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_
 
 // Paged geometry from the host snapshot (paged_ctx.rs:14-53); the arena must
 // be device-resident (the ROCm backend allocates it in HBM).
+// n_pos: entries staged from each positions array (0: the snapshot's batch size).
 FellmRocmPagedKv paged_geometry(State &st, const FellmPagedKvSnapshot &snap, uint32_t layer, uint32_t kv_dtype,
                                 std::vector<void *> &staged, const uint32_t *positions_a,
-                                const uint32_t *positions_b) {
+                                const uint32_t *positions_b, size_t n_pos = 0) {
+    const size_t npos = n_pos ? n_pos : snap.batch_size;
     if (!snap.device_arena || snap.device_arena_len == 0) fail(FELLM_ERR_PAGED_NO_DEVICE);
     if (snap.elem_bytes != 2 || !snap.block_table || snap.block_size == 0 || snap.tokens_stride == 0)
         fail(FELLM_ERR_PAGED_RANGE);
@@ -419,11 +422,11 @@ FellmRocmPagedKv paged_geometry(State &st, const FellmPagedKvSnapshot &snap, uin
     std::vector<size_t> sizes{snap.n_block_table * 4};
     if (positions_a) {
         srcs.push_back(positions_a);
-        sizes.push_back(snap.batch_size * 4);
+        sizes.push_back(npos * 4);
     }
     if (positions_b) {
         srcs.push_back(positions_b);
-        sizes.push_back(snap.batch_size * 4);
+        sizes.push_back(npos * 4);
     }
     stage_small(st, srcs, sizes, staged);
     FellmRocmPagedKv kv{};
@@ -521,6 +524,54 @@ int launch_rope_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, ui
                                        static_cast<const uint32_t *>(staged[1]), &kv, err, stream_ptr(st)));
         finish_outputs(st, out, has_kout ? 2 : 1);
         check(read_err(st));
+    });
+}
+
+// Attention [q, k, v] -> out in its paged decode form (block_size > 0 with a
+// paged context): backend.rs:1244-1368 and the CUDA plugin's paged decode
+// paths (launchers.rs:3243-3560).  A physical batch (batch_size > 1 or q wider
+// than one row) attends row r to row_lengths[r] keys, causal with
+// attention_window; a single sequence attends to past_len + 1 keys, causal
+// when attention_mode == 0.  K/V come from the device arena (f16, or bf16 when
+// cast_to is BF16, as rope_kv_write writes it).  Contiguous-KV and canvas
+// attention are not provided (-10).
+int launch_attention(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                     uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 1, 1, true, [&](State &st) {
+        const FellmOpAttrs &a = *attrs;
+        if (a.block_size == 0 || (a.attention_mode == 1 && n_in >= 5)) fail(FELLM_ERR_DTYPE);
+        FellmPagedKvSnapshot snap;
+        if (!snapshot(st, snap)) fail(FELLM_ERR_PAGED_MISSING);
+        const uint32_t dt = in[0].dtype, odt = out[0].dtype;
+        const size_t nh = a.n_heads ? a.n_heads : 1, nkv = a.n_kv_heads ? a.n_kv_heads : 1, hd = a.head_dim;
+        if (!hd) fail(FELLM_ERR_SHAPE);
+        const size_t width = nh * hd, qn = elems(in[0], dt);
+        const bool batched = snap.batch_size > 1 || qn > width;
+        const size_t batch = batched ? snap.batch_size : 1;
+        if (qn != batch * width || elems(out[0], odt) != qn) fail(FELLM_ERR_SHAPE);
+        std::vector<uint32_t> lens(batch);
+        if (batched) {
+            if (!snap.row_lengths) fail(FELLM_ERR_PAGED_MISSING);
+            std::memcpy(lens.data(), snap.row_lengths, batch * 4);
+        } else {
+            lens[0] = a.past_len + 1;
+        }
+        uint32_t max_seq = 1;
+        for (uint32_t v : lens) max_seq = v > max_seq ? v : max_seq;
+        const uint32_t causal = batched ? 1u : (a.attention_mode == 0 ? 1u : 0u);
+        const uint32_t kv_dt = a.cast_to == FELLM_DTYPE_BF16 ? FELLM_DTYPE_BF16 : FELLM_DTYPE_F16;
+        void *q = ensure_input(st, in[0]);
+        std::vector<void *> staged;
+        FellmRocmPagedKv kv = paged_geometry(st, snap, a.layer_ord, kv_dt, staged, lens.data(), nullptr, batch);
+        const uint64_t ws = fellm_rocm_paged_attention_workspace((uint32_t)batch, (uint32_t)nh, (uint32_t)nkv,
+                                                                 (uint32_t)hd, max_seq);
+        if (ws) ensure_capacity(st.attn_ws, ws);
+        void *o = ensure_output(st, out[0]);
+        check(fellm_rocm_paged_attention(q, dt, o, odt, (uint32_t)batch, (uint32_t)nh, (uint32_t)nkv, (uint32_t)hd,
+                                         static_cast<const uint32_t *>(staged[1]), max_seq, a.scale, causal,
+                                         a.attention_window, &kv, ws ? static_cast<float *>(st.attn_ws.dev) : nullptr,
+                                         ws, stream_ptr(st)));
+        finish_outputs(st, out, 1);
     });
 }
 
@@ -761,6 +812,10 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
             {FELLM_OP_GATE_UP_SWIGLU, {Q5K, Q6K, F32}, F32, launch_gate_up_swiglu},
             {FELLM_OP_GATE_UP_SWIGLU, {Q6K, Q4K, F32}, F32, launch_gate_up_swiglu},
             {FELLM_OP_GATE_UP_SWIGLU, {Q6K, Q5K, F32}, F32, launch_gate_up_swiglu},
+            // Paged decode attention (launchers.rs:3243; lib.rs:537-546 registers [F32, F32, F32]).
+            {FELLM_OP_ATTENTION, {F32, F32, F32}, F32, launch_attention},
+            {FELLM_OP_ATTENTION, {F16, F16, F16}, F16, launch_attention},
+            {FELLM_OP_ATTENTION, {BF16, BF16, BF16}, BF16, launch_attention},
             // Fused custom ops (OpKind::custom("rocm", ...)).
             {kOpAddRmsNorm, {F32, F32, F32}, F32, launch_add_rmsnorm},
             {kOpAddRmsNorm, {F16, F16, F32}, F16, launch_add_rmsnorm},

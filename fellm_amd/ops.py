@@ -214,6 +214,27 @@ def rope_kv_write(q, k, v, inv_freqs, kv_positions, cache: PagedKvCache, *, head
     return q_out
 
 
+def paged_attention(q, row_lengths, cache: PagedKvCache, *, n_heads: int, n_kv_heads: int, head_dim: int,
+                    max_seq: int, layer: int = 0, scale: float = 0.0, causal: bool = True, window: int = 0,
+                    out=None, out_dtype=None, workspace=None):
+    """Paged decode attention: q [batch, n_heads*head_dim] against each row's cache
+    (row_lengths int32 device [batch], max_seq >= every length).  Returns out
+    [batch, n_heads*head_dim] in out_dtype (default: q's dtype)."""
+    _dev(q, row_lengths)
+    batch = q.shape[0]
+    out_dtype = out_dtype or q.dtype
+    out = out if out is not None else torch.empty((batch, n_heads * head_dim), dtype=out_dtype, device=q.device)
+    need = _lib.lib().fellm_rocm_paged_attention_workspace(batch, n_heads, n_kv_heads, head_dim, max_seq)
+    if workspace is None and need:
+        workspace = torch.empty(need // 4, dtype=torch.float32, device=q.device)
+    ws_bytes = workspace.numel() * 4 if workspace is not None else 0
+    kv = cache.c_struct(layer)
+    _lib.call("fellm_rocm_paged_attention", _p(q), _code(q), _p(out), _code(out), batch, n_heads, n_kv_heads,
+              head_dim, _p(row_lengths), max_seq, scale, int(causal), window, C.byref(kv), _p(workspace), ws_bytes,
+              _stream())
+    return out
+
+
 def router_topk(logits, k: int, *, gating_func: int = 1, norm_topk_prob: bool = True,
                 routed_scaling_factor: float = 0.0, ids=None, weights=None):
     """Softmax/sigmoid gate + top-k + renorm: returns (ids int32 [T, k], weights f32 [T, k])."""

@@ -182,6 +182,35 @@ int fellm_rocm_matvec_kquant(const void *w, uint32_t w_dtype, uint32_t rows, uin
                              float *y, void *stream);
 
 /*
+ * Paged decode attention: one query token per batch row against that row's
+ * paged K/V cache (the layout fellm_rocm_rope_kv_write / fellm_rocm_kv_write
+ * fill).  Row b attends to keys 0 .. row_lengths[b]-1 (when causal and
+ * window > 0, only the last `window` of them); query head h uses KV head
+ * h / (n_heads / n_kv_heads); out = softmax(q . K^T * scale) . V with
+ * scale <= 0 meaning 1/sqrt(head_dim).
+ * replaces: crates/backend-cpu/src/backend.rs:1244-1368 (launch_attention, paged
+ * decode arms) and the CUDA plugin's attention_paged_batch_heads /
+ * attention_paged_heads paths (plugins/cuda_kernels/src/launchers.rs:3243-3560);
+ * oracle crates/fellm-plugin-abi/src/attention_provider.rs:391-459.
+ * q [batch, n_heads, head_dim] (F32, F16 or BF16), out same shape (the q dtype, or
+ * F32); row_lengths u32 [batch] in device memory, max_seq >= every length;
+ * head_dim 64, 128 or 256; n_heads / n_kv_heads <= 16; kv->block_size 16,
+ * kv->stride = n_kv_heads * head_dim, kv_dtype F16 or BF16.
+ * workspace: fellm_rocm_paged_attention_workspace() bytes for split-key
+ * partial sums (used when batch * n_kv_heads is small); with a null or short
+ * workspace every (row, KV head) runs in one wavefront.
+ * Products with the f16 cache are exact (q split into f16 high/low parts on
+ * the matrix cores); accumulation, exp and the softmax run in f32.
+ */
+uint64_t fellm_rocm_paged_attention_workspace(uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads,
+                                              uint32_t head_dim, uint32_t max_seq);
+int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void *out, uint32_t out_dtype, uint32_t batch,
+                               uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, const uint32_t *row_lengths,
+                               uint32_t max_seq, float scale, uint32_t causal, uint32_t window,
+                               const FellmRocmPagedKv *kv, float *workspace, uint64_t workspace_bytes,
+                               void *stream);
+
+/*
  * Self-check of the device expf restatement: out[i] = expf(in[i]) on the GPU.
  * Diagnostic only (no counterpart in the reference).
  */

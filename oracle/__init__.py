@@ -56,6 +56,8 @@ def lib() -> C.CDLL:
             "oracle_kquant_row_dot": (F, [U32, P, S, P, P, P]),
             "oracle_matvec_kquant": (C.c_int, [U32, P, S, S, P, P]),
             "oracle_gate_up_swiglu": (C.c_int, [U32, P, U32, P, S, S, P, P]),
+            "oracle_paged_attention": (C.c_int, [P, P, S, S, S, S, P, F, C.c_int, S, P, S, P, S, S, S, S, S, S,
+                                                 C.c_int]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(l, name)
@@ -285,4 +287,23 @@ def gate_up_swiglu(gate_dtype: int, gate_w: np.ndarray, up_dtype: int, up_w: np.
     rc = lib().oracle_gate_up_swiglu(gate_dtype, _p(g), up_dtype, _p(u), rows, cols, _p(xx), _p(out))
     if rc:
         raise ValueError(f"oracle_gate_up_swiglu rc={rc}")
+    return out
+
+
+# ---- next: paged decode attention ---------------------------------------------
+def paged_attention(q: np.ndarray, n_heads: int, n_kv: int, head_dim: int, row_lengths: np.ndarray, scale: float,
+                    arena: np.ndarray, table: np.ndarray, n_logical: int, n_layers: int, layer: int, block_size: int,
+                    block_bytes: int, causal: bool = True, window: int = 0, kind: str = "f16") -> np.ndarray:
+    """reference_attention_paged_f32 per batch row over the paged arena: q f32 [B, n_heads*head_dim]."""
+    qq = _c(q, np.float32)
+    B = len(row_lengths)
+    out = np.empty((B, n_heads * head_dim), np.float32)
+    rl = _c(row_lengths, np.uint32)
+    ar = _c(arena, np.uint8)
+    tb = _c(table, np.uint32)
+    rc = lib().oracle_paged_attention(_p(qq), _p(out), B, n_heads, n_kv, head_dim, _p(rl), scale, int(causal),
+                                      window, _p(ar), ar.size, _p(tb), tb.size, n_logical, n_layers, layer,
+                                      block_size, block_bytes, 1 if kind == "bf16" else 0)
+    if rc:
+        raise ValueError(f"oracle_paged_attention rc={rc}")
     return out

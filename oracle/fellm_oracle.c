@@ -637,3 +637,62 @@ int oracle_gate_up_swiglu(uint32_t gate_dtype, const uint8_t *gate_w, uint32_t u
     free(u);
     return rc;
 }
+
+/* ---- next: paged decode attention -----------------------------------------
+ * crates/fellm-plugin-abi/src/attention_provider.rs:391-459
+ * (reference_attention_paged_f32, the ABI's declared attention oracle): per
+ * query head h (kv head h / (n_heads / n_kv)), a serial online softmax over
+ * keys t = 0 .. seq-1, skipping t when causal && window > 0 &&
+ * seq-1-t >= window; score = (sum_d q[d]*k[d] in d order) * scale;
+ * m_new = max(m, score); alpha = m finite ? exp(m - m_new) : 0;
+ * p = exp(score - m_new); when alpha != 1 the output row and l are scaled by
+ * alpha; out += p * v; l += p; finally out *= 1/l when l > 0.
+ * Driven per batch row as backend.rs:1286-1323 does (seq = row_lengths[row],
+ * causal, window = attention_window); K/V rows from paged_ctx.rs:138-174
+ * (K rows of a block first, then its V rows, stride = n_kv * head_dim
+ * elements).  elem: 0 = f16 cache (reference), 1 = bf16 (extension). */
+int oracle_paged_attention(const float *q, float *out, size_t batch, size_t n_heads, size_t n_kv, size_t hd,
+                           const uint32_t *row_lengths, float scale, int causal, size_t window, const uint8_t *arena,
+                           size_t arena_len, const uint32_t *table, size_t n_table, size_t n_logical, size_t n_layers,
+                           size_t layer, size_t block_size, size_t block_bytes, int elem) {
+    const size_t nk = n_kv ? n_kv : 1, group = n_heads / nk ? n_heads / nk : 1, stride = nk * hd;
+    const size_t row_bytes = stride * 2;
+    for (size_t r = 0; r < batch; ++r) {
+        const size_t seq = row_lengths[r];
+        for (size_t h = 0; h < n_heads; ++h) {
+            const size_t g = h / group;
+            const float *qr = q + (r * n_heads + h) * hd;
+            float *o = out + (r * n_heads + h) * hd;
+            for (size_t d = 0; d < hd; ++d) o[d] = 0.0f;
+            float m = -INFINITY, l = 0.0f;
+            for (size_t t = 0; t < seq; ++t) {
+                if (causal && window > 0 && (seq - 1 - t) >= window) continue;
+                const size_t logical = t / block_size, slot = t % block_size;
+                const size_t idx = (r * n_layers + layer) * n_logical + logical;
+                if (logical >= n_logical || idx >= n_table) return -22;
+                const size_t base = (size_t)table[idx] * block_bytes + slot * row_bytes;
+                if (base + block_size * row_bytes + row_bytes > arena_len) return -22;
+                const uint16_t *kr = (const uint16_t *)(arena + base) + g * hd;
+                const uint16_t *vr = (const uint16_t *)(arena + base + block_size * row_bytes) + g * hd;
+                float score = 0.0f;
+                for (size_t d = 0; d < hd; ++d) score += qr[d] * (elem ? bf16_to_f32(kr[d]) : f16_to_f32(kr[d]));
+                score *= scale;
+                const float m_new = score > m ? score : m;
+                const float alpha = isfinite(m) ? expf(m - m_new) : 0.0f;
+                const float p = expf(score - m_new);
+                if (alpha != 1.0f) {
+                    for (size_t d = 0; d < hd; ++d) o[d] *= alpha;
+                    l *= alpha;
+                }
+                for (size_t d = 0; d < hd; ++d) o[d] += p * (elem ? bf16_to_f32(vr[d]) : f16_to_f32(vr[d]));
+                l += p;
+                m = m_new;
+            }
+            if (l > 0.0f) {
+                const float inv = 1.0f / l;
+                for (size_t d = 0; d < hd; ++d) o[d] *= inv;
+            }
+        }
+    }
+    return 0;
+}

@@ -321,3 +321,40 @@ def test_gate_up_swiglu_shape_errors(host):
                                             tref(g, D.Q4K, [rows, cols], logical_id=901), tref(x, D.F32)],
                          [tmut(out, D.F32)])
     assert rc == abi.ERR_SHAPE
+
+
+def test_attention_paged_batch(host):
+    """Attention [q, k, v] -> out through the paged snapshot (backend.rs:1286-1323
+    batch path): row r attends to row_lengths[r] keys of the device arena."""
+    from test_oracle_attention import build_cache
+
+    rng = np.random.default_rng(41)
+    nh, nkv, hd = 16, 4, 128
+    lengths = [3, 40, 17, 200]
+    k = [rng.normal(size=(n, nkv * hd)).astype(np.float32) for n in lengths]
+    v = [rng.normal(size=(n, nkv * hd)).astype(np.float32) for n in lengths]
+    arena_np, table, n_logical, bb, _, v16 = build_cache(rng, k, v)
+    arena = torch.from_numpy(arena_np).to("cuda")
+    _KEEP.append(arena)
+    q = rng.normal(size=(len(lengths), nh * hd)).astype(np.float32)
+    lens = np.array(lengths, np.uint32)
+    ctx = PagedKvContext(arena_ptr=arena_np.ctypes.data, arena_len=arena_np.size, block_table=table,
+                         n_logical_blocks=n_logical, n_layers=1, tokens_stride=nkv * hd, block_bytes=bb,
+                         block_size=16, row_positions=lens - 1, row_rope_positions=lens - 1, row_lengths=lens,
+                         device_arena_ptr=arena.data_ptr(), device_arena_len=arena.numel())
+    ctx._keep = (arena_np,)
+    host.set_paged_context(ctx)
+    try:
+        out = np.zeros_like(q)
+        dummy = np.zeros(1, np.float32)
+        run(host, abi.OpKind.ATTENTION, [D.F32, D.F32, D.F32], D.F32,
+            abi.OpAttrs(n_heads=nh, n_kv_heads=nkv, head_dim=hd, block_size=16, attention_window=0),
+            [tref(q, D.F32), tref(dummy, D.F32), tref(dummy, D.F32)], [tmut(out, D.F32)])
+        got = materialize(host, out, D.F32)
+    finally:
+        host.set_paged_context(None)
+    ref = oracle.paged_attention(q, nh, nkv, hd, lens, float(np.float32(1 / np.sqrt(hd))), arena_np, table,
+                                 n_logical, 1, 0, 16, bb)
+    for r in range(len(lengths)):
+        tol = 2e-5 * np.abs(v16[r]).max() + np.abs(ref[r]) * 2.0 ** -23
+        assert np.all(np.abs(got[r] - ref[r]) <= tol), (r, np.abs(got[r] - ref[r]).max())
