@@ -56,6 +56,9 @@ def lib() -> C.CDLL:
             "oracle_kquant_row_dot": (F, [U32, P, S, P, P, P]),
             "oracle_matvec_kquant": (C.c_int, [U32, P, S, S, P, P]),
             "oracle_gate_up_swiglu": (C.c_int, [U32, P, U32, P, S, S, P, P]),
+            "oracle_moe_dispatch": (C.c_int, [P, S, S, S, P, P, P, P]),
+            "oracle_moe_gather": (None, [P, S, S, S, P, P]),
+            "oracle_moe_combine": (None, [P, P, P, P, P, S, S, S, P]),
             "oracle_paged_attention": (C.c_int, [P, P, S, S, S, S, P, F, C.c_int, S, P, S, P, S, S, S, S, S, S,
                                                  C.c_int]),
         }
@@ -306,4 +309,39 @@ def paged_attention(q: np.ndarray, n_heads: int, n_kv: int, head_dim: int, row_l
                                       block_size, block_bytes, 1 if kind == "bf16" else 0)
     if rc:
         raise ValueError(f"oracle_paged_attention rc={rc}")
+    return out
+
+
+# ---- next: MoE dispatch / gather / combine -------------------------------------
+def moe_dispatch(ids: np.ndarray, n_experts: int):
+    """ids u32 [tokens, k] -> (counts [E], offsets [E+1], order [T*k], inv [T*k])."""
+    ii = _c(ids, np.uint32)
+    tokens, k = ii.shape
+    counts = np.empty(n_experts, np.uint32)
+    offsets = np.empty(n_experts + 1, np.uint32)
+    order = np.empty(tokens * k, np.uint32)
+    inv = np.empty(tokens * k, np.uint32)
+    rc = lib().oracle_moe_dispatch(_p(ii), tokens, k, n_experts, _p(counts), _p(offsets), _p(order), _p(inv))
+    if rc:
+        raise ValueError(f"oracle_moe_dispatch rc={rc}")
+    return counts, offsets, order, inv
+
+
+def moe_gather(x: np.ndarray, k: int, order: np.ndarray) -> np.ndarray:
+    xx = _c(x, np.float32)
+    tokens, h = xx.shape
+    out = np.empty((tokens * k, h), np.float32)
+    oo = _c(order, np.uint32)
+    lib().oracle_moe_gather(_p(xx), tokens, k, h, _p(oo), _p(out))
+    return out
+
+
+def moe_combine(y0: np.ndarray, expert_out: np.ndarray, ids: np.ndarray, weights: np.ndarray,
+                inv: np.ndarray) -> np.ndarray:
+    yy = _c(y0, np.float32)
+    tokens, h = yy.shape
+    k = ids.shape[1]
+    eo, ii, ww, iv = _c(expert_out, np.float32), _c(ids, np.uint32), _c(weights, np.float32), _c(inv, np.uint32)
+    out = np.empty_like(yy)
+    lib().oracle_moe_combine(_p(yy), _p(eo), _p(ii), _p(ww), _p(iv), tokens, k, h, _p(out))
     return out

@@ -696,3 +696,68 @@ int oracle_paged_attention(const float *q, float *out, size_t batch, size_t n_he
     }
     return 0;
 }
+
+/* ---- next: MoE dispatch / gather / combine around the expert FFNs ---------
+ * crates/backend-cpu/src/kernels/moe.rs:839-848 groups the routed assignments
+ * per expert while walking tokens in order and each token's selected experts
+ * in rank order (groups[expert].push((token, weight))), so inside an expert
+ * the assignments a = token * k + slot appear in ascending a; moe.rs:954-957
+ * copies each group's x rows; moe.rs:1024-1033 adds every group's outputs
+ * into y expert by expert (value += weight * contribution, no FMA), so a
+ * token's contributions arrive in ascending expert id order.  The CUDA
+ * plugin's count / prefix / scatter / weighted-reduce kernels
+ * (oxide_kernels.rs:2289-2327, 2507-2532) compute the same grouping with an
+ * atomic (unordered) scatter and a rank-order reduce from zero. */
+int oracle_moe_dispatch(const uint32_t *ids, size_t tokens, size_t k, size_t n_experts, uint32_t *counts,
+                        uint32_t *offsets, uint32_t *order, uint32_t *inv) {
+    const size_t n = tokens * k;
+    for (size_t e = 0; e < n_experts; ++e) counts[e] = 0;
+    for (size_t a = 0; a < n; ++a) {
+        if (ids[a] >= n_experts) return -2;
+        counts[ids[a]]++;
+    }
+    uint32_t run = 0;
+    for (size_t e = 0; e < n_experts; ++e) {
+        offsets[e] = run;
+        run += counts[e];
+    }
+    offsets[n_experts] = run;
+    uint32_t *cursor = calloc(n_experts, sizeof(uint32_t));
+    for (size_t a = 0; a < n; ++a) {
+        const uint32_t e = ids[a], pos = offsets[e] + cursor[e]++;
+        order[pos] = (uint32_t)a;
+        inv[a] = pos;
+    }
+    free(cursor);
+    return 0;
+}
+
+/* grouped[i] = x[order[i] / k] (moe.rs:954-957), f32 rows of width h. */
+void oracle_moe_gather(const float *x, size_t tokens, size_t k, size_t h, const uint32_t *order, float *grouped) {
+    for (size_t i = 0; i < tokens * k; ++i) memcpy(grouped + i * h, x + (size_t)(order[i] / k) * h, h * sizeof(float));
+}
+
+/* y[t] = y0[t] + sum over t's assignments in ascending expert id of
+ * weight * expert_out[inv[a]] (moe.rs:1024-1033). */
+void oracle_moe_combine(const float *y0, const float *expert_out, const uint32_t *ids, const float *weights,
+                        const uint32_t *inv, size_t tokens, size_t k, size_t h, float *y) {
+    for (size_t t = 0; t < tokens; ++t) {
+        float *yr = y + t * h;
+        memcpy(yr, y0 + t * h, h * sizeof(float));
+        size_t done = 0;
+        uint32_t last = 0;
+        while (done < k) {  /* next slot in ascending expert id */
+            size_t best = k;
+            for (size_t s = 0; s < k; ++s) {
+                const uint32_t e = ids[t * k + s];
+                if ((done == 0 || e > last) && (best == k || e < ids[t * k + best])) best = s;
+            }
+            if (best == k) break;
+            const float w = weights[t * k + best];
+            const float *src = expert_out + (size_t)inv[t * k + best] * h;
+            for (size_t d = 0; d < h; ++d) yr[d] += w * src[d];
+            last = ids[t * k + best];
+            ++done;
+        }
+    }
+}
