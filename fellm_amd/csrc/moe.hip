@@ -1,0 +1,405 @@
+// MoE dispatch around the expert FFNs: group the routed (token, slot)
+// assignments per expert, gather the token rows into that grouped order, and
+// add the weighted expert outputs back into the token rows.
+//
+// Reference behaviour:
+//   grouping   crates/backend-cpu/src/kernels/moe.rs:839-848 pushes
+//              (token, weight) onto groups[expert] walking tokens in order, so
+//              inside one expert the assignments a = token * top_k + slot come
+//              in ascending a.  plugins/cuda_kernels/src/oxide_kernels.rs:
+//              2283-2327 (fill_u32 / moe_count_assignments /
+//              moe_prefix_offsets / moe_scatter_assignments) computes the same
+//              counts and offsets but scatters with an atomic cursor, so its
+//              order inside an expert varies run to run.  Here the order is the
+//              CPU backend's, deterministically: a stable counting sort.
+//   gather     moe.rs:954-957 copies each group's x rows.
+//   combine    moe.rs:1024-1033: y[token] += weight * out, group by group,
+//              i.e. a token's contributions arrive in ascending expert id
+//              (grouped rows, located through inv).  oxide_kernels.rs:2507-2532
+//              (moe_weighted_reduce): value = 0; value += score * out in slot
+//              order, with out indexed by assignment.  Both orders are offered;
+//              neither contracts the multiply-add into an FMA, as the
+//              reference's Rust does not.
+//
+// Layout: ids / weights are [tokens][top_k] u32 / f32 (assignment-major, as
+// the router writes them); counts [E], offsets [E + 1], order [A] and inv [A]
+// are u32 with A = tokens * top_k; rows are contiguous, `hidden` elements.
+//
+// The dispatch is integer work over A * 4 bytes of ids: it is launch- and
+// latency-bound, not HBM-bound.  Chunks of kChunk assignments go to one
+// wavefront each; inside a chunk the rank of an assignment among the earlier
+// ones with the same expert is found 64 lanes at a time with ballots over the
+// expert id's bits (lanes whose ids agree on every bit are peers).
+#include "common.hpp"
+
+namespace fellm {
+namespace {
+
+constexpr uint32_t kChunkRounds = 8;
+constexpr uint32_t kChunk = kWave * kChunkRounds;  // assignments per wavefront
+constexpr uint32_t kMoeMaxExperts = 4096;
+constexpr uint32_t kMoeMaxTopK = 64;
+constexpr uint32_t kInvalid = 0xffffffffu;
+constexpr int kScanBlock = 1024;
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+// Counts of the valid ids of chunk c into cnt[E] (LDS, zeroed by the caller).
+__device__ __forceinline__ void count_chunk(const uint32_t *__restrict__ ids, uint64_t n, uint32_t E, uint64_t c,
+                                            uint32_t *cnt, uint32_t *err) {
+    const uint32_t lane = lane_id();
+    bool bad = false;
+#pragma unroll
+    for (uint32_t r = 0; r < kChunkRounds; ++r) {
+        const uint64_t a = c * kChunk + r * kWave + lane;
+        if (a < n) {
+            const uint32_t id = ids[a];
+            if (id < E)
+                atomicAdd(&cnt[id], 1u);
+            else
+                bad = true;
+        }
+    }
+    if (bad && err) atomicOr(err, 1u);
+}
+
+// Scatter of chunk c: cur[e] (LDS) holds the next free grouped position of
+// expert e for this chunk.  Assignments are placed in ascending index.
+__device__ __forceinline__ void scatter_chunk(const uint32_t *__restrict__ ids, uint64_t n, uint32_t E, uint32_t bits,
+                                              uint64_t c, uint32_t *cur, uint32_t *__restrict__ order,
+                                              uint32_t *__restrict__ inv) {
+    const uint32_t lane = lane_id();
+    const uint64_t lt = (1ull << lane) - 1ull;
+    for (uint32_t r = 0; r < kChunkRounds; ++r) {
+        const uint64_t a = c * kChunk + r * kWave + lane;
+        uint32_t id = a < n ? ids[a] : kInvalid;
+        const bool valid = id < E;
+        if (!valid && a < n && inv) inv[a] = kInvalid;
+        uint64_t peers = __ballot(valid);
+        if (peers == 0) continue;  // wave-uniform: no valid id this round
+        for (uint32_t b = 0; b < bits; ++b) {
+            const bool bit = (id >> b) & 1u;
+            const uint64_t ones = __ballot(bit);
+            peers &= bit ? ones : ~ones;
+        }
+        uint32_t base = 0;
+        if (valid) base = cur[id];
+        // Every lane has read its cursor before the leaders advance them.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t rank = __popcll(peers & lt);
+        if (valid) {
+            if (rank == 0) cur[id] = base + (uint32_t)__popcll(peers);
+            const uint32_t pos = base + rank;
+            order[pos] = (uint32_t)a;
+            if (inv) inv[a] = pos;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// Exclusive scan of v over the wavefront; returns the prefix, *total the sum.
+__device__ __forceinline__ uint32_t wave_exclusive(uint32_t v, uint32_t *total) {
+    const uint32_t lane = lane_id();
+    uint32_t inc = v;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t o = __shfl_up(inc, d);
+        if (lane >= (uint32_t)d) inc += o;
+    }
+    *total = __shfl(inc, kWave - 1);
+    return inc - v;
+}
+
+// A <= kChunk: everything in one wavefront, one launch (the decode case).
+__global__ __launch_bounds__(kWave) void moe_dispatch_one(const uint32_t *__restrict__ ids, uint32_t n, uint32_t E,
+                                                          uint32_t bits, uint32_t *__restrict__ counts,
+                                                          uint32_t *__restrict__ offsets,
+                                                          uint32_t *__restrict__ order, uint32_t *__restrict__ inv,
+                                                          uint32_t *err) {
+    extern __shared__ uint32_t cnt[];
+    const uint32_t lane = lane_id();
+    for (uint32_t e = lane; e < E; e += kWave) cnt[e] = 0;
+    __syncthreads();
+    count_chunk(ids, n, E, 0, cnt, err);
+    __syncthreads();
+    // Exclusive prefix over experts: lane l owns the contiguous run
+    // [l * per, (l + 1) * per).
+    const uint32_t per = (E + kWave - 1) / kWave;
+    const uint32_t lo = min(E, lane * per), hi = min(E, lo + per);
+    uint32_t s = 0;
+    for (uint32_t e = lo; e < hi; ++e) s += cnt[e];
+    uint32_t total;
+    uint32_t run = wave_exclusive(s, &total);
+    for (uint32_t e = lo; e < hi; ++e) {
+        const uint32_t c = cnt[e];
+        counts[e] = c;
+        offsets[e] = run;
+        cnt[e] = run;
+        run += c;
+    }
+    if (lane == 0) offsets[E] = total;
+    for (uint32_t i = total + lane; i < n; i += kWave) order[i] = kInvalid;
+    __syncthreads();
+    scatter_chunk(ids, n, E, bits, 0, cnt, order, inv);
+}
+
+// Pass 1: per-chunk counts, bc[c][e].
+__global__ __launch_bounds__(kWave) void moe_count_chunks(const uint32_t *__restrict__ ids, uint64_t n, uint32_t E,
+                                                          uint32_t *__restrict__ bc, uint32_t *err) {
+    extern __shared__ uint32_t cnt[];
+    const uint32_t lane = lane_id();
+    const uint64_t c = blockIdx.x;
+    for (uint32_t e = lane; e < E; e += kWave) cnt[e] = 0;
+    __syncthreads();
+    count_chunk(ids, n, E, c, cnt, err);
+    __syncthreads();
+    for (uint32_t e = lane; e < E; e += kWave) bc[c * E + e] = cnt[e];
+}
+
+// Pass 2 (one block): bc[c][e] becomes the exclusive prefix over chunks,
+// counts[e] the column sum, offsets the exclusive prefix over experts.
+__global__ __launch_bounds__(kScanBlock) void moe_scan_chunks(uint32_t *__restrict__ bc, uint32_t nchunks, uint32_t E,
+                                                              uint64_t n, uint32_t *__restrict__ counts,
+                                                              uint32_t *__restrict__ offsets,
+                                                              uint32_t *__restrict__ order) {
+    __shared__ uint32_t col[kMoeMaxExperts];
+    __shared__ uint32_t wsum[kScanBlock / kWave];
+    const uint32_t t = threadIdx.x;
+    for (uint32_t e = t; e < E; e += kScanBlock) {
+        uint32_t run = 0;
+        for (uint32_t c = 0; c < nchunks; ++c) {
+            const uint32_t v = bc[(size_t)c * E + e];
+            bc[(size_t)c * E + e] = run;
+            run += v;
+        }
+        counts[e] = run;
+        col[e] = run;
+    }
+    __syncthreads();
+    constexpr uint32_t kPer = kMoeMaxExperts / kScanBlock;
+    const uint32_t lo = min(E, t * kPer), hi = min(E, lo + kPer);
+    uint32_t s = 0;
+    for (uint32_t e = lo; e < hi; ++e) s += col[e];
+    uint32_t wtotal;
+    const uint32_t wpre = wave_exclusive(s, &wtotal);
+    const uint32_t w = t / kWave;
+    if (lane_id() == 0) wsum[w] = wtotal;
+    __syncthreads();
+    uint32_t run = wpre, total = 0;
+    for (uint32_t i = 0; i < kScanBlock / kWave; ++i) {
+        const uint32_t x = wsum[i];
+        if (i < w) run += x;
+        total += x;
+    }
+    for (uint32_t e = lo; e < hi; ++e) {
+        offsets[e] = run;
+        run += col[e];
+    }
+    if (t == 0) offsets[E] = total;
+    for (uint64_t i = total + t; i < n; i += kScanBlock) order[i] = kInvalid;
+}
+
+// Pass 3: stable scatter of each chunk from its cursors.
+__global__ __launch_bounds__(kWave) void moe_scatter_chunks(const uint32_t *__restrict__ ids, uint64_t n, uint32_t E,
+                                                            uint32_t bits, const uint32_t *__restrict__ bc,
+                                                            const uint32_t *__restrict__ offsets,
+                                                            uint32_t *__restrict__ order, uint32_t *__restrict__ inv) {
+    extern __shared__ uint32_t cur[];
+    const uint32_t lane = lane_id();
+    const uint64_t c = blockIdx.x;
+    for (uint32_t e = lane; e < E; e += kWave) cur[e] = offsets[e] + bc[c * E + e];
+    __syncthreads();
+    scatter_chunk(ids, n, E, bits, c, cur, order, inv);
+}
+
+// grouped[i] = x[order[i] / top_k]; an invalid order entry gives a zero row.
+template <typename V>
+__global__ __launch_bounds__(256) void moe_gather_rows(const V *__restrict__ x, const uint32_t *__restrict__ order,
+                                                       uint64_t n, uint32_t top_k, uint64_t row_vecs,
+                                                       V *__restrict__ grouped) {
+    for (uint64_t i = blockIdx.x; i < n; i += gridDim.x) {
+        const uint32_t a = order[i];
+        V *dst = grouped + i * row_vecs;
+        if (a < n) {
+            const V *src = x + (uint64_t)(a / top_k) * row_vecs;
+            for (uint64_t j = threadIdx.x; j < row_vecs; j += blockDim.x) dst[j] = src[j];
+        } else {
+            for (uint64_t j = threadIdx.x; j < row_vecs; j += blockDim.x) dst[j] = V{};
+        }
+    }
+}
+
+// y[t] = y0[t] (or 0) + sum over t's slots of weight * row, one token per
+// block iteration.  EXPERT_ORDER: slots in ascending (expert id, slot), rows
+// expert_out[inv[a]]; otherwise slot order, rows expert_out[a].
+template <bool EXPERT_ORDER, int VEC>
+__global__ __launch_bounds__(256) void moe_combine_rows(const float *y0, const float *__restrict__ expert_out,
+                                                        const uint32_t *__restrict__ ids,
+                                                        const float *__restrict__ weights,
+                                                        const uint32_t *__restrict__ inv, uint64_t tokens,
+                                                        uint32_t top_k, uint64_t hidden, uint64_t n_rows, float *y) {
+#pragma clang fp contract(off)
+    using Vec = Pack<float, VEC>;
+    __shared__ float sw[kMoeMaxTopK];
+    __shared__ uint32_t srow[kMoeMaxTopK];
+    const uint32_t t = threadIdx.x;
+    const uint64_t nvec = hidden / VEC;
+    for (uint64_t tok = blockIdx.x; tok < tokens; tok += gridDim.x) {
+        if (t < kWave) {
+            const uint64_t a = tok * top_k + t;
+            uint32_t rank = t, row = kInvalid;
+            float w = 0.0f;
+            if (t < top_k) {
+                w = weights[a];
+                row = (uint32_t)a;
+                if (EXPERT_ORDER) row = inv[a];
+            }
+            if (EXPERT_ORDER) {
+                const uint64_t key = t < top_k ? (uint64_t)ids[a] * kMoeMaxTopK + t : ~0ull;
+                rank = 0;
+                for (uint32_t j = 0; j < top_k; ++j) {
+                    const uint64_t kj = __shfl(key, j);
+                    rank += kj < key;
+                }
+            }
+            if (t < top_k) {
+                sw[rank] = w;
+                srow[rank] = row < n_rows ? row : kInvalid;
+            }
+        }
+        __syncthreads();
+        const uint64_t ybase = tok * nvec;
+        for (uint64_t j = t; j < nvec; j += blockDim.x) {
+            Vec acc;
+            if (y0) {
+                acc = reinterpret_cast<const Vec *>(y0)[ybase + j];
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) acc.v[e] = 0.0f;
+            }
+            for (uint32_t s0 = 0; s0 < top_k; s0 += 8) {
+                Vec r[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t s = s0 + u;
+                    const uint32_t row = s < top_k ? srow[s] : kInvalid;
+                    if (row != kInvalid)
+                        r[u] = reinterpret_cast<const Vec *>(expert_out)[(uint64_t)row * nvec + j];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t s = s0 + u;
+                    if (s < top_k && srow[s] != kInvalid) {
+                        const float w = sw[s];
+#pragma unroll
+                        for (int e = 0; e < VEC; ++e) acc.v[e] = acc.v[e] + w * r[u].v[e];
+                    }
+                }
+            }
+            reinterpret_cast<Vec *>(y)[ybase + j] = acc;
+        }
+        __syncthreads();
+    }
+}
+
+inline uint32_t id_bits(uint32_t E) { return E <= 1 ? 0 : 32 - __builtin_clz(E - 1); }
+
+inline uint64_t nchunks_of(uint64_t n) { return (n + kChunk - 1) / kChunk; }
+
+inline uint32_t grid_cap(uint64_t units, uint64_t cap) { return (uint32_t)(units < cap ? units : cap); }
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" uint64_t fellm_rocm_moe_dispatch_workspace(uint64_t tokens, uint32_t top_k, uint32_t n_experts) {
+    using namespace fellm;
+    const uint64_t n = tokens * top_k;
+    const uint64_t chunks = nchunks_of(n);
+    return chunks <= 1 ? 0 : chunks * n_experts * sizeof(uint32_t);
+}
+
+extern "C" int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32_t n_experts,
+                                       uint32_t *counts, uint32_t *offsets, uint32_t *order, uint32_t *inv,
+                                       uint32_t *err_flag, void *workspace, uint64_t workspace_bytes, void *stream) {
+    using namespace fellm;
+    if (!counts || !offsets) return FELLM_ERR_ARITY;
+    if (n_experts == 0 || n_experts > kMoeMaxExperts || top_k == 0 || top_k > kMoeMaxTopK) return FELLM_ERR_SHAPE;
+    const uint64_t n = tokens * top_k;
+    if (tokens > 0xffffffffull || n >= 0xffffffffull) return FELLM_ERR_SHAPE;
+    if (n && (!ids || !order)) return FELLM_ERR_ARITY;
+    hipStream_t st = as_stream(stream);
+    const uint32_t E = n_experts, bits = id_bits(E);
+    const size_t lds = (size_t)E * sizeof(uint32_t);
+    const uint64_t chunks = nchunks_of(n);
+    if (chunks <= 1) {
+        hipLaunchKernelGGL(moe_dispatch_one, dim3(1), dim3(kWave), lds, st, ids, (uint32_t)n, E, bits, counts,
+                           offsets, order, inv, err_flag);
+        return launch_status();
+    }
+    if (!workspace || workspace_bytes < chunks * E * sizeof(uint32_t)) return FELLM_ERR_SHAPE;
+    if (chunks > 0x7fffffffull) return FELLM_ERR_SHAPE;
+    uint32_t *bc = static_cast<uint32_t *>(workspace);
+    hipLaunchKernelGGL(moe_count_chunks, dim3((uint32_t)chunks), dim3(kWave), lds, st, ids, n, E, bc, err_flag);
+    hipLaunchKernelGGL(moe_scan_chunks, dim3(1), dim3(kScanBlock), 0, st, bc, (uint32_t)chunks, E, n, counts,
+                       offsets, order);
+    hipLaunchKernelGGL(moe_scatter_chunks, dim3((uint32_t)chunks), dim3(kWave), lds, st, ids, n, E, bits, bc,
+                       offsets, order, inv);
+    return launch_status();
+}
+
+extern "C" int fellm_rocm_moe_gather(const void *x, uint32_t elem_bytes, uint64_t tokens, uint32_t top_k,
+                                     uint64_t hidden, const uint32_t *order, void *grouped, void *stream) {
+    using namespace fellm;
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4) return FELLM_ERR_DTYPE;
+    if (top_k == 0 || top_k > kMoeMaxTopK) return FELLM_ERR_SHAPE;
+    const uint64_t n = tokens * top_k;
+    if (tokens > 0xffffffffull || n >= 0xffffffffull) return FELLM_ERR_SHAPE;
+    if (n == 0 || hidden == 0) return FELLM_OK;
+    if (!x || !order || !grouped) return FELLM_ERR_ARITY;
+    hipStream_t st = as_stream(stream);
+    const uint64_t row_bytes = hidden * elem_bytes;
+    const uint32_t grid = grid_cap(n, 8192);
+    if (row_bytes % 16 == 0 && aligned_to(x, 16) && aligned_to(grouped, 16))
+        hipLaunchKernelGGL(moe_gather_rows<uint4>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x),
+                           order, n, top_k, row_bytes / 16, static_cast<uint4 *>(grouped));
+    else if (row_bytes % 4 == 0 && aligned_to(x, 4) && aligned_to(grouped, 4))
+        hipLaunchKernelGGL(moe_gather_rows<uint32_t>, dim3(grid), dim3(256), 0, st,
+                           static_cast<const uint32_t *>(x), order, n, top_k, row_bytes / 4,
+                           static_cast<uint32_t *>(grouped));
+    else
+        hipLaunchKernelGGL(moe_gather_rows<uint8_t>, dim3(grid), dim3(256), 0, st, static_cast<const uint8_t *>(x),
+                           order, n, top_k, row_bytes, static_cast<uint8_t *>(grouped));
+    return launch_status();
+}
+
+extern "C" int fellm_rocm_moe_combine(const float *y0, const float *expert_out, const uint32_t *ids,
+                                      const float *weights, const uint32_t *inv, uint64_t tokens, uint32_t top_k,
+                                      uint64_t hidden, float *y, void *stream) {
+    using namespace fellm;
+    if (top_k == 0 || top_k > kMoeMaxTopK) return FELLM_ERR_SHAPE;
+    const uint64_t n = tokens * top_k;
+    if (tokens > 0xffffffffull || n >= 0xffffffffull) return FELLM_ERR_SHAPE;
+    if (tokens == 0 || hidden == 0) return FELLM_OK;
+    if (!expert_out || !weights || !y || (inv && !ids)) return FELLM_ERR_ARITY;
+    hipStream_t st = as_stream(stream);
+    const uint32_t grid = grid_cap(tokens, 8192);
+    const bool vec = hidden % 4 == 0 && aligned_to(expert_out, 16) && aligned_to(y, 16) && (!y0 || aligned_to(y0, 16));
+#define FELLM_MOE_COMBINE(ORD, V)                                                                                   \
+    hipLaunchKernelGGL((moe_combine_rows<ORD, V>), dim3(grid), dim3(256), 0, st, y0, expert_out, ids, weights, inv, \
+                       tokens, top_k, hidden, n, y)
+    if (inv) {
+        if (vec)
+            FELLM_MOE_COMBINE(true, 4);
+        else
+            FELLM_MOE_COMBINE(true, 1);
+    } else {
+        if (vec)
+            FELLM_MOE_COMBINE(false, 4);
+        else
+            FELLM_MOE_COMBINE(false, 1);
+    }
+#undef FELLM_MOE_COMBINE
+    return launch_status();
+}

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes as C
 from dataclasses import dataclass
+from typing import NamedTuple
 
 import torch
 
@@ -248,6 +249,67 @@ def router_topk(logits, k: int, *, gating_func: int = 1, norm_topk_prob: bool = 
     _lib.call("fellm_rocm_router_topk", _p(logits), tokens, n_exp, k, gating_func, int(norm_topk_prob),
               routed_scaling_factor, _p(ids), _p(weights), _stream())
     return ids, weights
+
+
+class MoeDispatch(NamedTuple):
+    """Per-expert grouping of the routed assignments (all int32 tensors on the device)."""
+
+    counts: torch.Tensor   # [E]
+    offsets: torch.Tensor  # [E + 1]
+    order: torch.Tensor    # [A], A = tokens * top_k
+    inv: torch.Tensor      # [A]
+
+
+def moe_dispatch(ids, n_experts: int, *, err_flag=None, workspace=None) -> MoeDispatch:
+    """Stable per-expert grouping of the router's ids [tokens, top_k]
+    (moe.rs:839-848 order; replaces oxide_kernels.rs:2283-2327)."""
+    _dev(ids)
+    if ids.dtype != torch.int32 or ids.dim() != 2 or not ids.is_contiguous():
+        raise TypeError("ids must be a contiguous int32 [tokens, top_k] tensor")
+    tokens, k = ids.shape
+    dev = ids.device
+    counts = torch.empty(n_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    order = torch.empty(tokens * k, dtype=torch.int32, device=dev)
+    inv = torch.empty(tokens * k, dtype=torch.int32, device=dev)
+    need = _lib.lib().fellm_rocm_moe_dispatch_workspace(tokens, k, n_experts)
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _lib.call("fellm_rocm_moe_dispatch", _p(ids), tokens, k, n_experts, _p(counts), _p(offsets), _p(order), _p(inv),
+              _p(err_flag), _p(workspace), ws_bytes, _stream())
+    return MoeDispatch(counts, offsets, order, inv)
+
+
+def moe_gather(x, order, top_k: int, out=None):
+    """grouped[p] = x[order[p] // top_k] (moe.rs:954-957), any 1/2/4-byte dtype."""
+    _dev(x, order)
+    tokens, hidden = x.shape
+    if not x.is_contiguous() or order.numel() != tokens * top_k:
+        raise ValueError("x must be contiguous [tokens, hidden] and order [tokens * top_k]")
+    out = out if out is not None else torch.empty((tokens * top_k, hidden), dtype=x.dtype, device=x.device)
+    _lib.call("fellm_rocm_moe_gather", _p(x), x.element_size(), tokens, top_k, hidden, _p(order), _p(out), _stream())
+    return out
+
+
+def moe_combine(expert_out, weights, *, ids=None, inv=None, y0=None, out=None):
+    """y = y0 + sum_s weights[:, s] * row(t, s) in f32 without FMA.  With inv
+    (grouped rows) the slots are added in ascending expert id (moe.rs:1024-1033);
+    without, rows are per assignment and added in slot order
+    (moe_weighted_reduce, oxide_kernels.rs:2507-2532)."""
+    _dev(expert_out, weights, ids, inv, y0)
+    tokens, k = weights.shape
+    hidden = expert_out.shape[1]
+    if expert_out.dtype != torch.float32 or weights.dtype != torch.float32:
+        raise TypeError("expert_out and weights must be float32")
+    if expert_out.shape[0] != tokens * k:
+        raise ValueError("expert_out must hold tokens * top_k rows")
+    if inv is not None and ids is None:
+        raise ValueError("the expert-order combine needs ids")
+    out = out if out is not None else torch.empty((tokens, hidden), dtype=torch.float32, device=expert_out.device)
+    _lib.call("fellm_rocm_moe_combine", _p(y0), _p(expert_out), _p(ids), _p(weights), _p(inv), tokens, k, hidden,
+              _p(out), _stream())
+    return out
 
 
 def _kquant_code(qtype: str, w, cols: int) -> int:

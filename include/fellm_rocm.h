@@ -211,6 +211,52 @@ int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void *out, uint3
                                void *stream);
 
 /*
+ * MoE dispatch: group the routed assignments a = token * top_k + slot by expert.
+ *   replaces: fill_u32 + moe_count_assignments + moe_prefix_offsets +
+ *             moe_scatter_assignments (plugins/cuda_kernels/src/
+ *             oxide_kernels.rs:2283-2327, launched at launchers.rs:2377-2406);
+ *             grouping order of crates/backend-cpu/src/kernels/moe.rs:839-848.
+ * ids u32 [tokens, top_k] (device); counts u32 [n_experts]; offsets u32
+ * [n_experts + 1] (exclusive prefix, offsets[n_experts] = valid assignments);
+ * order u32 [A] (A = tokens * top_k): order[offsets[e] + i] is expert e's i-th
+ * assignment, ascending in a (the CPU backend's order; the CUDA plugin's atomic
+ * scatter leaves it unspecified); inv u32 [A] (may be NULL): inv[order[p]] = p.
+ * An id >= n_experts is left out of every group (inv = 0xffffffff, the order
+ * tail past offsets[n_experts] = 0xffffffff) and sets *err_flag (device u32,
+ * may be NULL) to 1; the CPU reference indexes out of bounds on such ids.
+ * n_experts <= 4096, top_k <= 64.  workspace: device memory of
+ * fellm_rocm_moe_dispatch_workspace() bytes (0 when A <= 512).
+ */
+uint64_t fellm_rocm_moe_dispatch_workspace(uint64_t tokens, uint32_t top_k, uint32_t n_experts);
+int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32_t n_experts,
+                            uint32_t *counts, uint32_t *offsets, uint32_t *order, uint32_t *inv,
+                            uint32_t *err_flag, void *workspace, uint64_t workspace_bytes, void *stream);
+
+/*
+ * grouped[p, :] = x[order[p] / top_k, :] for p < A (moe.rs:954-957); rows of
+ * `hidden` elements of elem_bytes (1, 2 or 4) bytes, copied bit for bit.  An
+ * order entry >= A (0xffffffff) gives a zero row.
+ */
+int fellm_rocm_moe_gather(const void *x, uint32_t elem_bytes, uint64_t tokens, uint32_t top_k, uint64_t hidden,
+                          const uint32_t *order, void *grouped, void *stream);
+
+/*
+ * Weighted combine of the expert outputs, f32:
+ *   y[t, :] = y0[t, :] (0 when y0 == NULL) + sum over t's slots of
+ *             weights[t, s] * row(t, s), each step acc = acc + w * v (no FMA).
+ * inv != NULL: rows are grouped, row(t, s) = expert_out[inv[t * top_k + s]],
+ *   slots taken in ascending (ids[t, s], s) — crates/backend-cpu/src/kernels/
+ *   moe.rs:1024-1033, which adds group by group in expert order.
+ * inv == NULL: rows are per assignment, row(t, s) = expert_out[t * top_k + s],
+ *   slots in order s = 0..top_k-1 — moe_weighted_reduce (oxide_kernels.rs:
+ *   2507-2532, launched at launchers.rs:2228, 2533), ids unused (may be NULL).
+ * y may equal y0.  A slot whose inv is 0xffffffff contributes nothing.
+ */
+int fellm_rocm_moe_combine(const float *y0, const float *expert_out, const uint32_t *ids, const float *weights,
+                           const uint32_t *inv, uint64_t tokens, uint32_t top_k, uint64_t hidden, float *y,
+                           void *stream);
+
+/*
  * Self-check of the device expf restatement: out[i] = expf(in[i]) on the GPU.
  * Diagnostic only (no counterpart in the reference).
  */

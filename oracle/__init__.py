@@ -345,3 +345,17 @@ def moe_combine(y0: np.ndarray, expert_out: np.ndarray, ids: np.ndarray, weights
     out = np.empty_like(yy)
     lib().oracle_moe_combine(_p(yy), _p(eo), _p(ii), _p(ww), _p(iv), tokens, k, h, _p(out))
     return out
+
+
+def moe_weighted_reduce(y0: np.ndarray | None, expert_out: np.ndarray, weights: np.ndarray) -> np.ndarray:
+    """Slot-order combine over per-assignment rows, as the CUDA plugin's
+    moe_weighted_reduce (plugins/cuda_kernels/src/oxide_kernels.rs:2507-2532):
+    value = 0 (here y0 when given); value += score * out for slot 0..k-1.
+    numpy evaluates w * e and the add as two f32 roundings (no FMA)."""
+    ww = np.asarray(weights, np.float32)
+    tokens, k = ww.shape
+    eo = np.asarray(expert_out, np.float32).reshape(tokens, k, -1)
+    y = np.zeros((tokens, eo.shape[2]), np.float32) if y0 is None else np.array(y0, np.float32)
+    for s in range(k):
+        y = (y + (ww[:, s:s + 1] * eo[:, s]).astype(np.float32)).astype(np.float32)
+    return y

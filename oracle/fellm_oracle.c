@@ -737,27 +737,26 @@ void oracle_moe_gather(const float *x, size_t tokens, size_t k, size_t h, const 
     for (size_t i = 0; i < tokens * k; ++i) memcpy(grouped + i * h, x + (size_t)(order[i] / k) * h, h * sizeof(float));
 }
 
-/* y[t] = y0[t] + sum over t's assignments in ascending expert id of
+/* y[t] = y0[t] + sum over t's assignments in ascending (expert id, slot) of
  * weight * expert_out[inv[a]] (moe.rs:1024-1033). */
 void oracle_moe_combine(const float *y0, const float *expert_out, const uint32_t *ids, const float *weights,
                         const uint32_t *inv, size_t tokens, size_t k, size_t h, float *y) {
     for (size_t t = 0; t < tokens; ++t) {
         float *yr = y + t * h;
         memcpy(yr, y0 + t * h, h * sizeof(float));
-        size_t done = 0;
-        uint32_t last = 0;
-        while (done < k) {  /* next slot in ascending expert id */
+        /* next slot by (expert id, slot): a selection sort over the k slots */
+        uint64_t last = 0;
+        for (size_t done = 0; done < k; ++done) {
             size_t best = k;
+            uint64_t best_key = 0;
             for (size_t s = 0; s < k; ++s) {
-                const uint32_t e = ids[t * k + s];
-                if ((done == 0 || e > last) && (best == k || e < ids[t * k + best])) best = s;
+                const uint64_t key = (uint64_t)ids[t * k + s] * k + s;
+                if ((done == 0 || key > last) && (best == k || key < best_key)) best = s, best_key = key;
             }
-            if (best == k) break;
             const float w = weights[t * k + best];
             const float *src = expert_out + (size_t)inv[t * k + best] * h;
             for (size_t d = 0; d < h; ++d) yr[d] += w * src[d];
-            last = ids[t * k + best];
-            ++done;
+            last = best_key;
         }
     }
 }

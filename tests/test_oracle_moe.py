@@ -87,3 +87,37 @@ def test_dispatch_gather_combine_identity_experts():
     y = oracle.moe_combine(np.zeros((tokens, h), np.float32), eo, ids, w, inv)
     ref = (w.astype(np.float64)[:, :, None] * c[ids].astype(np.float64)[:, :, None] * x.astype(np.float64)[:, None, :]).sum(1)
     assert np.abs(y - ref).max() < 1e-5 * np.abs(ref).max()
+
+
+def test_combine_repeated_expert_in_a_token():
+    """Drawn with replacement: a token may route twice to one expert; the
+    group walk then meets its two slots in slot order."""
+    rng = np.random.default_rng(8)
+    tokens, k, E, h = 20, 4, 3, 8
+    ids = rng.integers(0, E, size=(tokens, k)).astype(np.uint32)
+    w = rng.random(size=(tokens, k)).astype(np.float32)
+    _, offsets, order, inv = oracle.moe_dispatch(ids, E)
+    eo = rng.normal(size=(tokens * k, h)).astype(np.float32)
+    y0 = rng.normal(size=(tokens, h)).astype(np.float32)
+    got = oracle.moe_combine(y0, eo, ids, w, inv)
+    ref = combine_by_groups(y0, eo, ids, w, offsets, order, E)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_weighted_reduce_closed_forms():
+    rng = np.random.default_rng(12)
+    tokens, k, h = 16, 4, 24
+    w = rng.random(size=(tokens, k)).astype(np.float32)
+    eo = rng.normal(size=(tokens * k, h)).astype(np.float32)
+    # one slot: exactly w * e
+    got = oracle.moe_weighted_reduce(None, eo[::k], w[:, :1])
+    assert np.array_equal(got, (w[:, :1] * eo[::k]).astype(np.float32))
+    # slot order matters only through rounding: close to the f64 sum
+    got = oracle.moe_weighted_reduce(None, eo, w)
+    ref = (w.astype(np.float64)[:, :, None] * eo.reshape(tokens, k, h)).sum(1)
+    assert np.abs(got - ref).max() < 1e-5
+    # grouped rows in slot order: the group walk with one expert per slot index
+    ids = np.tile(np.arange(k, dtype=np.uint32), (tokens, 1))
+    _, _, order, inv = oracle.moe_dispatch(ids, k)
+    grouped = eo[order]
+    assert np.array_equal(oracle.moe_combine(np.zeros((tokens, h), np.float32), grouped, ids, w, inv), got)
