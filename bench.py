@@ -44,6 +44,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sets", type=int, default=3, help="rotating input sets")
+    ap.add_argument("--only", default=None, help="with --suite: comma-separated suite entries to run")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     ap.add_argument("--suite", action="store_true", help="per-op table for every config")
@@ -288,6 +289,48 @@ def attention_ops(torch, ops, dev, n_sets, seed=7):
     return chain, [{}], 1
 
 
+def moe_ops(torch, ops, dev, n_sets, seed=8):
+    """MoE dispatch around the expert FFNs at the configs[4] shape (Qwen3-30B-A3B:
+    16384 tokens, top-8 of 128 experts, H 2048): stable per-expert grouping,
+    bf16 row gather into grouped order, f32 weighted combine in expert order
+    (CPU backend) and slot order (CUDA plugin); plus the grouping of one
+    64-token decode batch (launch-latency bound)."""
+    T, E, K, H = 16384, 128, 8, 2048
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    sets = []
+    for _ in range(n_sets):
+        ids = torch.argsort(torch.rand(T, E, generator=g, device=dev), dim=1)[:, :K].to(torch.int32).contiguous()
+        d = ops.moe_dispatch(ids, E)
+        sets.append({
+            "ids": ids, "d": d,
+            "d2": ops.moe_dispatch(ids, E),
+            "ids64": ids[:64].contiguous(),
+            "d64": ops.moe_dispatch(ids[:64].contiguous(), E),
+            "ws": torch.empty(ops._lib.lib().fellm_rocm_moe_dispatch_workspace(T, K, E), dtype=torch.uint8,
+                              device=dev),
+            "wts": torch.rand(T, K, generator=g, device=dev),
+            "x": torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16),
+            "grouped": torch.empty(T * K, H, dtype=torch.bfloat16, device=dev),
+            "eo": torch.randn(T * K, H, generator=g, device=dev),
+            "y0": torch.randn(T, H, generator=g, device=dev),
+            "y": torch.empty(T, H, device=dev),
+        })
+    A = T * K
+    chain = [
+        Op("moe_dispatch_t16384", A * 4 + 2 * A * 4 + (2 * E + 1) * 4,
+           lambda s: ops.moe_dispatch(s["ids"], E, workspace=s["ws"], out=s["d2"])),
+        Op("moe_dispatch_t64", 64 * K * 4 * 3 + (2 * E + 1) * 4, lambda s: ops.moe_dispatch(s["ids64"], E, out=s["d64"])),
+        Op("moe_gather_bf16", A * 4 + T * H * 2 + A * H * 2,
+           lambda s: ops.moe_gather(s["x"], s["d"].order, K, out=s["grouped"])),
+        Op("moe_combine_expert_order", A * H * 4 + 2 * T * H * 4 + A * 12,
+           lambda s: ops.moe_combine(s["eo"], s["wts"], ids=s["ids"], inv=s["d"].inv, y0=s["y0"], out=s["y"])),
+        Op("moe_combine_slot_order", A * H * 4 + T * H * 4 + A * 4,
+           lambda s: ops.moe_combine(s["eo"], s["wts"], out=s["y"])),
+    ]
+    return chain, sets, T
+
+
 # --------------------------------------------------------------------------- #
 # Timing
 # --------------------------------------------------------------------------- #
@@ -423,7 +466,10 @@ def main():
     if args.suite:
         result = {}
         for name, make in (("c2", c2_ops), ("c3", c3_ops), ("c4", c4_ops), ("c5", c5_ops),
-                           ("next_gemv", gemv_ops), ("next_attention", attention_ops)):
+                           ("next_gemv", gemv_ops), ("next_attention", attention_ops),
+                           ("next_moe", moe_ops)):
+            if args.only and name not in args.only.split(","):
+                continue
             chain, sets, _ = make(torch, ops, dev, args.sets)
             _, per_op = run_chain(torch, chain, sets, args.steps, args.warmup)
             result[name] = op_report(per_op)

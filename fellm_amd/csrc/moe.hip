@@ -26,55 +26,54 @@
 // are u32 with A = tokens * top_k; rows are contiguous, `hidden` elements.
 //
 // The dispatch is integer work over A * 4 bytes of ids: it is launch- and
-// latency-bound, not HBM-bound.  Chunks of kChunk assignments go to one
-// wavefront each; inside a chunk the rank of an assignment among the earlier
-// ones with the same expert is found 64 lanes at a time with ballots over the
-// expert id's bits (lanes whose ids agree on every bit are peers).
+// latency-bound, not HBM-bound.  At most 256 blocks each take a contiguous
+// chunk (>= 2048 assignments), a wavefront a quarter of it; pass 1 counts per
+// block, pass 2 turns the counts into cursors and scatters stably.  Up to 2048
+// assignments (decode batches) it is one launch.
 #include "common.hpp"
 
 namespace fellm {
 namespace {
 
-constexpr uint32_t kChunkRounds = 8;
-constexpr uint32_t kChunk = kWave * kChunkRounds;  // assignments per wavefront
+constexpr uint32_t kDispatchBlock = 256;                  // 4 wavefronts
+constexpr uint32_t kDispatchWaves = kDispatchBlock / kWave;
+constexpr uint32_t kMinChunk = 2048;                      // assignments per block, at least
+constexpr uint32_t kMaxDispatchBlocks = 256;
 constexpr uint32_t kMoeMaxExperts = 4096;
 constexpr uint32_t kMoeMaxTopK = 64;
 constexpr uint32_t kInvalid = 0xffffffffu;
-constexpr int kScanBlock = 1024;
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
-// Counts of the valid ids of chunk c into cnt[E] (LDS, zeroed by the caller).
-__device__ __forceinline__ void count_chunk(const uint32_t *__restrict__ ids, uint64_t n, uint32_t E, uint64_t c,
-                                            uint32_t *cnt, uint32_t *err) {
-    const uint32_t lane = lane_id();
+// cnt[id] += 1 for every valid id in [lo, hi), `stride` threads from `t`.
+__device__ __forceinline__ void count_range(const uint32_t *__restrict__ ids, uint64_t lo, uint64_t hi, uint32_t t,
+                                            uint32_t stride, uint32_t E, uint32_t *cnt, uint32_t *err) {
     bool bad = false;
-#pragma unroll
-    for (uint32_t r = 0; r < kChunkRounds; ++r) {
-        const uint64_t a = c * kChunk + r * kWave + lane;
-        if (a < n) {
-            const uint32_t id = ids[a];
-            if (id < E)
-                atomicAdd(&cnt[id], 1u);
-            else
-                bad = true;
-        }
+    for (uint64_t a = lo + t; a < hi; a += stride) {
+        const uint32_t id = ids[a];
+        if (id < E)
+            atomicAdd(&cnt[id], 1u);
+        else
+            bad = true;
     }
     if (bad && err) atomicOr(err, 1u);
 }
 
-// Scatter of chunk c: cur[e] (LDS) holds the next free grouped position of
-// expert e for this chunk.  Assignments are placed in ascending index.
-__device__ __forceinline__ void scatter_chunk(const uint32_t *__restrict__ ids, uint64_t n, uint32_t E, uint32_t bits,
-                                              uint64_t c, uint32_t *cur, uint32_t *__restrict__ order,
+// Stable scatter of [lo, hi) by one wavefront: cur[e] (LDS, private to the
+// wavefront) holds expert e's next free grouped position.  64 assignments per
+// round; an assignment's rank among the round's earlier lanes with the same
+// expert comes from ballots over the id's bits (lanes agreeing on every bit
+// are peers), and the round's lowest peer advances the cursor.
+__device__ __forceinline__ void scatter_range(const uint32_t *__restrict__ ids, uint64_t lo, uint64_t hi, uint32_t E,
+                                              uint32_t bits, uint32_t *cur, uint32_t *__restrict__ order,
                                               uint32_t *__restrict__ inv) {
     const uint32_t lane = lane_id();
     const uint64_t lt = (1ull << lane) - 1ull;
-    for (uint32_t r = 0; r < kChunkRounds; ++r) {
-        const uint64_t a = c * kChunk + r * kWave + lane;
-        uint32_t id = a < n ? ids[a] : kInvalid;
+    for (uint64_t r = lo; r < hi; r += kWave) {
+        const uint64_t a = r + lane;
+        const uint32_t id = a < hi ? ids[a] : kInvalid;
         const bool valid = id < E;
-        if (!valid && a < n && inv) inv[a] = kInvalid;
+        if (!valid && a < hi && inv) inv[a] = kInvalid;
         uint64_t peers = __ballot(valid);
         if (peers == 0) continue;  // wave-uniform: no valid id this round
         for (uint32_t b = 0; b < bits; ++b) {
@@ -112,106 +111,131 @@ __device__ __forceinline__ uint32_t wave_exclusive(uint32_t v, uint32_t *total) 
     return inc - v;
 }
 
-// A <= kChunk: everything in one wavefront, one launch (the decode case).
-__global__ __launch_bounds__(kWave) void moe_dispatch_one(const uint32_t *__restrict__ ids, uint32_t n, uint32_t E,
-                                                          uint32_t bits, uint32_t *__restrict__ counts,
-                                                          uint32_t *__restrict__ offsets,
-                                                          uint32_t *__restrict__ order, uint32_t *__restrict__ inv,
-                                                          uint32_t *err) {
+// Pass 1 (only with more than one block): bc[c][e] = valid ids of expert e in
+// block c's chunk [c * chunk, (c + 1) * chunk).
+__global__ __launch_bounds__(kDispatchBlock) void moe_count_blocks(const uint32_t *__restrict__ ids, uint64_t n,
+                                                                   uint32_t E, uint64_t chunk,
+                                                                   uint32_t *__restrict__ bc, uint32_t *err) {
     extern __shared__ uint32_t cnt[];
-    const uint32_t lane = lane_id();
-    for (uint32_t e = lane; e < E; e += kWave) cnt[e] = 0;
-    __syncthreads();
-    count_chunk(ids, n, E, 0, cnt, err);
-    __syncthreads();
-    // Exclusive prefix over experts: lane l owns the contiguous run
-    // [l * per, (l + 1) * per).
-    const uint32_t per = (E + kWave - 1) / kWave;
-    const uint32_t lo = min(E, lane * per), hi = min(E, lo + per);
-    uint32_t s = 0;
-    for (uint32_t e = lo; e < hi; ++e) s += cnt[e];
-    uint32_t total;
-    uint32_t run = wave_exclusive(s, &total);
-    for (uint32_t e = lo; e < hi; ++e) {
-        const uint32_t c = cnt[e];
-        counts[e] = c;
-        offsets[e] = run;
-        cnt[e] = run;
-        run += c;
-    }
-    if (lane == 0) offsets[E] = total;
-    for (uint32_t i = total + lane; i < n; i += kWave) order[i] = kInvalid;
-    __syncthreads();
-    scatter_chunk(ids, n, E, bits, 0, cnt, order, inv);
-}
-
-// Pass 1: per-chunk counts, bc[c][e].
-__global__ __launch_bounds__(kWave) void moe_count_chunks(const uint32_t *__restrict__ ids, uint64_t n, uint32_t E,
-                                                          uint32_t *__restrict__ bc, uint32_t *err) {
-    extern __shared__ uint32_t cnt[];
-    const uint32_t lane = lane_id();
-    const uint64_t c = blockIdx.x;
-    for (uint32_t e = lane; e < E; e += kWave) cnt[e] = 0;
-    __syncthreads();
-    count_chunk(ids, n, E, c, cnt, err);
-    __syncthreads();
-    for (uint32_t e = lane; e < E; e += kWave) bc[c * E + e] = cnt[e];
-}
-
-// Pass 2 (one block): bc[c][e] becomes the exclusive prefix over chunks,
-// counts[e] the column sum, offsets the exclusive prefix over experts.
-__global__ __launch_bounds__(kScanBlock) void moe_scan_chunks(uint32_t *__restrict__ bc, uint32_t nchunks, uint32_t E,
-                                                              uint64_t n, uint32_t *__restrict__ counts,
-                                                              uint32_t *__restrict__ offsets,
-                                                              uint32_t *__restrict__ order) {
-    __shared__ uint32_t col[kMoeMaxExperts];
-    __shared__ uint32_t wsum[kScanBlock / kWave];
     const uint32_t t = threadIdx.x;
-    for (uint32_t e = t; e < E; e += kScanBlock) {
-        uint32_t run = 0;
-        for (uint32_t c = 0; c < nchunks; ++c) {
-            const uint32_t v = bc[(size_t)c * E + e];
-            bc[(size_t)c * E + e] = run;
+    const uint64_t c = blockIdx.x;
+    for (uint32_t e = t; e < E; e += kDispatchBlock) cnt[e] = 0;
+    __syncthreads();
+    const uint64_t lo = c * chunk, hi = min(n, lo + chunk);
+    count_range(ids, lo, hi, t, kDispatchBlock, E, cnt, err);
+    __syncthreads();
+    for (uint32_t e = t; e < E; e += kDispatchBlock) bc[c * E + e] = cnt[e];
+}
+
+// Pass 2: block c scatters its chunk, wavefront w the w-th quarter of it.
+// Every block derives what it needs from bc: the per-expert totals (their
+// exclusive prefix over experts is `offsets`) and the counts of the chunks
+// before its own.  Block 0 writes counts / offsets and fills the order tail
+// past the valid assignments.  With one block (nblocks == 1) bc is unused and
+// the whole dispatch is this one launch.
+//
+// LDS: wcur[kDispatchWaves][E] (per-wavefront counts, then cursors), col[E].
+__global__ __launch_bounds__(kDispatchBlock) void moe_scatter_blocks(const uint32_t *__restrict__ ids, uint64_t n,
+                                                                     uint32_t E, uint32_t bits, uint64_t chunk,
+                                                                     uint32_t nblocks,
+                                                                     const uint32_t *__restrict__ bc,
+                                                                     uint32_t *__restrict__ counts,
+                                                                     uint32_t *__restrict__ offsets,
+                                                                     uint32_t *__restrict__ order,
+                                                                     uint32_t *__restrict__ inv, uint32_t *err) {
+    extern __shared__ uint32_t lds[];
+    uint32_t *wcur = lds;                        // [waves][E]
+    uint32_t *col = lds + kDispatchWaves * E;    // [E]
+    __shared__ uint32_t wsum[kDispatchWaves];
+    const uint32_t t = threadIdx.x, w = t / kWave;
+    const uint32_t c = blockIdx.x;
+    const uint64_t lo = (uint64_t)c * chunk, hi = min(n, lo + chunk);
+    const uint64_t sub = chunk / kDispatchWaves;
+    const uint64_t wlo = min(hi, lo + w * sub), whi = min(hi, wlo + sub);
+    for (uint32_t i = t; i < kDispatchWaves * E; i += kDispatchBlock) wcur[i] = 0;
+    __syncthreads();
+    // Counts per wavefront quarter (the error flag is raised by pass 1 when
+    // there is one, here otherwise).
+    count_range(ids, wlo, whi, lane_id(), kWave, E, wcur + w * E, nblocks == 1 ? err : nullptr);
+    __syncthreads();
+    // Per expert: total, count before this block, then per-wavefront cursors
+    // relative to the expert's first grouped position.
+    for (uint32_t e = t; e < E; e += kDispatchBlock) {
+        uint32_t before = 0, total = 0;
+        if (nblocks == 1) {
+#pragma unroll
+            for (uint32_t q = 0; q < kDispatchWaves; ++q) total += wcur[q * E + e];
+        } else {
+#pragma unroll 8
+            for (uint32_t b = 0; b < nblocks; ++b) {
+                const uint32_t v = bc[(size_t)b * E + e];
+                total += v;
+                before += b < c ? v : 0u;
+            }
+        }
+        if (c == 0) counts[e] = total;
+        col[e] = total;
+        uint32_t run = before;
+#pragma unroll
+        for (uint32_t q = 0; q < kDispatchWaves; ++q) {
+            const uint32_t v = wcur[q * E + e];
+            wcur[q * E + e] = run;
             run += v;
         }
-        counts[e] = run;
-        col[e] = run;
     }
     __syncthreads();
-    constexpr uint32_t kPer = kMoeMaxExperts / kScanBlock;
-    const uint32_t lo = min(E, t * kPer), hi = min(E, lo + kPer);
+    // Exclusive prefix of col over experts: thread t owns a contiguous run.
+    const uint32_t per = (E + kDispatchBlock - 1) / kDispatchBlock;
+    const uint32_t elo = min(E, t * per), ehi = min(E, elo + per);
     uint32_t s = 0;
-    for (uint32_t e = lo; e < hi; ++e) s += col[e];
+    for (uint32_t e = elo; e < ehi; ++e) s += col[e];
     uint32_t wtotal;
     const uint32_t wpre = wave_exclusive(s, &wtotal);
-    const uint32_t w = t / kWave;
     if (lane_id() == 0) wsum[w] = wtotal;
     __syncthreads();
-    uint32_t run = wpre, total = 0;
-    for (uint32_t i = 0; i < kScanBlock / kWave; ++i) {
-        const uint32_t x = wsum[i];
-        if (i < w) run += x;
-        total += x;
+    uint32_t run = wpre, all = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kDispatchWaves; ++q) {
+        const uint32_t x = wsum[q];
+        run += q < w ? x : 0u;
+        all += x;
     }
-    for (uint32_t e = lo; e < hi; ++e) {
-        offsets[e] = run;
-        run += col[e];
+    for (uint32_t e = elo; e < ehi; ++e) {
+        const uint32_t v = col[e];
+        col[e] = run;
+        if (c == 0) offsets[e] = run;
+        run += v;
     }
-    if (t == 0) offsets[E] = total;
-    for (uint64_t i = total + t; i < n; i += kScanBlock) order[i] = kInvalid;
+    if (c == 0) {
+        if (t == 0) offsets[E] = all;
+        for (uint64_t i = all + t; i < n; i += kDispatchBlock) order[i] = kInvalid;
+    }
+    __syncthreads();
+    for (uint32_t e = t; e < E; e += kDispatchBlock) {
+#pragma unroll
+        for (uint32_t q = 0; q < kDispatchWaves; ++q) wcur[q * E + e] += col[e];
+    }
+    __syncthreads();
+    scatter_range(ids, wlo, whi, E, bits, wcur + w * E, order, inv);
 }
 
-// Pass 3: stable scatter of each chunk from its cursors.
-__global__ __launch_bounds__(kWave) void moe_scatter_chunks(const uint32_t *__restrict__ ids, uint64_t n, uint32_t E,
-                                                            uint32_t bits, const uint32_t *__restrict__ bc,
-                                                            const uint32_t *__restrict__ offsets,
-                                                            uint32_t *__restrict__ order, uint32_t *__restrict__ inv) {
-    extern __shared__ uint32_t cur[];
-    const uint32_t lane = lane_id();
-    const uint64_t c = blockIdx.x;
-    for (uint32_t e = lane; e < E; e += kWave) cur[e] = offsets[e] + bc[c * E + e];
-    __syncthreads();
-    scatter_chunk(ids, n, E, bits, c, cur, order, inv);
+// Block count and chunk (a multiple of kDispatchBlock, so each wavefront's
+// quarter is whole rounds) for n assignments.
+struct DispatchGrid {
+    uint32_t nblocks;
+    uint64_t chunk;
+};
+
+inline DispatchGrid dispatch_grid(uint64_t n) {
+    uint64_t nb = (n + kMinChunk - 1) / kMinChunk;
+    if (nb < 1) nb = 1;
+    if (nb > kMaxDispatchBlocks) nb = kMaxDispatchBlocks;
+    uint64_t chunk = (n + nb - 1) / nb;
+    chunk = (chunk + kDispatchBlock - 1) / kDispatchBlock * kDispatchBlock;
+    if (chunk == 0) chunk = kDispatchBlock;
+    nb = (n + chunk - 1) / chunk;
+    if (nb < 1) nb = 1;
+    return {(uint32_t)nb, chunk};
 }
 
 // grouped[i] = x[order[i] / top_k]; an invalid order entry gives a zero row.
@@ -306,8 +330,6 @@ __global__ __launch_bounds__(256) void moe_combine_rows(const float *y0, const f
 
 inline uint32_t id_bits(uint32_t E) { return E <= 1 ? 0 : 32 - __builtin_clz(E - 1); }
 
-inline uint64_t nchunks_of(uint64_t n) { return (n + kChunk - 1) / kChunk; }
-
 inline uint32_t grid_cap(uint64_t units, uint64_t cap) { return (uint32_t)(units < cap ? units : cap); }
 
 }  // namespace
@@ -315,9 +337,8 @@ inline uint32_t grid_cap(uint64_t units, uint64_t cap) { return (uint32_t)(units
 
 extern "C" uint64_t fellm_rocm_moe_dispatch_workspace(uint64_t tokens, uint32_t top_k, uint32_t n_experts) {
     using namespace fellm;
-    const uint64_t n = tokens * top_k;
-    const uint64_t chunks = nchunks_of(n);
-    return chunks <= 1 ? 0 : chunks * n_experts * sizeof(uint32_t);
+    const DispatchGrid g = dispatch_grid(tokens * top_k);
+    return g.nblocks <= 1 ? 0 : (uint64_t)g.nblocks * n_experts * sizeof(uint32_t);
 }
 
 extern "C" int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32_t n_experts,
@@ -331,21 +352,18 @@ extern "C" int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uin
     if (n && (!ids || !order)) return FELLM_ERR_ARITY;
     hipStream_t st = as_stream(stream);
     const uint32_t E = n_experts, bits = id_bits(E);
-    const size_t lds = (size_t)E * sizeof(uint32_t);
-    const uint64_t chunks = nchunks_of(n);
-    if (chunks <= 1) {
-        hipLaunchKernelGGL(moe_dispatch_one, dim3(1), dim3(kWave), lds, st, ids, (uint32_t)n, E, bits, counts,
-                           offsets, order, inv, err_flag);
-        return launch_status();
+    const DispatchGrid g = dispatch_grid(n);
+    const uint32_t *bc = nullptr;
+    if (g.nblocks > 1) {
+        if (!workspace || workspace_bytes < (uint64_t)g.nblocks * E * sizeof(uint32_t)) return FELLM_ERR_SHAPE;
+        uint32_t *ws = static_cast<uint32_t *>(workspace);
+        hipLaunchKernelGGL(moe_count_blocks, dim3(g.nblocks), dim3(kDispatchBlock), (size_t)E * sizeof(uint32_t),
+                           st, ids, n, E, g.chunk, ws, err_flag);
+        bc = ws;
     }
-    if (!workspace || workspace_bytes < chunks * E * sizeof(uint32_t)) return FELLM_ERR_SHAPE;
-    if (chunks > 0x7fffffffull) return FELLM_ERR_SHAPE;
-    uint32_t *bc = static_cast<uint32_t *>(workspace);
-    hipLaunchKernelGGL(moe_count_chunks, dim3((uint32_t)chunks), dim3(kWave), lds, st, ids, n, E, bc, err_flag);
-    hipLaunchKernelGGL(moe_scan_chunks, dim3(1), dim3(kScanBlock), 0, st, bc, (uint32_t)chunks, E, n, counts,
-                       offsets, order);
-    hipLaunchKernelGGL(moe_scatter_chunks, dim3((uint32_t)chunks), dim3(kWave), lds, st, ids, n, E, bits, bc,
-                       offsets, order, inv);
+    const size_t lds = (size_t)(kDispatchWaves + 1) * E * sizeof(uint32_t);
+    hipLaunchKernelGGL(moe_scatter_blocks, dim3(g.nblocks), dim3(kDispatchBlock), lds, st, ids, n, E, bits, g.chunk,
+                       g.nblocks, bc, counts, offsets, order, inv, err_flag);
     return launch_status();
 }
 

@@ -260,18 +260,25 @@ class MoeDispatch(NamedTuple):
     inv: torch.Tensor      # [A]
 
 
-def moe_dispatch(ids, n_experts: int, *, err_flag=None, workspace=None) -> MoeDispatch:
+def moe_dispatch(ids, n_experts: int, *, err_flag=None, workspace=None, out: MoeDispatch | None = None) -> MoeDispatch:
     """Stable per-expert grouping of the router's ids [tokens, top_k]
-    (moe.rs:839-848 order; replaces oxide_kernels.rs:2283-2327)."""
+    (moe.rs:839-848 order; replaces oxide_kernels.rs:2283-2327).  `out`
+    reuses the tensors of an earlier result of the same shape."""
     _dev(ids)
     if ids.dtype != torch.int32 or ids.dim() != 2 or not ids.is_contiguous():
         raise TypeError("ids must be a contiguous int32 [tokens, top_k] tensor")
     tokens, k = ids.shape
     dev = ids.device
-    counts = torch.empty(n_experts, dtype=torch.int32, device=dev)
-    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
-    order = torch.empty(tokens * k, dtype=torch.int32, device=dev)
-    inv = torch.empty(tokens * k, dtype=torch.int32, device=dev)
+    if out is not None:
+        counts, offsets, order, inv = out
+        if counts.numel() != n_experts or offsets.numel() != n_experts + 1 or order.numel() != tokens * k \
+                or inv.numel() != tokens * k:
+            raise ValueError("out does not match ids / n_experts")
+    else:
+        counts = torch.empty(n_experts, dtype=torch.int32, device=dev)
+        offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+        order = torch.empty(tokens * k, dtype=torch.int32, device=dev)
+        inv = torch.empty(tokens * k, dtype=torch.int32, device=dev)
     need = _lib.lib().fellm_rocm_moe_dispatch_workspace(tokens, k, n_experts)
     if workspace is None and need:
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)

@@ -225,7 +225,7 @@ int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void *out, uint3
  * tail past offsets[n_experts] = 0xffffffff) and sets *err_flag (device u32,
  * may be NULL) to 1; the CPU reference indexes out of bounds on such ids.
  * n_experts <= 4096, top_k <= 64.  workspace: device memory of
- * fellm_rocm_moe_dispatch_workspace() bytes (0 when A <= 512).
+ * fellm_rocm_moe_dispatch_workspace() bytes (0 when A <= 2048).
  */
 uint64_t fellm_rocm_moe_dispatch_workspace(uint64_t tokens, uint32_t top_k, uint32_t n_experts);
 int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32_t n_experts,

@@ -40,8 +40,9 @@ def u32(t):
     return t.cpu().numpy().view(np.uint32)
 
 
-DISPATCH = [(1, 1, 1), (3, 2, 4), (64, 8, 128), (65, 8, 128), (1000, 8, 128), (16384, 8, 128), (700, 6, 4096),
-            (300, 64, 300), (4096, 4, 2), (2000, 8, 256)]
+DISPATCH = [(1, 1, 1), (3, 2, 4), (64, 8, 128), (65, 8, 128), (256, 8, 128), (257, 8, 128), (1000, 8, 128),
+            (16384, 8, 128), (700, 6, 4096), (300, 64, 300), (4096, 4, 2), (2000, 8, 256), (70001, 8, 64),
+            (1 << 17, 8, 128)]
 
 
 @pytest.mark.parametrize("tokens,k,n_experts", DISPATCH)
@@ -62,9 +63,13 @@ def test_dispatch_repeated_calls_are_identical(ops, dev):
     rng = np.random.default_rng(4)
     ids = to_dev(route_ids(rng, 5000, 8, 64), dev)
     a = ops.moe_dispatch(ids, 64)
+    b = ops.moe_dispatch(ids, 64)
     for _ in range(3):
-        b = ops.moe_dispatch(ids, 64)
+        b.order.fill_(7)
+        b.inv.fill_(7)
+        ops.moe_dispatch(ids, 64, out=b)
         assert torch.equal(a.order, b.order) and torch.equal(a.inv, b.inv)
+        assert torch.equal(a.counts, b.counts) and torch.equal(a.offsets, b.offsets)
 
 
 @pytest.mark.parametrize("tokens", [10, 3000])
