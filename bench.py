@@ -292,7 +292,8 @@ def attention_ops(torch, ops, dev, n_sets, seed=7):
 def moe_ops(torch, ops, dev, n_sets, seed=8):
     """MoE dispatch around the expert FFNs at the configs[4] shape (Qwen3-30B-A3B:
     16384 tokens, top-8 of 128 experts, H 2048): stable per-expert grouping,
-    bf16 row gather into grouped order, f32 weighted combine in expert order
+    bf16 row gather into grouped order (scatter form through inv, and the
+    read-by-order form), f32 weighted combine in expert order
     (CPU backend) and slot order (CUDA plugin); plus the grouping of one
     64-token decode batch (launch-latency bound)."""
     T, E, K, H = 16384, 128, 8, 2048
@@ -321,7 +322,9 @@ def moe_ops(torch, ops, dev, n_sets, seed=8):
         Op("moe_dispatch_t16384", A * 4 + 2 * A * 4 + (2 * E + 1) * 4,
            lambda s: ops.moe_dispatch(s["ids"], E, workspace=s["ws"], out=s["d2"])),
         Op("moe_dispatch_t64", 64 * K * 4 * 3 + (2 * E + 1) * 4, lambda s: ops.moe_dispatch(s["ids64"], E, out=s["d64"])),
-        Op("moe_gather_bf16", A * 4 + T * H * 2 + A * H * 2,
+        Op("moe_gather_bf16", 2 * A * 4 + T * H * 2 + A * H * 2,
+           lambda s: ops.moe_gather(s["x"], s["d"].order, K, inv=s["d"].inv, out=s["grouped"])),
+        Op("moe_gather_bf16_by_order", A * 4 + T * H * 2 + A * H * 2,
            lambda s: ops.moe_gather(s["x"], s["d"].order, K, out=s["grouped"])),
         Op("moe_combine_expert_order", A * H * 4 + 2 * T * H * 4 + A * 12,
            lambda s: ops.moe_combine(s["eo"], s["wts"], ids=s["ids"], inv=s["d"].inv, y0=s["y0"], out=s["y"])),

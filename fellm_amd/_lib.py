@@ -64,7 +64,7 @@ _SIGNATURES = {
                                          C.POINTER(FellmRocmPagedKv), P, U64, P]),
     "fellm_rocm_moe_dispatch_workspace": (U64, [U64, U32, U32]),
     "fellm_rocm_moe_dispatch": (I32, [P, U64, U32, U32, P, P, P, P, P, P, U64, P]),
-    "fellm_rocm_moe_gather": (I32, [P, U32, U64, U32, U64, P, P, P]),
+    "fellm_rocm_moe_gather": (I32, [P, U32, U64, U32, U64, P, P, P, P]),
     "fellm_rocm_moe_combine": (I32, [P, P, P, P, P, U64, U32, U64, P, P]),
     # plugin ABI
     "_fellm_plugin_abi_version": (abi.AbiVersion, []),

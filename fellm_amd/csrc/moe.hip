@@ -46,15 +46,26 @@ constexpr uint32_t kInvalid = 0xffffffffu;
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
 // cnt[id] += 1 for every valid id in [lo, hi), `stride` threads from `t`.
+// Loads go out in batches of 8 before their LDS atomics.
 __device__ __forceinline__ void count_range(const uint32_t *__restrict__ ids, uint64_t lo, uint64_t hi, uint32_t t,
                                             uint32_t stride, uint32_t E, uint32_t *cnt, uint32_t *err) {
+    constexpr int kBatch = 8;
     bool bad = false;
-    for (uint64_t a = lo + t; a < hi; a += stride) {
-        const uint32_t id = ids[a];
-        if (id < E)
-            atomicAdd(&cnt[id], 1u);
-        else
-            bad = true;
+    for (uint64_t a0 = lo + t; a0 < hi; a0 += (uint64_t)stride * kBatch) {
+        uint32_t v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const uint64_t a = a0 + (uint64_t)j * stride;
+            v[j] = a < hi ? ids[a] : kInvalid;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const uint64_t a = a0 + (uint64_t)j * stride;
+            if (v[j] < E)
+                atomicAdd(&cnt[v[j]], 1u);
+            else if (a < hi)
+                bad = true;
+        }
     }
     if (bad && err) atomicOr(err, 1u);
 }
@@ -134,7 +145,8 @@ __global__ __launch_bounds__(kDispatchBlock) void moe_count_blocks(const uint32_
 // past the valid assignments.  With one block (nblocks == 1) bc is unused and
 // the whole dispatch is this one launch.
 //
-// LDS: wcur[kDispatchWaves][E] (per-wavefront counts, then cursors), col[E].
+// LDS: wcur[kDispatchWaves][E] (per-wavefront counts, then cursors), col[E],
+// bef[E].
 __global__ __launch_bounds__(kDispatchBlock) void moe_scatter_blocks(const uint32_t *__restrict__ ids, uint64_t n,
                                                                      uint32_t E, uint32_t bits, uint64_t chunk,
                                                                      uint32_t nblocks,
@@ -146,6 +158,7 @@ __global__ __launch_bounds__(kDispatchBlock) void moe_scatter_blocks(const uint3
     extern __shared__ uint32_t lds[];
     uint32_t *wcur = lds;                        // [waves][E]
     uint32_t *col = lds + kDispatchWaves * E;    // [E]
+    uint32_t *bef = col + E;                     // [E]
     __shared__ uint32_t wsum[kDispatchWaves];
     const uint32_t t = threadIdx.x, w = t / kWave;
     const uint32_t c = blockIdx.x;
@@ -158,24 +171,44 @@ __global__ __launch_bounds__(kDispatchBlock) void moe_scatter_blocks(const uint3
     // there is one, here otherwise).
     count_range(ids, wlo, whi, lane_id(), kWave, E, wcur + w * E, nblocks == 1 ? err : nullptr);
     __syncthreads();
-    // Per expert: total, count before this block, then per-wavefront cursors
-    // relative to the expert's first grouped position.
-    for (uint32_t e = t; e < E; e += kDispatchBlock) {
-        uint32_t before = 0, total = 0;
-        if (nblocks == 1) {
+    // Per expert: total over all blocks (col) and count in the blocks before
+    // this one (bef), read from bc with every load of a batch in flight.
+    if (nblocks == 1) {
+        for (uint32_t e = t; e < E; e += kDispatchBlock) {
+            uint32_t total = 0;
 #pragma unroll
             for (uint32_t q = 0; q < kDispatchWaves; ++q) total += wcur[q * E + e];
-        } else {
-#pragma unroll 8
-            for (uint32_t b = 0; b < nblocks; ++b) {
-                const uint32_t v = bc[(size_t)b * E + e];
-                total += v;
-                before += b < c ? v : 0u;
+            col[e] = total;
+            bef[e] = 0;
+        }
+    } else {
+        for (uint32_t e = t; e < E; e += kDispatchBlock) col[e] = bef[e] = 0;
+        __syncthreads();
+        constexpr int kBatch = 16;
+        const uint32_t cells = nblocks * E, cut = c * E;
+        for (uint32_t i0 = t; i0 < cells; i0 += kDispatchBlock * kBatch) {
+            uint32_t v[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const uint32_t i = i0 + j * kDispatchBlock;
+                v[j] = i < cells ? bc[i] : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const uint32_t i = i0 + j * kDispatchBlock;
+                if (i < cells && v[j]) {
+                    const uint32_t e = i % E;
+                    atomicAdd(&col[e], v[j]);
+                    if (i < cut) atomicAdd(&bef[e], v[j]);
+                }
             }
         }
-        if (c == 0) counts[e] = total;
-        col[e] = total;
-        uint32_t run = before;
+    }
+    __syncthreads();
+    // Per-wavefront cursors relative to the expert's first grouped position.
+    for (uint32_t e = t; e < E; e += kDispatchBlock) {
+        if (c == 0) counts[e] = col[e];
+        uint32_t run = bef[e];
 #pragma unroll
         for (uint32_t q = 0; q < kDispatchWaves; ++q) {
             const uint32_t v = wcur[q * E + e];
@@ -252,6 +285,63 @@ __global__ __launch_bounds__(256) void moe_gather_rows(const V *__restrict__ x, 
         } else {
             for (uint64_t j = threadIdx.x; j < row_vecs; j += blockDim.x) dst[j] = V{};
         }
+    }
+}
+
+// Scatter form of the gather: token t's row is read once and written to
+// grouped[inv[t * top_k + s]] for every slot s, so HBM sees the grouped
+// writes plus one read of x.  A grouped row whose order entry is invalid (the
+// tail past the valid assignments) is zeroed; rows p in [t * top_k,
+// (t + 1) * top_k) are checked by token t's block.  The row is staged
+// through registers in segments of kSeg 16-byte vectors per thread.
+template <int kSeg>
+__global__ __launch_bounds__(256) void moe_scatter_rows(const uint4 *__restrict__ x,
+                                                        const uint32_t *__restrict__ order,
+                                                        const uint32_t *__restrict__ inv, uint64_t tokens,
+                                                        uint32_t top_k, uint64_t row_vecs,
+                                                        uint4 *__restrict__ grouped) {
+    __shared__ uint32_t sdst[kMoeMaxTopK];
+    __shared__ uint32_t szero[kMoeMaxTopK];
+    const uint32_t t = threadIdx.x;
+    const uint64_t n = tokens * top_k;
+    for (uint64_t tok = blockIdx.x; tok < tokens; tok += gridDim.x) {
+        if (t < top_k) {
+            const uint64_t a = tok * top_k + t;
+            const uint32_t p = inv[a];
+            sdst[t] = p < n ? p : kInvalid;
+            szero[t] = order[a] < n ? kInvalid : (uint32_t)a;
+        }
+        __syncthreads();
+        const uint4 *src = x + tok * row_vecs;
+        for (uint64_t j0 = 0; j0 < row_vecs; j0 += (uint64_t)kSeg * 256) {
+            uint4 v[kSeg];
+#pragma unroll
+            for (int u = 0; u < kSeg; ++u) {
+                const uint64_t j = j0 + (uint64_t)u * 256 + t;
+                if (j < row_vecs) v[u] = src[j];
+            }
+            for (uint32_t s = 0; s < top_k; ++s) {
+                const uint32_t p = sdst[s];
+                if (p == kInvalid) continue;
+                uint4 *dst = grouped + (uint64_t)p * row_vecs;
+#pragma unroll
+                for (int u = 0; u < kSeg; ++u) {
+                    const uint64_t j = j0 + (uint64_t)u * 256 + t;
+                    if (j < row_vecs) dst[j] = v[u];
+                }
+            }
+            for (uint32_t s = 0; s < top_k; ++s) {
+                const uint32_t p = szero[s];
+                if (p == kInvalid) continue;
+                uint4 *dst = grouped + (uint64_t)p * row_vecs;
+#pragma unroll
+                for (int u = 0; u < kSeg; ++u) {
+                    const uint64_t j = j0 + (uint64_t)u * 256 + t;
+                    if (j < row_vecs) dst[j] = uint4{0, 0, 0, 0};
+                }
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -361,14 +451,15 @@ extern "C" int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uin
                            st, ids, n, E, g.chunk, ws, err_flag);
         bc = ws;
     }
-    const size_t lds = (size_t)(kDispatchWaves + 1) * E * sizeof(uint32_t);
+    const size_t lds = (size_t)(kDispatchWaves + 2) * E * sizeof(uint32_t);
     hipLaunchKernelGGL(moe_scatter_blocks, dim3(g.nblocks), dim3(kDispatchBlock), lds, st, ids, n, E, bits, g.chunk,
                        g.nblocks, bc, counts, offsets, order, inv, err_flag);
     return launch_status();
 }
 
 extern "C" int fellm_rocm_moe_gather(const void *x, uint32_t elem_bytes, uint64_t tokens, uint32_t top_k,
-                                     uint64_t hidden, const uint32_t *order, void *grouped, void *stream) {
+                                     uint64_t hidden, const uint32_t *order, const uint32_t *inv, void *grouped,
+                                     void *stream) {
     using namespace fellm;
     if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4) return FELLM_ERR_DTYPE;
     if (top_k == 0 || top_k > kMoeMaxTopK) return FELLM_ERR_SHAPE;
@@ -378,8 +469,20 @@ extern "C" int fellm_rocm_moe_gather(const void *x, uint32_t elem_bytes, uint64_
     if (!x || !order || !grouped) return FELLM_ERR_ARITY;
     hipStream_t st = as_stream(stream);
     const uint64_t row_bytes = hidden * elem_bytes;
+    const bool vec16 = row_bytes % 16 == 0 && aligned_to(x, 16) && aligned_to(grouped, 16);
+    if (inv && vec16) {
+        const uint64_t row_vecs = row_bytes / 16;
+        const uint32_t grid = grid_cap(tokens, 16384);
+        if (row_vecs <= 256)
+            hipLaunchKernelGGL(moe_scatter_rows<1>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x), order,
+                               inv, tokens, top_k, row_vecs, static_cast<uint4 *>(grouped));
+        else
+            hipLaunchKernelGGL(moe_scatter_rows<4>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x), order,
+                               inv, tokens, top_k, row_vecs, static_cast<uint4 *>(grouped));
+        return launch_status();
+    }
     const uint32_t grid = grid_cap(n, 8192);
-    if (row_bytes % 16 == 0 && aligned_to(x, 16) && aligned_to(grouped, 16))
+    if (vec16)
         hipLaunchKernelGGL(moe_gather_rows<uint4>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x),
                            order, n, top_k, row_bytes / 16, static_cast<uint4 *>(grouped));
     else if (row_bytes % 4 == 0 && aligned_to(x, 4) && aligned_to(grouped, 4))

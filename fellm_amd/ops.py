@@ -288,14 +288,16 @@ def moe_dispatch(ids, n_experts: int, *, err_flag=None, workspace=None, out: Moe
     return MoeDispatch(counts, offsets, order, inv)
 
 
-def moe_gather(x, order, top_k: int, out=None):
-    """grouped[p] = x[order[p] // top_k] (moe.rs:954-957), any 1/2/4-byte dtype."""
-    _dev(x, order)
+def moe_gather(x, order, top_k: int, *, inv=None, out=None):
+    """grouped[p] = x[order[p] // top_k] (moe.rs:954-957), any 1/2/4-byte dtype.
+    With the dispatch's inv, each x row is read once and scattered."""
+    _dev(x, order, inv)
     tokens, hidden = x.shape
     if not x.is_contiguous() or order.numel() != tokens * top_k:
         raise ValueError("x must be contiguous [tokens, hidden] and order [tokens * top_k]")
     out = out if out is not None else torch.empty((tokens * top_k, hidden), dtype=x.dtype, device=x.device)
-    _lib.call("fellm_rocm_moe_gather", _p(x), x.element_size(), tokens, top_k, hidden, _p(order), _p(out), _stream())
+    _lib.call("fellm_rocm_moe_gather", _p(x), x.element_size(), tokens, top_k, hidden, _p(order), _p(inv), _p(out),
+              _stream())
     return out
 
 

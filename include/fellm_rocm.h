@@ -236,9 +236,11 @@ int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uint32_t top_k
  * grouped[p, :] = x[order[p] / top_k, :] for p < A (moe.rs:954-957); rows of
  * `hidden` elements of elem_bytes (1, 2 or 4) bytes, copied bit for bit.  An
  * order entry >= A (0xffffffff) gives a zero row.
+ * inv (may be NULL) is the dispatch's inverse permutation; with it (and 16-byte
+ * rows) each x row is read once and written to its top_k grouped positions.
  */
 int fellm_rocm_moe_gather(const void *x, uint32_t elem_bytes, uint64_t tokens, uint32_t top_k, uint64_t hidden,
-                          const uint32_t *order, void *grouped, void *stream);
+                          const uint32_t *order, const uint32_t *inv, void *grouped, void *stream);
 
 /*
  * Weighted combine of the expert outputs, f32:

@@ -112,30 +112,39 @@ def test_dispatch_zero_tokens_and_shape_errors(ops, dev):
 
 
 @pytest.mark.parametrize("dtype,hidden", [(torch.float32, 2048), (torch.float16, 256), (torch.bfloat16, 2048),
-                                          (torch.float32, 7), (torch.float16, 7), (torch.uint8, 33)])
-def test_gather_rows(ops, dev, dtype, hidden):
+                                          (torch.float32, 7), (torch.float16, 7), (torch.uint8, 33),
+                                          (torch.float32, 8192), (torch.bfloat16, 3000), (torch.uint8, 16)])
+@pytest.mark.parametrize("use_inv", [False, True])
+def test_gather_rows(ops, dev, dtype, hidden, use_inv):
     rng = np.random.default_rng(hidden)
     tokens, k, E = 300, 8, 64
     ids = route_ids(rng, tokens, k, E)
-    _, _, order, _ = oracle.moe_dispatch(ids, E)
+    _, _, order, inv = oracle.moe_dispatch(ids, E)
     if dtype == torch.uint8:
         x = torch.from_numpy(rng.integers(0, 256, size=(tokens, hidden), dtype=np.uint8))
     else:
         x = torch.from_numpy(rng.normal(size=(tokens, hidden)).astype(np.float32)).to(dtype)
-    got = ops.moe_gather(x.to(dev), to_dev(order, dev), k).cpu()
+    got = ops.moe_gather(x.to(dev), to_dev(order, dev), k, inv=to_dev(inv, dev) if use_inv else None).cpu()
     ref = x[torch.from_numpy((order // k).astype(np.int64))]
     assert torch.equal(got.view(torch.uint8), ref.contiguous().view(torch.uint8))
     if dtype == torch.float32:
         assert np.array_equal(got.numpy(), oracle.moe_gather(x.numpy(), k, order))
 
 
-def test_gather_invalid_order_rows_are_zero(ops, dev):
-    tokens, k, h = 4, 2, 16
+@pytest.mark.parametrize("use_inv", [False, True])
+def test_gather_invalid_order_rows_are_zero(ops, dev, use_inv):
+    """Ids >= E leave the order tail invalid: those grouped rows come out zero
+    (pre-filled with garbage here), every other row is its token's row."""
+    tokens, k, E, h = 4, 2, 4, 16
+    ids = torch.tensor([[0, 9], [3, 1], [7, 2], [1, 0]], dtype=torch.int32, device=dev)
+    d = ops.moe_dispatch(ids, E)
     x = torch.arange(tokens * h, dtype=torch.float32, device=dev).reshape(tokens, h) + 1
-    order = torch.tensor([0, 3, 5, 7, -1, -1, 2, 1], dtype=torch.int32, device=dev)
-    got = ops.moe_gather(x, order, k).cpu()
-    assert torch.all(got[4:6] == 0)
-    assert torch.equal(got[[0, 1, 2, 3, 6, 7]], x.cpu()[[0, 1, 2, 3, 1, 0]])
+    out = torch.full((tokens * k, h), 123.0, device=dev)
+    got = ops.moe_gather(x, d.order, k, inv=d.inv if use_inv else None, out=out).cpu()
+    order = u32(d.order)
+    assert list(order[6:]) == [0xFFFFFFFF, 0xFFFFFFFF]
+    assert torch.all(got[6:] == 0)
+    assert torch.equal(got[:6], x.cpu()[torch.from_numpy(order[:6].astype(np.int64) // k)])
 
 
 COMBINE = [(40, 8, 128, 2048), (9, 2, 4, 17), (128, 6, 64, 256), (1, 1, 1, 64), (257, 64, 128, 12), (3000, 8, 16, 100)]
@@ -198,7 +207,7 @@ def test_dispatch_gather_combine_chain_at_headline_size(ops, dev):
     counts, offsets, order, inv = oracle.moe_dispatch(ids, E)
     assert np.array_equal(u32(d.order), order) and np.array_equal(u32(d.inv), inv)
     xd = torch.from_numpy(x).to(dev)
-    g = ops.moe_gather(xd, d.order, k)
+    g = ops.moe_gather(xd, d.order, k, inv=d.inv)
     scale = torch.from_numpy(c[ids.ravel()[order]]).to(dev)
     eo = g * scale[:, None]
     y0 = torch.from_numpy(x).to(dev)
