@@ -78,34 +78,44 @@ __device__ __forceinline__ void count_range(const uint32_t *__restrict__ ids, ui
 __device__ __forceinline__ void scatter_range(const uint32_t *__restrict__ ids, uint64_t lo, uint64_t hi, uint32_t E,
                                               uint32_t bits, uint32_t *cur, uint32_t *__restrict__ order,
                                               uint32_t *__restrict__ inv) {
+    constexpr int kBatch = 8;  // rounds whose ids are loaded together
     const uint32_t lane = lane_id();
     const uint64_t lt = (1ull << lane) - 1ull;
-    for (uint64_t r = lo; r < hi; r += kWave) {
-        const uint64_t a = r + lane;
-        const uint32_t id = a < hi ? ids[a] : kInvalid;
-        const bool valid = id < E;
-        if (!valid && a < hi && inv) inv[a] = kInvalid;
-        uint64_t peers = __ballot(valid);
-        if (peers == 0) continue;  // wave-uniform: no valid id this round
-        for (uint32_t b = 0; b < bits; ++b) {
-            const bool bit = (id >> b) & 1u;
-            const uint64_t ones = __ballot(bit);
-            peers &= bit ? ones : ~ones;
+    for (uint64_t r0 = lo; r0 < hi; r0 += (uint64_t)kWave * kBatch) {
+        uint32_t idv[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const uint64_t a = r0 + (uint64_t)j * kWave + lane;
+            idv[j] = a < hi ? ids[a] : kInvalid;
         }
-        uint32_t base = 0;
-        if (valid) base = cur[id];
-        // Every lane has read its cursor before the leaders advance them.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-        __builtin_amdgcn_wave_barrier();
-        const uint32_t rank = __popcll(peers & lt);
-        if (valid) {
-            if (rank == 0) cur[id] = base + (uint32_t)__popcll(peers);
-            const uint32_t pos = base + rank;
-            order[pos] = (uint32_t)a;
-            if (inv) inv[a] = pos;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const uint64_t a = r0 + (uint64_t)j * kWave + lane;
+            const uint32_t id = idv[j];
+            const bool valid = id < E;
+            if (!valid && a < hi && inv) inv[a] = kInvalid;
+            uint64_t peers = __ballot(valid);
+            if (peers == 0) continue;  // wave-uniform: no valid id this round
+            for (uint32_t b = 0; b < bits; ++b) {
+                const bool bit = (id >> b) & 1u;
+                const uint64_t ones = __ballot(bit);
+                peers &= bit ? ones : ~ones;
+            }
+            uint32_t base = 0;
+            if (valid) base = cur[id];
+            // Every lane has read its cursor before the leaders advance them.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+            __builtin_amdgcn_wave_barrier();
+            const uint32_t rank = __popcll(peers & lt);
+            if (valid) {
+                if (rank == 0) cur[id] = base + (uint32_t)__popcll(peers);
+                const uint32_t pos = base + rank;
+                order[pos] = (uint32_t)a;
+                if (inv) inv[a] = pos;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+            __builtin_amdgcn_wave_barrier();
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
