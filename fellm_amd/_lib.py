@@ -66,6 +66,13 @@ _SIGNATURES = {
     "fellm_rocm_moe_dispatch": (I32, [P, U64, U32, U32, P, P, P, P, P, P, U64, P]),
     "fellm_rocm_moe_gather": (I32, [P, U32, U64, U32, U64, P, P, P, P]),
     "fellm_rocm_moe_combine": (I32, [P, P, P, P, P, U64, U32, U64, P, P]),
+    "fellm_rocm_step_kv_position": (I32, [P, U32, P, P]),
+    "fellm_rocm_graph_begin": (I32, [P]),
+    "fellm_rocm_graph_end": (I32, [P, P]),
+    "fellm_rocm_graph_abort": (I32, [P]),
+    "fellm_rocm_graph_launch": (I32, [P, P]),
+    "fellm_rocm_graph_destroy": (None, [P]),
+    "fellm_rocm_stream_is_capturing": (I32, [P]),
     # plugin ABI
     "_fellm_plugin_abi_version": (abi.AbiVersion, []),
     "_fellm_plugin_manifest_json": (abi.PluginManifestJson, []),

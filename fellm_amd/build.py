@@ -21,7 +21,7 @@ LIB_NAME = "libfellm_rocm_kernels.so"
 LIB_PATH = PKG / LIB_NAME
 ARCH = os.environ.get("FELLM_ROCM_ARCH", "gfx950")
 
-SOURCES = ["norm.hip", "elementwise.hip", "embedding.hip", "rope.hip", "router.hip", "gemv.hip", "attention.hip", "moe.hip", "plugin.cpp"]
+SOURCES = ["norm.hip", "elementwise.hip", "embedding.hip", "rope.hip", "router.hip", "gemv.hip", "attention.hip", "moe.hip", "graph.cpp", "plugin.cpp"]
 
 # -ffp-contract=off keeps the reference's operation order (no silent FMA);
 # the packed-fp32 feature is disabled for every HIP translation unit.

@@ -80,7 +80,10 @@ struct State {
     std::map<std::pair<uintptr_t, size_t>, Mirror> act;          // activations
     std::unordered_map<uint64_t, Mirror> weights;                 // logical_id (or ptr) -> mirror
     std::map<std::pair<uintptr_t, size_t>, uint64_t> external;   // registered device tensors
-    Mirror step_params;
+    Mirror step_params;                                          // DeviceStepParams block
+    bool step_valid = false;                                     // step_params has been written
+    Mirror step_kv_pos;                                          // u32: the single row's KV position
+    bool capturing = false;                                      // stream is being captured (this launch)
     Mirror scratch;                                              // per-launch small uploads
     Mirror attn_ws;                                              // split-key attention partial sums
     void *pinned = nullptr;                                      // host staging for `scratch`
@@ -100,6 +103,16 @@ hipStream_t stream_locked(State &st) {
     return st.stream;
 }
 
+// Whether the plugin stream is being captured.  A stream that does not exist
+// yet cannot be (captures start on the stream _fellm_plugin_device_stream
+// hands out), and asking must not create one: error paths that need no GPU
+// stay GPU-free.
+bool stream_capturing(State &st) {
+    if (!st.stream) return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st.stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusActive;
+}
+
 bool sync_outputs(State &st) {
     if (st.sync_outputs < 0) {
         auto on = [](const char *name) {
@@ -111,8 +124,19 @@ bool sync_outputs(State &st) {
     return st.sync_outputs == 1;
 }
 
+State &state();
+
+// Allocations, uploads, staging and host reads cannot be recorded into a
+// graph: a launch captured into one must find every buffer already resident
+// (a warm-up launch outside the capture does that) and reads its per-step
+// values from the DeviceStepParams block.
+void no_capture() {
+    if (state().capturing) fail(FELLM_ERR_LAUNCH);
+}
+
 void ensure_capacity(Mirror &m, size_t bytes) {
     if (m.dev && m.bytes >= bytes) return;
+    no_capture();
     if (m.dev) hip_check(hipFree(m.dev));
     m.dev = nullptr;
     m.bytes = 0;
@@ -125,6 +149,7 @@ void ensure_capacity(Mirror &m, size_t bytes) {
 // its stream before returning (see guarded()).
 void upload(State &st, void *dev, const void *host, size_t bytes) {
     if (!bytes) return;
+    no_capture();
     hip_check(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, stream_locked(st)));
     st.host_reads_pending = true;
 }
@@ -175,7 +200,7 @@ void *ensure_output(State &st, const FellmTensorMut &t, bool inout = false) {
 // Marks outputs device-valid and downloads them when sync is requested
 // (launchers.rs:174-189).
 void finish_outputs(State &st, FellmTensorMut *outs, uint32_t n, bool sync_host = false) {
-    const bool sync = sync_host || sync_outputs(st);
+    const bool sync = !st.capturing && (sync_host || sync_outputs(st));
     for (uint32_t i = 0; i < n; ++i) {
         if (!outs[i].data) continue;
         if (find_external(st, outs[i].data, outs[i].byte_len)) continue;
@@ -194,6 +219,7 @@ void finish_outputs(State &st, FellmTensorMut *outs, uint32_t n, bool sync_host 
 // the kernel that reads it; the host waits for the stream before reusing it.
 void *stage_small(State &st, const std::vector<const void *> &srcs, const std::vector<size_t> &sizes,
                   std::vector<void *> &dsts) {
+    no_capture();
     size_t total = 0;
     std::vector<size_t> offs;
     for (size_t sz : sizes) {
@@ -218,7 +244,10 @@ void *stage_small(State &st, const std::vector<const void *> &srcs, const std::v
     return st.scratch.dev;
 }
 
+// Error word for kernels that flag bad slots; none while capturing (the
+// check would need a host read).
 uint32_t *err_word(State &st) {
+    if (st.capturing) return nullptr;
     if (!st.err_flag.dev) {
         ensure_capacity(st.err_flag, 4);
     }
@@ -227,6 +256,7 @@ uint32_t *err_word(State &st) {
 }
 
 int read_err(State &st) {
+    if (st.capturing) return FELLM_OK;
     uint32_t v = 0;
     hip_check(hipMemcpyAsync(&v, st.err_flag.dev, 4, hipMemcpyDeviceToHost, stream_locked(st)));
     hip_check(hipStreamSynchronize(stream_locked(st)));
@@ -269,6 +299,7 @@ int guarded(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, 
         State &st = state();
         std::lock_guard<std::mutex> lock(st.mu);
         st.host_reads_pending = false;
+        st.capturing = stream_capturing(st);
         body(st);
         if (st.host_reads_pending) {
             st.host_reads_pending = false;
@@ -283,6 +314,26 @@ int guarded(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, 
 }
 
 void *stream_ptr(State &st) { return reinterpret_cast<void *>(stream_locked(st)); }
+
+// Device address of a u32 field of the DeviceStepParams block (word index:
+// 0 token_id, 1 position, 2 sequence_length, 5 kv_write_slot), or NULL before
+// the first _fellm_plugin_update_step_params.  Single-row decode launches read
+// these instead of host values, as the CUDA plugin's controlled kernels do, so
+// that a captured step replays with the values of the step being replayed.
+const uint32_t *step_u32(State &st, size_t word) {
+    if (!st.step_valid || !st.step_params.dev) return nullptr;
+    return static_cast<const uint32_t *>(st.step_params.dev) + word;
+}
+
+// The single row's KV position from the step block (device-side; see
+// fellm_rocm_step_kv_position), or NULL without a step block.
+const uint32_t *step_kv_position(State &st, uint32_t block_size) {
+    if (!st.step_valid || !st.step_params.dev) return nullptr;
+    ensure_capacity(st.step_kv_pos, 4);
+    check(fellm_rocm_step_kv_position(static_cast<const FellmDeviceStepParams *>(st.step_params.dev), block_size,
+                                      static_cast<uint32_t *>(st.step_kv_pos.dev), stream_ptr(st)));
+    return static_cast<const uint32_t *>(st.step_kv_pos.dev);
+}
 
 // ---------------------------------------------------------------------------
 // Launchers.
@@ -397,8 +448,11 @@ int launch_rope(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_
         void *f = ensure_input(st, in[1]);
         void *o = ensure_output(st, out[0]);
         std::vector<void *> d;
-        const uint32_t *pd = nullptr;
-        if (any) {
+        // A decode row takes its position from the step block when there is
+        // one (rope_controlled: launchers.rs:479-497, used unless the
+        // snapshot holds a batch of more than one row).
+        const uint32_t *pd = rows == 1 ? step_u32(st, 1) : nullptr;
+        if (!pd && any) {
             stage_small(st, {pos.data()}, {pos.size() * 4}, d);
             pd = static_cast<const uint32_t *>(d[0]);
         }
@@ -409,32 +463,53 @@ int launch_rope(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_
 }
 
 // Paged geometry from the host snapshot (paged_ctx.rs:14-53); the arena must
-// be device-resident (the ROCm backend allocates it in HBM).
-// n_pos: entries staged from each positions array (0: the snapshot's batch size).
+// be device-resident (the ROCm backend allocates it in HBM).  The block table
+// is the snapshot's device-resident table when it holds at least the host
+// table's entries (then its logical stride applies: launchers.rs:3963-3985),
+// else the host table staged for this launch.  pos_a / pos_b (may be NULL)
+// are staged too, n_pos entries each (0: the snapshot's batch size); their
+// device addresses come back in dev_a / dev_b.
 FellmRocmPagedKv paged_geometry(State &st, const FellmPagedKvSnapshot &snap, uint32_t layer, uint32_t kv_dtype,
-                                std::vector<void *> &staged, const uint32_t *positions_a,
-                                const uint32_t *positions_b, size_t n_pos = 0) {
+                                const uint32_t *pos_a, const uint32_t **dev_a, const uint32_t *pos_b = nullptr,
+                                const uint32_t **dev_b = nullptr, size_t n_pos = 0) {
     const size_t npos = n_pos ? n_pos : snap.batch_size;
     if (!snap.device_arena || snap.device_arena_len == 0) fail(FELLM_ERR_PAGED_NO_DEVICE);
     if (snap.elem_bytes != 2 || !snap.block_table || snap.block_size == 0 || snap.tokens_stride == 0)
         fail(FELLM_ERR_PAGED_RANGE);
-    std::vector<const void *> srcs{snap.block_table};
-    std::vector<size_t> sizes{snap.n_block_table * 4};
-    if (positions_a) {
-        srcs.push_back(positions_a);
+    const bool device_table = snap.device_block_table && snap.n_device_block_table >= snap.n_block_table &&
+                              snap.device_logical_stride > 0;
+    std::vector<const void *> srcs;
+    std::vector<size_t> sizes;
+    if (!device_table) {
+        srcs.push_back(snap.block_table);
+        sizes.push_back(snap.n_block_table * 4);
+    }
+    if (pos_a) {
+        srcs.push_back(pos_a);
         sizes.push_back(npos * 4);
     }
-    if (positions_b) {
-        srcs.push_back(positions_b);
+    if (pos_b) {
+        srcs.push_back(pos_b);
         sizes.push_back(npos * 4);
     }
-    stage_small(st, srcs, sizes, staged);
+    std::vector<void *> staged;
+    if (!srcs.empty()) stage_small(st, srcs, sizes, staged);
+    size_t i = 0;
     FellmRocmPagedKv kv{};
     kv.arena = snap.device_arena;
     kv.arena_len = snap.device_arena_len;
-    kv.block_table = static_cast<const uint32_t *>(staged[0]);
-    kv.n_block_table = snap.n_block_table;
-    kv.n_logical_blocks = (uint32_t)snap.n_logical_blocks;
+    if (device_table) {
+        kv.block_table = snap.device_block_table;
+        kv.n_block_table = snap.n_device_block_table;
+        kv.n_logical_blocks = (uint32_t)snap.device_logical_stride;
+    } else {
+        kv.block_table = static_cast<const uint32_t *>(staged[i++]);
+        kv.n_block_table = snap.n_block_table;
+        kv.n_logical_blocks = (uint32_t)snap.n_logical_blocks;
+    }
+    if (pos_a && dev_a) *dev_a = static_cast<const uint32_t *>(staged[i]);
+    if (pos_a) ++i;
+    if (pos_b && dev_b) *dev_b = static_cast<const uint32_t *>(staged[i]);
     kv.n_layers = (uint32_t)snap.n_layers;
     kv.layer = layer;
     kv.block_size = (uint32_t)snap.block_size;
@@ -457,13 +532,17 @@ int launch_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_
         if (paged) {
             const size_t batch = snap.batch_size ? snap.batch_size : 1;
             if (snap.tokens_stride == 0 || n != batch * snap.tokens_stride) fail(FELLM_ERR_SHAPE);
-            if (!snap.row_positions) fail(FELLM_ERR_PAGED_MISSING);
             void *rows = ensure_input(st, in[0]);
-            std::vector<void *> staged;
-            FellmRocmPagedKv kv = paged_geometry(st, snap, a.layer_ord, FELLM_DTYPE_F16, staged, snap.row_positions, nullptr);
+            // A single row takes its slot from the step block when there is
+            // one (kv_write_row, launchers.rs:3993-4010), else the snapshot.
+            const bool controlled = batch == 1 && step_u32(st, 2);
+            if (!controlled && !snap.row_positions) fail(FELLM_ERR_PAGED_MISSING);
+            const uint32_t *pos = nullptr;
+            FellmRocmPagedKv kv = paged_geometry(st, snap, a.layer_ord, FELLM_DTYPE_F16,
+                                                 controlled ? nullptr : snap.row_positions, &pos);
+            if (controlled) pos = step_kv_position(st, kv.block_size);
             uint32_t *err = err_word(st);
-            check(fellm_rocm_kv_write(rows, dt, (uint32_t)batch, static_cast<const uint32_t *>(staged[1]), &kv,
-                                      a.kv_slot != 0, err, stream_ptr(st)));
+            check(fellm_rocm_kv_write(rows, dt, (uint32_t)batch, pos, &kv, a.kv_slot != 0, err, stream_ptr(st)));
             check(read_err(st));
             return;
         }
@@ -497,8 +576,11 @@ int launch_rope_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, ui
         if (in[1].dtype != dt || in[2].dtype != dt || in[3].dtype != FELLM_DTYPE_F32 || out[0].dtype != dt)
             fail(FELLM_ERR_DTYPE);
         FellmPagedKvSnapshot snap;
-        if (!snapshot(st, snap) || !snap.row_positions) fail(FELLM_ERR_PAGED_MISSING);
+        if (!snapshot(st, snap)) fail(FELLM_ERR_PAGED_MISSING);
         const size_t batch = snap.batch_size ? snap.batch_size : 1;
+        // One decode row: RoPE position and KV slot from the step block.
+        const bool controlled = batch == 1 && step_u32(st, 2);
+        if (!controlled && !snap.row_positions) fail(FELLM_ERR_PAGED_MISSING);
         const size_t hd = a.head_dim, nq = a.n_heads, nkv = a.n_kv_heads;
         if (!hd || !nq || !nkv) fail(FELLM_ERR_SHAPE);
         if (elems(in[0], dt) != batch * nq * hd || elems(in[1], dt) != batch * nkv * hd ||
@@ -514,14 +596,20 @@ int launch_rope_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, ui
         void *qo = ensure_output(st, out[0]);
         void *ko = has_kout ? ensure_output(st, out[1]) : nullptr;
         const uint32_t kv_dt = a.cast_to == FELLM_DTYPE_BF16 ? FELLM_DTYPE_BF16 : FELLM_DTYPE_F16;
-        std::vector<void *> staged;
-        FellmRocmPagedKv kv = paged_geometry(st, snap, a.layer_ord, kv_dt, staged, snap.row_positions,
-                                             snap.row_rope_positions);
-        const uint32_t *rope_pos = snap.row_rope_positions ? static_cast<const uint32_t *>(staged[2]) : nullptr;
+        const uint32_t *kv_pos = nullptr, *rope_pos = nullptr;
+        FellmRocmPagedKv kv;
+        if (controlled) {
+            kv = paged_geometry(st, snap, a.layer_ord, kv_dt, nullptr, nullptr);
+            kv_pos = step_kv_position(st, kv.block_size);
+            rope_pos = step_u32(st, 1);
+        } else {
+            kv = paged_geometry(st, snap, a.layer_ord, kv_dt, snap.row_positions, &kv_pos, snap.row_rope_positions,
+                                &rope_pos);
+        }
         uint32_t *err = err_word(st);
         check(fellm_rocm_rope_kv_write(q, qo, (uint32_t)nq, k, ko, v, (uint32_t)nkv, dt, (uint32_t)batch, (uint32_t)hd,
-                                       a.rope_dim, a.rope_pairing, (const float *)f, rope_pos,
-                                       static_cast<const uint32_t *>(staged[1]), &kv, err, stream_ptr(st)));
+                                       a.rope_dim, a.rope_pairing, (const float *)f, rope_pos, kv_pos, &kv, err,
+                                       stream_ptr(st)));
         finish_outputs(st, out, has_kout ? 2 : 1);
         check(read_err(st));
     });
@@ -550,6 +638,10 @@ int launch_attention(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32
         const size_t batch = batched ? snap.batch_size : 1;
         if (qn != batch * width || elems(out[0], odt) != qn) fail(FELLM_ERR_SHAPE);
         std::vector<uint32_t> lens(batch);
+        // One decode row attends to the step block's sequence_length keys
+        // when there is a step block (launchers.rs:3495-3660), which a replay
+        // can advance; its key range is then sized for the whole table.
+        const uint32_t *step_len = batched ? nullptr : step_u32(st, 2);
         if (batched) {
             if (!snap.row_lengths) fail(FELLM_ERR_PAGED_MISSING);
             std::memcpy(lens.data(), snap.row_lengths, batch * 4);
@@ -561,14 +653,20 @@ int launch_attention(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32
         const uint32_t causal = batched ? 1u : (a.attention_mode == 0 ? 1u : 0u);
         const uint32_t kv_dt = a.cast_to == FELLM_DTYPE_BF16 ? FELLM_DTYPE_BF16 : FELLM_DTYPE_F16;
         void *q = ensure_input(st, in[0]);
-        std::vector<void *> staged;
-        FellmRocmPagedKv kv = paged_geometry(st, snap, a.layer_ord, kv_dt, staged, lens.data(), nullptr, batch);
+        const uint32_t *len_dev = nullptr;
+        FellmRocmPagedKv kv = paged_geometry(st, snap, a.layer_ord, kv_dt, step_len ? nullptr : lens.data(), &len_dev,
+                                             nullptr, nullptr, batch);
+        if (step_len) {
+            len_dev = step_len;
+            const uint64_t cap = (uint64_t)kv.n_logical_blocks * kv.block_size;
+            max_seq = cap > 0xffffffffull ? 0xffffffffu : (uint32_t)cap;
+        }
         const uint64_t ws = fellm_rocm_paged_attention_workspace((uint32_t)batch, (uint32_t)nh, (uint32_t)nkv,
                                                                  (uint32_t)hd, max_seq);
         if (ws) ensure_capacity(st.attn_ws, ws);
         void *o = ensure_output(st, out[0]);
         check(fellm_rocm_paged_attention(q, dt, o, odt, (uint32_t)batch, (uint32_t)nh, (uint32_t)nkv, (uint32_t)hd,
-                                         static_cast<const uint32_t *>(staged[1]), max_seq, a.scale, causal,
+                                         len_dev, max_seq, a.scale, causal,
                                          a.attention_window, &kv, ws ? static_cast<float *>(st.attn_ws.dev) : nullptr,
                                          ws, stream_ptr(st)));
         finish_outputs(st, out, 1);
@@ -581,6 +679,26 @@ void check_ids(const FellmTensorRef &ids_t, uint64_t vocab, std::vector<uint32_t
     std::memcpy(ids.data(), ids_t.data, ids_t.byte_len);
     for (uint32_t id : ids)
         if (id >= vocab) fail(FELLM_ERR_SHAPE);  // CPU panics on out-of-range rows; CUDA returns -2
+}
+
+// Ids of an embedding launch.  One id with a step block: the device address
+// of the block's token_id (embedding_*_row, launchers.rs:1225-1260), and the
+// host value is not read (an out-of-range device id gives a zero row).
+// Otherwise the host ids, validated, and NULL (stage them).
+const void *single_id(State &st, const FellmTensorRef &ids_t, uint64_t vocab, std::vector<uint32_t> &ids) {
+    if (ids_t.dtype == FELLM_DTYPE_U32 && ids_t.byte_len == 4)
+        if (const uint32_t *p = step_u32(st, 0)) {
+            ids.assign(1, 0);
+            return p;
+        }
+    check_ids(ids_t, vocab, ids);
+    return nullptr;
+}
+
+const void *stage_ids(State &st, const std::vector<uint32_t> &ids) {
+    std::vector<void *> staged;
+    stage_small(st, {ids.data()}, {ids.size() * 4}, staged);
+    return staged[0];
 }
 
 uint64_t table_row_bytes(uint32_t dt, uint64_t dim) {
@@ -601,13 +719,11 @@ int launch_embedding(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32
         const uint64_t rb = table_row_bytes(w.dtype, dim);
         if (!rb || w.byte_len < vocab * rb || dim > 0xffffffffull) fail(FELLM_ERR_SHAPE);
         std::vector<uint32_t> ids;
-        check_ids(in[1], vocab, ids);
+        const void *idd = single_id(st, in[1], vocab, ids);
         const uint32_t odt = out[0].dtype;
         if (elems(out[0], odt) != ids.size() * dim) fail(FELLM_ERR_SHAPE);
         void *table = ensure_input(st, w);
-        std::vector<void *> staged;
-        stage_small(st, {ids.data()}, {ids.size() * 4}, staged);
-        void *idd = staged[0];
+        if (!idd) idd = stage_ids(st, ids);
         void *o = ensure_output(st, out[0]);
         check(fellm_rocm_embedding(table, w.dtype, vocab, (uint32_t)dim, (const uint32_t *)idd, (uint32_t)ids.size(), o,
                                    odt, nullptr, stream_ptr(st)));
@@ -625,15 +741,13 @@ int launch_embedding_rmsnorm(const FellmOpAttrs *attrs, const FellmTensorRef *in
         const uint64_t rb = table_row_bytes(w.dtype, dim);
         if (!rb || w.byte_len < vocab * rb || dim > 0xffffffffull) fail(FELLM_ERR_SHAPE);
         std::vector<uint32_t> ids;
-        check_ids(in[1], vocab, ids);
+        const void *idd = single_id(st, in[1], vocab, ids);
         if (in[2].dtype != FELLM_DTYPE_F32 || elems(in[2], FELLM_DTYPE_F32) != dim) fail(FELLM_ERR_SHAPE);
         const uint32_t odt = out[0].dtype;
         if (out[1].dtype != odt || elems(out[0], odt) != ids.size() * dim || elems(out[1], odt) != ids.size() * dim)
             fail(FELLM_ERR_SHAPE);
         void *table = ensure_input(st, w);
-        std::vector<void *> staged;
-        stage_small(st, {ids.data()}, {ids.size() * 4}, staged);
-        void *idd = staged[0];
+        if (!idd) idd = stage_ids(st, ids);
         void *nw = ensure_input(st, in[2]);
         void *h = ensure_output(st, out[0]);
         void *y = ensure_output(st, out[1]);
@@ -876,9 +990,11 @@ int _fellm_plugin_update_step_params(const FellmDeviceStepParams *params) {
         if (!params) return FELLM_ERR_ARITY;
         State &st = state();
         std::lock_guard<std::mutex> lock(st.mu);
+        st.capturing = stream_capturing(st);  // updates go between replays, not into one
         ensure_capacity(st.step_params, sizeof(FellmDeviceStepParams));
         upload(st, st.step_params.dev, params, sizeof(FellmDeviceStepParams));
         hip_check(hipStreamSynchronize(stream_locked(st)));
+        st.step_valid = true;
         return FELLM_OK;
     } catch (const LaunchError &e) {
         return e.code;

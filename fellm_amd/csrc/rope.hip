@@ -421,6 +421,35 @@ extern "C" int fellm_rocm_kv_write(const void *rows, uint32_t act_dtype, uint32_
     });
 }
 
+namespace fellm {
+namespace {
+
+// The reference's controlled single-row KV addressing (oxide_kernels.rs:
+// 4203-4214): logical block (sequence_length - 1) / block_size (saturating),
+// slot kv_write_slot.  Expressed as the position logical * block_size + slot
+// that the KV kernels take; a slot outside the block gives 0xffffffff, which
+// the KV kernels reject (error flag) instead of writing past the block.
+__global__ void step_kv_position_kernel(const FellmDeviceStepParams *__restrict__ p, uint32_t block_size,
+                                        uint32_t *__restrict__ kv_pos) {
+    if (threadIdx.x != 0) return;
+    const uint32_t seq = p->sequence_length, slot = p->kv_write_slot;
+    const uint32_t logical = (seq ? seq - 1 : 0) / block_size;
+    kv_pos[0] = slot < block_size ? logical * block_size + slot : 0xffffffffu;
+}
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" int fellm_rocm_step_kv_position(const FellmDeviceStepParams *params, uint32_t block_size,
+                                           uint32_t *kv_pos, void *stream) {
+    using namespace fellm;
+    if (!params || !kv_pos) return FELLM_ERR_ARITY;
+    if (block_size == 0) return FELLM_ERR_SHAPE;
+    hipLaunchKernelGGL(step_kv_position_kernel, dim3(1), dim3(kWave), 0, as_stream(stream), params, block_size,
+                       kv_pos);
+    return launch_status();
+}
+
 extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q_heads, const void *k,
                                         void *k_out, const void *v, uint32_t n_kv_heads, uint32_t act_dtype,
                                         uint32_t batch, uint32_t head_dim, uint32_t rope_dim, uint32_t pairing,

@@ -321,6 +321,26 @@ def moe_combine(expert_out, weights, *, ids=None, inv=None, y0=None, out=None):
     return out
 
 
+def step_kv_position(params, block_size: int, out=None):
+    """KV position of the single decode row from a device DeviceStepParams
+    block (uint8 [48] tensor): ((sequence_length - 1) // block_size) *
+    block_size + kv_write_slot (oxide_kernels.rs:4203-4214)."""
+    _dev(params)
+    out = out if out is not None else torch.empty(1, dtype=torch.int32, device=params.device)
+    _lib.call("fellm_rocm_step_kv_position", _p(params), block_size, _p(out), _stream())
+    return out
+
+
+def step_field(params, name: str):
+    """A u32 field of a device DeviceStepParams block as a 1-element int32 view
+    (token_id, position, sequence_length, ...), usable as the ids /
+    positions / row_lengths array of a decode launch."""
+    from .abi import DeviceStepParams
+
+    off = getattr(DeviceStepParams, name).offset
+    return params[off:off + 4].view(torch.int32)
+
+
 def _kquant_code(qtype: str, w, cols: int) -> int:
     code, bb = QTYPES[qtype]
     if w.dtype != torch.uint8 or w.dim() != 2 or w.shape[1] != cols // 256 * bb:

@@ -43,6 +43,9 @@ class PagedKvContext:
     device_arena_ptr: int = 0
     device_arena_len: int = 0
     elem_bytes: int = 2
+    device_block_table_ptr: int = 0     # device u32 table (engine.rs:3060-3087), 0 = none
+    n_device_block_table: int = 0
+    device_logical_stride: int = 0
 
 
 @dataclass
@@ -155,6 +158,10 @@ class PluginHost:
         if self.device_stream is not None:
             self.device_stream.restype = C.c_uint64
             self.device_stream.argtypes = []
+        self._update_step_params = getattr(self.lib, "_fellm_plugin_update_step_params", None)
+        if self._update_step_params is not None:
+            self._update_step_params.restype = C.c_int
+            self._update_step_params.argtypes = [C.POINTER(abi.DeviceStepParams)]
         self.register_device_tensor = getattr(self.lib, "_fellm_plugin_register_device_tensor", None)
         if self.register_device_tensor is not None:
             self.register_device_tensor.restype = C.c_int
@@ -211,14 +218,39 @@ class PluginHost:
         s.elem_bytes = ctx.elem_bytes
         s.device_arena = ctx.device_arena_ptr or None
         s.device_arena_len = ctx.device_arena_len
-        s.device_block_table = None
-        s.n_device_block_table = 0
-        s.device_logical_stride = 0
+        s.device_block_table = ctx.device_block_table_ptr or None
+        s.n_device_block_table = ctx.n_device_block_table
+        s.device_logical_stride = ctx.device_logical_stride
         s.batch_size = max(ctx.row_positions.size, 1)
         s.row_positions = ctx.row_positions.ctypes.data
         s.row_lengths = ctx.row_lengths.ctypes.data if ctx.row_lengths is not None else None
         s.row_rope_positions = ctx.row_rope_positions.ctypes.data
         return 0
+
+    # -- device plan (loader.rs:212-224, backend-cuda backend.rs:140-152) ------
+    def update_step_params(self, params: abi.DeviceStepParams) -> None:
+        """Upload the one device-resident step block read by single-row decode
+        launches (and by every replay of a captured step)."""
+        if self._update_step_params is None:
+            raise PluginError("plugin has no _fellm_plugin_update_step_params")
+        rc = self._update_step_params(C.byref(params))
+        if rc != 0:
+            raise PluginError(f"plugin step-parameter update failed ({rc})", rc)
+
+    def stream(self):
+        """The plugin's compute stream as a torch stream (for capture and sync)."""
+        import torch
+
+        if self.device_stream is None:
+            raise PluginError("plugin has no capture-capable device stream")
+        return torch.cuda.ExternalStream(self.device_stream())
+
+    def begin_graph_capture(self):
+        """Start capturing the plugin stream (CudaBackend::begin_graph_capture);
+        `finish()` on the result returns a replayable graph."""
+        from .graph import GraphCapture
+
+        return GraphCapture(self.stream()).begin()
 
     # -- registry -------------------------------------------------------------
     def lookup(self, op: int, input_dtypes, output_dtype: int) -> int | None:

@@ -21,6 +21,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "fellm_abi.h" /* FellmDeviceStepParams, FELLM_ERR_*, FELLM_DTYPE_* */
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -257,6 +259,43 @@ int fellm_rocm_moe_gather(const void *x, uint32_t elem_bytes, uint64_t tokens, u
 int fellm_rocm_moe_combine(const float *y0, const float *expert_out, const uint32_t *ids, const float *weights,
                            const uint32_t *inv, uint64_t tokens, uint32_t top_k, uint64_t hidden, float *y,
                            void *stream);
+
+/*
+ * Device-resident step state (graph replay).
+ *   replaces: the controlled single-row kernels of the CUDA plugin, which read
+ *   DeviceStepParams (crates/fellm-plugin-abi/src/physical_plan.rs:103-128)
+ *   from device memory so that a captured decode step replays with new values
+ *   (oxide_kernels.rs:294-321 rope_controlled, :3578-3600 embedding rows,
+ *   :4186-4223 kv_write_row, :4467 attention).
+ * In the device-pointer API the block's u32 fields are themselves the device
+ * arrays the kernels take: &p->token_id as ids[1], &p->position as
+ * positions[1], &p->sequence_length as row_lengths[1].  The KV position of the
+ * single row is written by fellm_rocm_step_kv_position:
+ *   kv_pos[0] = ((sequence_length - 1) / block_size) * block_size + kv_write_slot
+ * (saturating at sequence_length 0; 0xffffffff, which the KV writes reject,
+ * when kv_write_slot >= block_size).
+ */
+int fellm_rocm_step_kv_position(const FellmDeviceStepParams *params, uint32_t block_size, uint32_t *kv_pos,
+                                void *stream);
+
+/*
+ * HIP graph capture and replay on a caller stream.
+ *   replaces: crates/backend-cuda/src/graph.rs (CudaGraphCapture, CudaGraphExec).
+ * begin: start thread-local capture (stream must not be the null stream);
+ * end: finish, instantiate and upload, returning an opaque executable;
+ * abort: end an unfinished capture and drop what was recorded;
+ * launch: enqueue one replay; destroy: free the executable.
+ * stream_is_capturing: 1 while `stream` is capturing, 0 if not.
+ * Entry points of this library enqueue kernels only (no memset, copy or
+ * allocation), so any sequence of them can be captured; per-step values are
+ * read from device memory at replay time.
+ */
+int fellm_rocm_graph_begin(void *stream);
+int fellm_rocm_graph_end(void *stream, void **graph_exec);
+int fellm_rocm_graph_abort(void *stream);
+int fellm_rocm_graph_launch(void *graph_exec, void *stream);
+void fellm_rocm_graph_destroy(void *graph_exec);
+int fellm_rocm_stream_is_capturing(void *stream);
 
 /*
  * Self-check of the device expf restatement: out[i] = expf(in[i]) on the GPU.
