@@ -334,6 +334,232 @@ def moe_ops(torch, ops, dev, n_sets, seed=8):
     return chain, sets, T
 
 
+def time_eager_vs_graph(torch, fn, steps, warmup):
+    """Wall time per step of `fn` launched eagerly (every launch from the
+    host) and of one captured replay of it (fellm_rocm_graph_*), both on a
+    side stream, synchronised before and after the timed steps."""
+    import time
+
+    from fellm_amd import graph
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
+    stream.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for _ in range(steps):
+            fn()
+    stream.synchronize()
+    eager = (time.perf_counter() - t0) / steps
+    with graph.GraphCapture(stream) as cap:
+        fn()
+    exe = cap.graph
+    for _ in range(warmup):
+        exe.launch(stream)
+    stream.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        exe.launch(stream)
+    stream.synchronize()
+    replay = (time.perf_counter() - t0) / steps
+    exe.close()
+    return {"eager_us_per_step": round(eager * 1e6, 2), "graph_us_per_step": round(replay * 1e6, 2),
+            "speedup": round(eager / replay, 2)}
+
+
+def decode_graph_report(torch, ops, dev, steps, warmup):
+    """Launch-latency floor of decode steps, eager against HIP graph replay.
+
+    * configs[3]'s decode step (RoPE + paged K/V append, residual + RMSNorm,
+      SwiGLU for 256 sequences at Llama-3-70B shape);
+    * one Llama-3-8B decode layer for one sequence with Q4_K weights and f32
+      activations, driven by a device DeviceStepParams block: RMSNorm, QKV
+      GEMV, RoPE + K/V append at the step position, paged attention over the
+      step's sequence length (2048 keys of a 4096-key table), O GEMV,
+      residual + RMSNorm, gate/up GEMV + SwiGLU, down GEMV, residual add."""
+    import numpy as np
+
+    from fellm_amd import synth
+    from fellm_amd.abi import DeviceStepParams
+
+    out = {}
+    chain, sets, _ = c4_ops(torch, ops, dev, 1)
+    st = sets[0]
+    out["c4_decode_step_b256"] = time_eager_vs_graph(torch, lambda: [op.fn(st) for op in chain], steps, warmup)
+    del chain, sets, st
+    torch.cuda.empty_cache()
+
+    H, I, nq, nkv, hd, n_logical = 4096, 14336, 32, 8, 128, 256
+    stride = nkv * hd
+    rng = np.random.default_rng(9)
+    q4k = synth.KQUANT_TABLES[12]
+    w_qkv = torch.from_numpy(q4k(rng, H + 2 * stride, H)).to(dev)
+    w_o = torch.from_numpy(q4k(rng, H, H)).to(dev)
+    w_g = torch.from_numpy(q4k(rng, I, H)).to(dev)
+    w_u = torch.from_numpy(q4k(rng, I, H)).to(dev)
+    w_d = torch.from_numpy(q4k(rng, H, I)).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    n1 = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).float()
+    n2 = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).float()
+    inv = ops.rope_inv_freqs(500000.0, hd).to(dev)
+    bb = ops.PagedKvCache.block_bytes_for(stride)
+    arena = torch.zeros(n_logical * bb, dtype=torch.uint8, device=dev)
+    arena.view(torch.float16).copy_((0.5 * torch.randn(arena.numel() // 2, generator=g, device=dev)).half())
+    table = torch.from_numpy(rng.permutation(n_logical).astype(np.int32)).to(dev)
+    cache = ops.PagedKvCache(arena=arena, block_table=table, n_layers=1, n_logical_blocks=n_logical, block_size=16,
+                             block_bytes=bb, stride=stride)
+    seq = 2048
+    params = torch.frombuffer(bytearray(bytes(DeviceStepParams(token_id=0, position=seq - 1, sequence_length=seq,
+                                                               active_batch=1, kv_write_slot=(seq - 1) % 16))),
+                              dtype=torch.uint8).to(dev)
+    max_seq = n_logical * 16
+    b = {"x": torch.randn(1, H, generator=g, device=dev), "h": torch.empty(1, H, device=dev),
+         "y": torch.empty(1, H, device=dev), "qkv": torch.empty(H + 2 * stride, device=dev),
+         "qo": torch.empty(1, H, device=dev), "kvpos": torch.empty(1, dtype=torch.int32, device=dev),
+         "att": torch.empty(1, H, device=dev), "o": torch.empty(H, device=dev), "h2": torch.empty(1, H, device=dev),
+         "y2": torch.empty(1, H, device=dev), "act": torch.empty(I, device=dev), "down": torch.empty(H, device=dev),
+         "out": torch.empty(1, H, device=dev),
+         "ws": torch.empty(max(ops._lib.lib().fellm_rocm_paged_attention_workspace(1, nq, nkv, hd, max_seq) // 4, 1),
+                           dtype=torch.float32, device=dev)}
+    qkv = b["qkv"]
+    q, k, v = qkv[:H].view(1, H), qkv[H:H + stride].view(1, stride), qkv[H + stride:].view(1, stride)
+
+    def layer():
+        ops.rmsnorm(b["x"], n1, 1e-5, out=b["y"])
+        ops.matvec_kquant(w_qkv, b["y"].view(-1), qtype="q4k", out=qkv)
+        ops.step_kv_position(params, 16, out=b["kvpos"])
+        ops.rope_kv_write(q, k, v, inv, b["kvpos"], cache, head_dim=hd,
+                          rope_positions=ops.step_field(params, "position"), q_out=b["qo"])
+        ops.paged_attention(b["qo"], ops.step_field(params, "sequence_length"), cache, n_heads=nq, n_kv_heads=nkv,
+                            head_dim=hd, max_seq=max_seq, out=b["att"], workspace=b["ws"])
+        ops.matvec_kquant(w_o, b["att"].view(-1), qtype="q4k", out=b["o"])
+        ops.add_rmsnorm(b["o"].view(1, H), b["x"], n2, 1e-5, h_out=b["h2"], y_out=b["y2"])
+        ops.gate_up_swiglu(w_g, w_u, b["y2"].view(-1), qtype="q4k", out=b["act"])
+        ops.matvec_kquant(w_d, b["act"], qtype="q4k", out=b["down"])
+        ops.add(b["down"].view(1, H), b["h2"], out=b["out"])
+
+    out["llama8b_decode_layer_q4k"] = time_eager_vs_graph(torch, layer, steps, warmup)
+    out["llama8b_decode_layer_q4k"]["weight_bytes"] = int(sum(t.numel() for t in (w_qkv, w_o, w_g, w_u, w_d)))
+    out["llama8b_decode_layer_plugin"] = plugin_decode_graph(torch, dev, steps, warmup)
+    return out
+
+
+def plugin_decode_graph(torch, dev, steps, warmup):
+    """The same decode layer minus the projections, driven through the plugin
+    ABI with host buffers as FeLLM's host drives it (RmsNorm, rope_kv_write,
+    Attention, add_rmsnorm, GateUpSwiGlu on Q4_K, Add; positions and lengths
+    from the step block, device-resident block table): eager launches (host
+    mirror bookkeeping, snapshot callbacks and error-word reads per launch)
+    against one replay of the captured plugin stream."""
+    import time
+
+    import numpy as np
+
+    from fellm_amd import abi, synth
+    from fellm_amd.plugin_host import PagedKvContext, PluginHost
+
+    D = abi.DType
+    H, I, nq, nkv, hd, n_logical, bs = 4096, 14336, 32, 8, 128, 256, 16
+    stride = nkv * hd
+    rng = np.random.default_rng(10)
+    keep = []
+
+    def tref(a, dt, dims=None, logical_id=0):
+        keep.append(a)
+        return abi.tensor_ref(a.ctypes.data, a.nbytes, dt, dims or [a.size], logical_id)
+
+    def tmut(a, dt, dims=None):
+        keep.append(a)
+        return abi.tensor_mut(a.ctypes.data, a.nbytes, dt, dims or [a.size])
+
+    host = PluginHost()
+    bb = (2 * bs * stride * 2 + 63) // 64 * 64
+    arena = torch.zeros(n_logical * bb, dtype=torch.uint8, device=dev)
+    table = rng.permutation(n_logical).astype(np.uint32)
+    table_dev = torch.from_numpy(table.view(np.int32)).to(dev)
+    host_arena = np.zeros(8, np.uint8)
+    zero = np.zeros(1, np.uint32)
+    ctx = PagedKvContext(arena_ptr=host_arena.ctypes.data, arena_len=8, block_table=table, n_logical_blocks=n_logical,
+                         n_layers=1, tokens_stride=stride, block_bytes=bb, block_size=bs, row_positions=zero,
+                         row_rope_positions=zero, row_lengths=zero + 1, device_arena_ptr=arena.data_ptr(),
+                         device_arena_len=arena.numel(), device_block_table_ptr=table_dev.data_ptr(),
+                         n_device_block_table=table.size, device_logical_stride=n_logical)
+    seq = 2048
+    x = rng.normal(size=H).astype(np.float32)
+    n1 = (1 + 0.1 * rng.normal(size=H)).astype(np.float32)
+    n2 = (1 + 0.1 * rng.normal(size=H)).astype(np.float32)
+    q = rng.normal(size=H).astype(np.float32)
+    k = rng.normal(size=stride).astype(np.float32)
+    v = rng.normal(size=stride).astype(np.float32)
+    inv = (1.0 / (500000.0 ** (np.arange(0, hd, 2) / hd))).astype(np.float32)
+    wg = synth.KQUANT_TABLES[12](rng, I, H)
+    wu = synth.KQUANT_TABLES[12](rng, I, H)
+    y = np.zeros(H, np.float32)
+    qo = np.zeros(H, np.float32)
+    att = np.zeros(H, np.float32)
+    h2 = np.zeros(H, np.float32)
+    y2 = np.zeros(H, np.float32)
+    act = np.zeros(I, np.float32)
+    o = np.zeros(I, np.float32)
+    dummy = np.zeros(1, np.float32)
+    lk = lambda op, i, od: host.lookup(op, i, od)  # noqa: E731
+    h_rms = lk(abi.OpKind.RMSNORM, [D.F32, D.F32], D.F32)
+    h_rkv = lk(abi.OP_ROPE_KV_WRITE, [D.F32, D.F32, D.F32, D.F32], D.F32)
+    h_att = lk(abi.OpKind.ATTENTION, [D.F32, D.F32, D.F32], D.F32)
+    h_arn = lk(abi.OP_ADD_RMSNORM, [D.F32, D.F32, D.F32], D.F32)
+    h_gu = lk(abi.OpKind.GATE_UP_SWIGLU, [D.Q4K, D.Q4K, D.F32], D.F32)
+    h_add = lk(abi.OpKind.ADD, [D.F32, D.F32], D.F32)
+
+    def layer():
+        host.launch(h_rms, abi.OpAttrs(eps=1e-5), [tref(x, D.F32), tref(n1, D.F32)], [tmut(y, D.F32)])
+        host.launch(h_rkv, abi.OpAttrs(n_heads=nq, n_kv_heads=nkv, head_dim=hd, rope_dim=hd, block_size=bs),
+                    [tref(q, D.F32), tref(k, D.F32), tref(v, D.F32), tref(inv, D.F32)], [tmut(qo, D.F32)])
+        host.launch(h_att, abi.OpAttrs(n_heads=nq, n_kv_heads=nkv, head_dim=hd, block_size=bs),
+                    [tref(qo, D.F32), tref(dummy, D.F32), tref(dummy, D.F32)], [tmut(att, D.F32)])
+        host.launch(h_arn, abi.OpAttrs(eps=1e-5), [tref(att, D.F32), tref(x, D.F32), tref(n2, D.F32)],
+                    [tmut(h2, D.F32), tmut(y2, D.F32)])
+        host.launch(h_gu, abi.OpAttrs(), [tref(wg, D.Q4K, [I, H], 91), tref(wu, D.Q4K, [I, H], 92),
+                                          tref(y2, D.F32)], [tmut(act, D.F32)])
+        host.launch(h_add, abi.OpAttrs(), [tref(act, D.F32), tref(act, D.F32)], [tmut(o, D.F32)])
+
+    host.set_paged_context(ctx)
+    try:
+        host.update_step_params(abi.DeviceStepParams(position=seq - 1, sequence_length=seq, active_batch=1,
+                                                     kv_write_slot=(seq - 1) % bs))
+        stream = host.stream()
+        for _ in range(warmup):
+            layer()
+        stream.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            layer()
+        stream.synchronize()
+        eager = (time.perf_counter() - t0) / steps
+        cap = host.begin_graph_capture()
+        try:
+            layer()
+        except Exception:
+            cap.abort()
+            raise
+        exe = cap.finish()
+        for _ in range(warmup):
+            exe.launch(stream)
+        stream.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            exe.launch(stream)
+        stream.synchronize()
+        replay = (time.perf_counter() - t0) / steps
+        exe.close()
+    finally:
+        host.set_paged_context(None)
+    return {"eager_us_per_step": round(eager * 1e6, 2), "graph_us_per_step": round(replay * 1e6, 2),
+            "speedup": round(eager / replay, 2)}
+
+
 # --------------------------------------------------------------------------- #
 # Timing
 # --------------------------------------------------------------------------- #
@@ -478,6 +704,8 @@ def main():
             result[name] = op_report(per_op)
             del chain, sets
             torch.cuda.empty_cache()
+        if not args.only or "next_graph" in args.only.split(","):
+            result["next_graph"] = decode_graph_report(torch, ops, dev, max(args.steps, 50), args.warmup)
         print(json.dumps({"suite": result}, indent=1))
         return
 
