@@ -258,13 +258,14 @@ def gemv_ops(torch, ops, dev, n_sets, seed=6):
 def attention_ops(torch, ops, dev, n_sets, seed=7):
     """Paged decode attention over an f16 cache in FeLLM's layout:
     configs[3]-shaped (Llama-3-70B heads 64/8/128, 256 sequences x 4096 keys,
-    the whole 4.29 GB arena) and one Llama-3-8B sequence of 32768 keys (the
-    split-key path).  Physical blocks are a random permutation."""
+    the whole 4.29 GB arena) and one Llama-3-8B sequence of 32768 or 2048 keys
+    (the split-key path).  Physical blocks are a random permutation."""
     chain = []
     g = torch.Generator(device="cpu")
     g.manual_seed(seed)
     for name, B, seq, nh, nkv, hd in (("attn_decode_70b_b256_s4096", 256, 4096, 64, 8, 128),
-                                      ("attn_decode_8b_b1_s32768", 1, 32768, 32, 8, 128)):
+                                      ("attn_decode_8b_b1_s32768", 1, 32768, 32, 8, 128),
+                                      ("attn_decode_8b_b1_s2048", 1, 2048, 32, 8, 128)):
         stride = nkv * hd
         bb = ops.PagedKvCache.block_bytes_for(stride)
         n_logical = (seq + 15) // 16

@@ -30,6 +30,7 @@
 // kernel combines them.  Tokens outside [lo, seq) are masked with -inf and
 // their V rows read as zero, so stale cache bytes never reach the output.
 #include "common.hpp"
+
 #include "fellm_rocm.h"
 
 namespace fellm {
@@ -125,7 +126,7 @@ __device__ __forceinline__ void split_range(uint32_t seq, uint32_t lo, uint32_t 
 
 // Q: query activation policy, O: output policy, C: cache policy, HD: head
 // dim (64, 128 or 256), GM: maximum query heads per KV head (8 or 16).
-template <typename Q, typename O, typename C, int HD, int GM>
+template <typename Q, typename O, typename C, int HD, int GM, int DEPTH>
 __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T *__restrict__ q,
                                                              typename O::T *__restrict__ out,
                                                              float *__restrict__ part, const uint32_t *__restrict__ lens,
@@ -145,34 +146,6 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
     const uint32_t bg = blockIdx.x / splits;
     const uint32_t g = bg % n_kv, b = bg / n_kv;
     const uint32_t G = n_heads / n_kv;
-    const uint32_t seq = lens[b];
-    const uint32_t lo = (causal && window && seq > window) ? seq - window : 0;
-    uint32_t blk0, blk1;
-    split_range(seq, lo, s, bps, blk0, blk1);
-
-    // q^T as the B operand: head slot col (= query head g*G + col), dims of step st.
-    typename C::Op qb[NS][C::kParts];
-    {
-        const bool hv = col < G;
-        const typename Q::T *qh = q + ((size_t)b * n_heads + (size_t)g * G + (hv ? col : 0)) * HD;
-#pragma unroll
-        for (int st = 0; st < NS; ++st) {
-            float v[4], rem[4];
-            const uint32_t d0 = 32 * (st / 2) + 8 * grp + 4 * (st % 2);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) rem[e] = v[e] = hv ? Q::load(qh[d0 + e]) : 0.0f;
-#pragma unroll
-            for (int p = 0; p < C::kParts; ++p) qb[st][p] = C::part(v, p, rem);
-        }
-    }
-
-    float acc[GM][DP];
-#pragma unroll
-    for (int h = 0; h < GM; ++h)
-#pragma unroll
-        for (int d = 0; d < DP; ++d) acc[h][d] = 0.0f;
-    float m = -__builtin_inff(), l = 0.0f;  // running max / denominator of head slot col
-
     const size_t row_bytes = (size_t)geo.stride * 2;
     const size_t table_base = ((size_t)b * geo.n_layers + geo.layer) * geo.n_logical;
     // One cache block's K and V slices for this lane, fetched through a
@@ -184,10 +157,10 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
         uint32_t vr[4][DP / 2]; // V: token 4i + grp, dims col*DP .. +DP-1
         bool ok;
     };
-    auto fetch = [&](uint32_t blk, BlockRegs &R) {
+    auto fetch = [&](uint32_t blk, uint32_t lim, BlockRegs &R) {
         const size_t ti = table_base + blk;
         const uint64_t phys =
-            (blk < blk1 && blk < geo.n_logical && ti < geo.n_table) ? (uint64_t)table[ti] : ~0ull;
+            (blk < lim && blk < geo.n_logical && ti < geo.n_table) ? (uint64_t)table[ti] : ~0ull;
         const bool ok = phys != ~0ull && (phys + 1) * geo.block_bytes <= geo.arena_len;
         const uint8_t *base = geo.arena + (ok ? phys * geo.block_bytes : 0);
         const Rsrc rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0,
@@ -219,6 +192,51 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
         }
         R.ok = ok;
     };
+    // Without a sliding window the split's first block is s * bps whatever
+    // the sequence length, so it is requested before the length arrives
+    // (tokens past the length are masked in process); with a window the
+    // first block depends on the length and is fetched once it is known.
+    const bool spec = !(causal && window);
+    // DEPTH blocks are in flight ahead of the one being reduced.
+    BlockRegs ra, rb, rc;
+    if constexpr (DEPTH == 2) fetch(s * bps + 1, spec ? s * bps + bps : 0u, rb);
+    fetch(s * bps, spec ? s * bps + bps : 0u, ra);
+    const uint32_t seq = lens[b];
+    const uint32_t lo = (causal && window && seq > window) ? seq - window : 0;
+    uint32_t blk0, blk1;
+    split_range(seq, lo, s, bps, blk0, blk1);
+
+    // q^T as the B operand: head slot col (= query head g*G + col), dims of step st.
+    typename C::Op qb[NS][C::kParts];
+    {
+        // Steps 2j and 2j+1 use dims 32j + 8 grp .. +7: one vector load each.
+        const bool hv = col < G;
+        const typename Q::T *qh = q + ((size_t)b * n_heads + (size_t)g * G + (hv ? col : 0)) * HD;
+        float qv[NS / 2][8];
+#pragma unroll
+        for (int j = 0; j < NS / 2; ++j) {
+            load_f32<Q, 8>(qh + 32 * j + 8 * grp, qv[j]);
+            if (!hv)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qv[j][e] = 0.0f;
+        }
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            float v[4], rem[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rem[e] = v[e] = qv[st / 2][4 * (st % 2) + e];
+#pragma unroll
+            for (int p = 0; p < C::kParts; ++p) qb[st][p] = C::part(v, p, rem);
+        }
+    }
+
+    float acc[GM][DP];
+#pragma unroll
+    for (int h = 0; h < GM; ++h)
+#pragma unroll
+        for (int d = 0; d < DP; ++d) acc[h][d] = 0.0f;
+    float m = -__builtin_inff(), l = 0.0f;  // running max / denominator of head slot col
+
     auto process = [&](uint32_t blk, const BlockRegs &R) {
         const bool blk_ok = R.ok;
         const uint4(&kr)[NKL] = R.kr;
@@ -306,14 +324,30 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
         };
-    BlockRegs ra, rb;
-    fetch(blk0, ra);
-    for (uint32_t blk = blk0; blk < blk1; blk += 2) {
-        fetch(blk + 1, rb);
-        process(blk, ra);
-        if (blk + 1 >= blk1) break;
-        fetch(blk + 2, ra);
-        process(blk + 1, rb);
+    if constexpr (DEPTH == 2) {
+        if (!spec) {
+            fetch(blk0, blk1, ra);
+            fetch(blk0 + 1, blk1, rb);
+        }
+        for (uint32_t blk = blk0; blk < blk1; blk += 3) {
+            fetch(blk + 2, blk1, rc);
+            process(blk, ra);
+            if (blk + 1 >= blk1) break;
+            fetch(blk + 3, blk1, ra);
+            process(blk + 1, rb);
+            if (blk + 2 >= blk1) break;
+            fetch(blk + 4, blk1, rb);
+            process(blk + 2, rc);
+        }
+    } else {
+        if (!spec) fetch(blk0, blk1, ra);
+        for (uint32_t blk = blk0; blk < blk1; blk += 2) {
+            fetch(blk + 1, blk1, rb);
+            process(blk, ra);
+            if (blk + 1 >= blk1) break;
+            fetch(blk + 2, blk1, ra);
+            process(blk + 1, rb);
+        }
     }
 
     // Sum the four token groups; lanes 0..15 then hold dims col*DP .. of every head.
@@ -361,51 +395,81 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
 }
 
 // Combine the splits of one (b, query head): M = max m_s, w_s = exp(m_s - M),
-// out = sum w_s acc_s / sum w_s l_s.  256 threads: the split maxima and
-// weights are formed in parallel through LDS, then thread d sums dimension d.
-constexpr int kCombineThreads = 256;
-constexpr uint32_t kMaxSplits = 128;
+// out = sum w_s acc_s / sum w_s l_s.  1024 threads: thread (p, d) owns
+// dimension d of splits p, p + kParts, ...  Every load (the partial sums and
+// each split's m, l) is issued up front, so the kernel pays one memory
+// latency; the maxima, weights and denominators then go through LDS.
+constexpr int kCombineThreads = 1024;
+constexpr uint32_t kMaxSplits = 256;
 
 template <typename O, int HD, int GM>
 __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine(const float *__restrict__ part,
                                                                         typename O::T *__restrict__ out,
                                                                         uint32_t n_heads, uint32_t n_kv,
                                                                         uint32_t splits) {
+    constexpr int kParts = kCombineThreads / HD;
+    constexpr int kPer = kMaxSplits / kParts;  // splits per thread at most
+    constexpr int kWaves = kCombineThreads / kWave;
     __shared__ float w_lds[kMaxSplits];
-    __shared__ float red[kCombineThreads / kWave];
+    __shared__ float red[kWaves];
+    __shared__ float acc_lds[kParts][HD];
     const uint32_t bh = blockIdx.x, h = bh % n_heads, b = bh / n_heads;
     const uint32_t G = n_heads / n_kv, g = h / G, slot = h % G;
     constexpr uint32_t kRec = GM * (HD + 2);
     const float *base = part + ((size_t)(b * n_kv + g) * splits) * kRec + slot * (HD + 2);
-    const uint32_t t = threadIdx.x;
+    const uint32_t t = threadIdx.x, d = t % HD, p = t / HD;
+    float av[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t sp = p + (uint32_t)i * kParts;
+        av[i] = sp < splits ? base[(size_t)sp * kRec + d] : 0.0f;
+    }
     const float ms = t < splits ? base[(size_t)t * kRec + HD] : -__builtin_inff();
+    const float ls = t < splits ? base[(size_t)t * kRec + HD + 1] : 0.0f;
     float M = wave_max(ms);
     if (t % kWave == 0) red[t / kWave] = M;
     __syncthreads();
-    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    M = red[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) M = fmaxf(M, red[i]);
     const float w = (t < splits && ms > -__builtin_inff()) ? __expf(ms - M) : 0.0f;
-    if (t < splits) w_lds[t] = w;
-    const float lw = t < splits ? w * base[(size_t)t * kRec + HD + 1] : 0.0f;
-    __syncthreads();
-    float L = wave_sum(lw);
+    if (t < kMaxSplits) w_lds[t] = w;
+    float L = wave_sum(w * ls);
     __syncthreads();
     if (t % kWave == 0) red[t / kWave] = L;
     __syncthreads();
-    L = (red[0] + red[1]) + (red[2] + red[3]);
+    L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) L += red[i];
+    float o = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t sp = p + (uint32_t)i * kParts;
+        if (sp < splits) o += w_lds[sp] * av[i];
+    }
+    acc_lds[p][d] = o;
+    __syncthreads();
     if (t < (uint32_t)HD) {
-        float o = 0.0f;
-        for (uint32_t s = 0; s < splits; ++s) o += w_lds[s] * base[(size_t)s * kRec + t];
-        out[((size_t)b * n_heads + h) * HD + t] = O::store(L > 0.0f ? o * (1.0f / L) : 0.0f);
+        float r = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kParts; ++q) r += acc_lds[q][t];
+        out[((size_t)b * n_heads + h) * HD + t] = O::store(L > 0.0f ? r * (1.0f / L) : 0.0f);
     }
 }
 
-// Split count: enough wavefronts to cover the chip (~8 per CU) when batch * n_kv is small,
-// at least 16 blocks (256 keys) per split, at most kMaxSplits.
+// Split count: about kTargetWaves wavefronts when batch * n_kv is small, at
+// least kMinSplitBlocks blocks per split, at most kMaxSplits.
+// Measured (one Llama-3-8B sequence, 8 KV heads): 2048 keys took 32 us with
+// 16-block splits and 17.5 us with 2-block ones; 32768 keys did best at
+// 128 splits (1024 wavefronts) rather than 256.
+constexpr uint32_t kMinSplitBlocks = 2;
+constexpr uint32_t kTargetWaves = 1024;
+constexpr uint32_t kDeepWalk = 64;  // blocks per wavefront from which DEPTH 2 is used
 uint32_t choose_splits(uint32_t batch, uint32_t n_kv, uint32_t max_seq) {
     const uint32_t pairs = batch * n_kv;
     const uint32_t blocks = (max_seq + kBlockTokens - 1) / kBlockTokens;
-    uint32_t s = pairs >= 2048 ? 1 : (2048 + pairs - 1) / pairs;
-    const uint32_t cap = blocks / 16 > 0 ? blocks / 16 : 1;
+    uint32_t s = pairs >= kTargetWaves ? 1 : (kTargetWaves + pairs - 1) / pairs;
+    const uint32_t cap = blocks / kMinSplitBlocks > 0 ? blocks / kMinSplitBlocks : 1;
     if (s > cap) s = cap;
     if (s > kMaxSplits) s = kMaxSplits;
     return s ? s : 1;
@@ -420,9 +484,16 @@ int launch_decode(const void *q, void *out, uint32_t batch, uint32_t n_heads, ui
     if (splits > 1 && (!ws || ws_bytes < need)) splits = 1;
     const uint32_t blocks = (max_seq + kBlockTokens - 1) / kBlockTokens;
     const uint32_t bps = (blocks + splits - 1) / splits;
-    hipLaunchKernelGGL((paged_decode_kernel<Q, O, C, HD, GM>), dim3(batch * n_kv * splits), dim3(kWave), 0, st,
-                       static_cast<const typename Q::T *>(q), static_cast<typename O::T *>(out), ws, lens, geo.table, geo,
-                       n_heads, n_kv, scale, causal, window, splits, bps > 0 ? bps : 1);
+    // Two blocks in flight pay off on long walks (256 sequences x 4096 keys:
+    // 754 -> 720 us); splits of a few blocks do better with one.
+    if (bps >= kDeepWalk)
+        hipLaunchKernelGGL((paged_decode_kernel<Q, O, C, HD, GM, 2>), dim3(batch * n_kv * splits), dim3(kWave), 0,
+                           st, static_cast<const typename Q::T *>(q), static_cast<typename O::T *>(out), ws, lens,
+                           geo.table, geo, n_heads, n_kv, scale, causal, window, splits, bps);
+    else
+        hipLaunchKernelGGL((paged_decode_kernel<Q, O, C, HD, GM, 1>), dim3(batch * n_kv * splits), dim3(kWave), 0,
+                           st, static_cast<const typename Q::T *>(q), static_cast<typename O::T *>(out), ws, lens,
+                           geo.table, geo, n_heads, n_kv, scale, causal, window, splits, bps > 0 ? bps : 1);
     int rc = launch_status();
     if (rc != FELLM_OK || splits == 1) return rc;
     hipLaunchKernelGGL((paged_decode_combine<O, HD, GM>), dim3(batch * n_heads), dim3(kCombineThreads), 0, st, ws,
