@@ -224,7 +224,8 @@ def c5_ops(torch, ops, dev, n_sets, seed=5):
 def gemv_ops(torch, ops, dev, n_sets, seed=6):
     """Decode FFN gate/up GEMV + SwiGLU (GateUpSwiGlu) on GGUF K-quant weights:
     Llama-3-8B (14336 x 4096) as Q4_K and Q6_K, Llama-3-70B (28672 x 8192) as
-    Q4_K.  One activation vector; weights rotate over enough copies (device
+    Q4_K; each also as quantize_q8k + the _q8k GEMV (x quantized once per
+    call instead of once per workgroup, both launches timed).  One activation vector; weights rotate over enough copies (device
     rolls of one synthetic matrix) that every launch streams them from HBM."""
     import numpy as np
 
@@ -249,8 +250,39 @@ def gemv_ops(torch, ops, dev, n_sets, seed=6):
             i = s["i"][key] = (s["i"][key] + 1) % len(mats)
             ops.gate_up_swiglu(mats[i][0], mats[i][1], x, qtype=qt, out=out)
 
+        xq = torch.empty(ops._lib.lib().fellm_rocm_q8k_bytes(cols), dtype=torch.uint8, device=dev)
+
+        def fn_q8k(s, mats=mats, x=x, out=out, qt=qt, key=name, xq=xq):
+            i = s["i"][key] = (s["i"][key] + 1) % len(mats)
+            ops.quantize_q8k(x, out=xq)
+            ops.gate_up_swiglu_q8k(mats[i][0], mats[i][1], xq, qtype=qt, out=out)
+
         chain.append(Op(name, nbytes, fn))
-    state = {"i": {c[0]: 0 for c in cases}}
+        chain.append(Op(name + "_q8k", nbytes, fn_q8k))
+    # Plain K-quant GEMVs of a Llama-3-8B decode layer: QKV (6144 x 4096) and
+    # down (4096 x 14336, rows longer than one 32-block pass).
+    mv_cases = (("matvec_q4k_8b_qkv", 6144, 4096, max(n_sets, 16)), ("matvec_q4k_8b_down", 4096, 14336, max(n_sets, 8)))
+    for name, rows, cols, nset in mv_cases:
+        w0 = torch.from_numpy(synth.KQUANT_TABLES[12](rng, rows, cols)).to(dev)
+        mats = [w0.roll(3 * i, 0).contiguous() for i in range(nset)]
+        x = torch.randn(cols, device=dev)
+        out = torch.empty(rows, device=dev)
+        nbytes = w0.numel() + cols * 4 + rows * 4
+
+        def fn(s, mats=mats, x=x, out=out, key=name):
+            i = s["i"][key] = (s["i"][key] + 1) % len(mats)
+            ops.matvec_kquant(mats[i], x, qtype="q4k", out=out)
+
+        xq = torch.empty(ops._lib.lib().fellm_rocm_q8k_bytes(cols), dtype=torch.uint8, device=dev)
+
+        def fn_q8k(s, mats=mats, x=x, out=out, key=name, xq=xq):
+            i = s["i"][key] = (s["i"][key] + 1) % len(mats)
+            ops.quantize_q8k(x, out=xq)
+            ops.matvec_kquant_q8k(mats[i], xq, qtype="q4k", out=out)
+
+        chain.append(Op(name, nbytes, fn))
+        chain.append(Op(name + "_q8k", nbytes, fn_q8k))
+    state = {"i": {c[0]: 0 for c in cases + tuple((m[0], 0, 0, 0, 0, 0) for m in mv_cases)}}
     sets = [state]
     return chain, sets, 1
 

@@ -49,6 +49,10 @@ namespace {
 constexpr int kGemvBlock = 256;
 constexpr int kGemvWaves = kGemvBlock / kWave;
 constexpr uint32_t kGemvMaxCols = 49152;
+#ifndef FELLM_GEMV_MAX_GRID_PRE
+#define FELLM_GEMV_MAX_GRID_PRE 1024
+#endif
+constexpr uint32_t kGemvMaxGridPre = FELLM_GEMV_MAX_GRID_PRE;
 
 // Q8_K copy of x in (dynamic) LDS: qs[cols], bsums[cols/16], d[cols/256],
 // then the per-wavefront row-fold buffers [waves][rows][matrices][nb rounded up to 4].
@@ -69,10 +73,12 @@ __device__ __forceinline__ XLds carve_lds(uint8_t *base, uint32_t nb) {
 }
 
 // quantize_row_q8_k_avx2 (matmul.rs:213-270) for the 256-element blocks of x:
-// wavefront w takes blocks w, w + 4, ...; lane l holds elements 4l..4l+3.
-__device__ void quantize_x(const float *__restrict__ x, uint32_t nb, const XLds &xl) {
-    const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    for (uint32_t b = wave; b < nb; b += kGemvWaves) {
+// wavefront `first` takes blocks first, first + stride, ...; lane l holds
+// elements 4l..4l+3.  xl may point into LDS or global memory.
+__device__ void quantize_x(const float *__restrict__ x, uint32_t nb, const XLds &xl, uint32_t first,
+                           uint32_t stride) {
+    const uint32_t lane = threadIdx.x % kWave;
+    for (uint32_t b = first; b < nb; b += stride) {
         const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)b * 256 + lane * 4);
         float a = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
                         fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
@@ -98,6 +104,37 @@ __device__ void quantize_x(const float *__restrict__ x, uint32_t nb, const XLds 
         s += __shfl_xor(s, 2, kWave);
         if ((lane & 3) == 0) xl.bs[b * 16 + lane / 4] = (int16_t)s;
         if (lane == 0) xl.d[b] = a / 127.0f;
+    }
+}
+
+// The Q8_K activation blob: the same layout in global memory as in LDS
+// (qs[nb * 256] int8, bsums[nb * 16] int16, d[nb] f32; nb * 292 bytes).
+__host__ __device__ constexpr uint32_t q8k_blob_bytes(uint32_t nb) { return nb * 292; }
+
+// x into the workgroup's LDS: quantized here (PREQ = false), or copied from a
+// blob that fellm_rocm_quantize_q8k wrote once for the whole launch.
+template <bool PREQ>
+__device__ __forceinline__ void fill_x(const void *__restrict__ xsrc, uint32_t nb, const XLds &xl, uint8_t *smem) {
+    if constexpr (PREQ) {
+        const uint32_t words = q8k_blob_bytes(nb) / 4;
+        const uint32_t *src = static_cast<const uint32_t *>(xsrc);
+        uint32_t *dst = reinterpret_cast<uint32_t *>(smem);
+        constexpr int kBatch = 4;
+        for (uint32_t i0 = threadIdx.x; i0 < words; i0 += blockDim.x * kBatch) {
+            uint32_t v[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const uint32_t i = i0 + j * blockDim.x;
+                v[j] = i < words ? src[i] : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const uint32_t i = i0 + j * blockDim.x;
+                if (i < words) dst[i] = v[j];
+            }
+        }
+    } else {
+        quantize_x(static_cast<const float *>(xsrc), nb, xl, threadIdx.x / kWave, kGemvWaves);
     }
 }
 
@@ -418,10 +455,10 @@ constexpr uint32_t kStagePerWave = 1024 * (kChunks<GW> + (FUSED ? kChunks<UW> : 
 // fold buffer; after a row's last unit, lanes 0 .. mats*rows-1 each fold one
 // (row, matrix) serially over its block values from 0.0 and the even lanes
 // apply silu(gate) * up; then the next unit is written to the stage.
-template <typename GW, typename UW, bool FUSED, bool MULTI>
+template <typename GW, typename UW, bool FUSED, bool MULTI, bool PREQ>
 __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *__restrict__ gw,
                                                                   const uint8_t *__restrict__ uw,
-                                                                  const float *__restrict__ x, float *__restrict__ out,
+                                                                  const void *__restrict__ x, float *__restrict__ out,
                                                                   uint32_t rows, uint32_t nb, uint32_t rp) {
     constexpr uint32_t kMats = FUSED ? 2 : 1;
     extern __shared__ __align__(16) uint8_t gemv_smem[];
@@ -475,7 +512,7 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *
         constexpr ExpfTable T = make_expf_table();
         if (threadIdx.x < 32) tab_lds[threadIdx.x] = T.tab[threadIdx.x];
     }
-    quantize_x(x, nb, xl);
+    fill_x<PREQ>(x, nb, xl, gemv_smem);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
@@ -534,10 +571,10 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *
 // Rows whose bytes do not end on a 16-byte boundary (Q6_K rows of nb % 8 != 0
 // blocks) are finished by this direct kernel so that no staged chunk reaches
 // past the matrix: one wavefront per row, blocks read straight from memory.
-template <typename GW, typename UW, bool FUSED>
+template <typename GW, typename UW, bool FUSED, bool PREQ>
 __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_direct(const uint8_t *__restrict__ gw,
                                                                   const uint8_t *__restrict__ uw,
-                                                                  const float *__restrict__ x, float *__restrict__ out,
+                                                                  const void *__restrict__ x, float *__restrict__ out,
                                                                   uint32_t rows, uint32_t nb) {
     constexpr uint32_t kMats = FUSED ? 2 : 1;
     extern __shared__ __align__(16) uint8_t gemv_smem[];
@@ -547,7 +584,7 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_direct(const uint8_t *
     const uint32_t h = lane & 1, slot = lane >> 1;
     const uint32_t nbp = (nb + 3) & ~3u;
     stage_expf_table(tab_lds);
-    quantize_x(x, nb, xl);
+    fill_x<PREQ>(x, nb, xl, gemv_smem);
     __syncthreads();
     float *fold = xl.fold + wave * kMats * nbp;
     for (uint32_t row = blockIdx.x * kGemvWaves + wave; row < rows; row += gridDim.x * kGemvWaves) {
@@ -575,9 +612,19 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_direct(const uint8_t *
     }
 }
 
-template <typename GW, typename UW, bool FUSED>
-int launch_gemv(const void *gw, const void *uw, const float *x, float *out, uint32_t rows, uint32_t cols,
+// Standalone Q8_K quantization of x into a blob (one wavefront per block).
+__global__ __launch_bounds__(kGemvBlock) void quantize_q8k_kernel(const float *__restrict__ x, uint32_t nb,
+                                                                   uint8_t *__restrict__ blob) {
+    const XLds xl = carve_lds(blob, nb);
+    quantize_x(x, nb, xl, blockIdx.x * kGemvWaves + threadIdx.x / kWave, gridDim.x * kGemvWaves);
+}
+
+template <typename GW, typename UW, bool FUSED, bool PREQ = false>
+int launch_gemv(const void *gw, const void *uw, const void *x, float *out, uint32_t rows, uint32_t cols,
                 hipStream_t s) {
+    // With x already quantized the prologue is a copy, so more workgroups
+    // (more wavefronts in flight) pay off.
+    const uint32_t max_grid = PREQ ? kGemvMaxGridPre : FELLM_GEMV_MAX_GRID;
     const uint32_t nb = cols / 256;
     const uint32_t mats = FUSED ? 2 : 1;
     const uint32_t nbp = (nb + 3) & ~3u;
@@ -596,15 +643,15 @@ int launch_gemv(const void *gw, const void *uw, const float *x, float *out, uint
         if (nb <= 32) {
             const uint32_t rp = 32 / nb;
             uint32_t grid = (n + kGemvWaves * rp - 1) / (kGemvWaves * rp);
-            if (grid > FELLM_GEMV_MAX_GRID) grid = FELLM_GEMV_MAX_GRID;
+            if (grid > max_grid) grid = max_grid;
             const uint32_t lds = gemv_lds_bytes(nb, mats * rp * nbp) + kGemvWaves * kStagePerWave<GW, UW, FUSED>;
-            hipLaunchKernelGGL((kquant_gemv_kernel<GW, UW, FUSED, false>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
+            hipLaunchKernelGGL((kquant_gemv_kernel<GW, UW, FUSED, false, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
                                out + r0, n, nb, rp);
         } else {
             uint32_t grid = (n + kGemvWaves - 1) / kGemvWaves;
-            if (grid > FELLM_GEMV_MAX_GRID) grid = FELLM_GEMV_MAX_GRID;
+            if (grid > max_grid) grid = max_grid;
             const uint32_t lds = gemv_lds_bytes(nb, mats * nbp) + kGemvWaves * kStagePerWave<GW, UW, FUSED>;
-            hipLaunchKernelGGL((kquant_gemv_kernel<GW, UW, FUSED, true>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
+            hipLaunchKernelGGL((kquant_gemv_kernel<GW, UW, FUSED, true, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
                                out + r0, n, nb, 1u);
         }
         const int rc = launch_status();
@@ -614,7 +661,7 @@ int launch_gemv(const void *gw, const void *uw, const float *x, float *out, uint
         const uint32_t n = rows - rows_main;
         const uint8_t *g = g8 + (uint64_t)rows_main * nb * GW::kBytes;
         const uint8_t *u = FUSED ? u8 + (uint64_t)rows_main * nb * UW::kBytes : nullptr;
-        hipLaunchKernelGGL((kquant_gemv_direct<GW, UW, FUSED>), dim3((n + kGemvWaves - 1) / kGemvWaves),
+        hipLaunchKernelGGL((kquant_gemv_direct<GW, UW, FUSED, PREQ>), dim3((n + kGemvWaves - 1) / kGemvWaves),
                            dim3(kGemvBlock), gemv_lds_bytes(nb, mats * nbp), s, g, u, x, out + rows_main, n, nb);
         const int rc = launch_status();
         if (rc != FELLM_OK) return rc;
@@ -627,7 +674,7 @@ bool kquant_ok(uint32_t dt) { return dt == FELLM_DTYPE_Q4K || dt == FELLM_DTYPE_
 // Q4_K and Q5_K blocks (144 and 176 bytes) are read with aligned 16-byte loads.
 bool weight_aligned(const void *w, uint32_t dt) { return dt == FELLM_DTYPE_Q6K || aligned_to(w, 16); }
 
-int check_gemv(const void *w, uint32_t dt, const float *x, const float *out, uint32_t cols) {
+int check_gemv(const void *w, uint32_t dt, const void *x, const float *out, uint32_t cols) {
     if (!w || !x || !out) return FELLM_ERR_ARITY;
     if (!kquant_ok(dt)) return FELLM_ERR_DTYPE;
     if (cols == 0 || cols % 256 != 0 || cols > kGemvMaxCols) return FELLM_ERR_SHAPE;
@@ -670,4 +717,55 @@ extern "C" int fellm_rocm_matvec_kquant(const void *w, uint32_t w_dtype, uint32_
     if (w_dtype == FELLM_DTYPE_Q4K) return launch_gemv<Q4K, Q4K, false>(w, nullptr, x, y, rows, cols, s);
     if (w_dtype == FELLM_DTYPE_Q5K) return launch_gemv<Q5K, Q5K, false>(w, nullptr, x, y, rows, cols, s);
     return launch_gemv<Q6K, Q6K, false>(w, nullptr, x, y, rows, cols, s);
+}
+
+extern "C" uint64_t fellm_rocm_q8k_bytes(uint32_t cols) {
+    using namespace fellm;
+    return cols % 256 ? 0 : q8k_blob_bytes(cols / 256);
+}
+
+extern "C" int fellm_rocm_quantize_q8k(const float *x, uint32_t cols, void *xq, void *stream) {
+    using namespace fellm;
+    if (!x || !xq) return FELLM_ERR_ARITY;
+    if (cols == 0 || cols % 256 != 0 || cols > kGemvMaxCols) return FELLM_ERR_SHAPE;
+    if (!aligned_to(x, 16) || !aligned_to(xq, 16)) return FELLM_ERR_SHAPE;
+    const uint32_t nb = cols / 256;
+    hipLaunchKernelGGL(quantize_q8k_kernel, dim3((nb + kGemvWaves - 1) / kGemvWaves), dim3(kGemvBlock), 0,
+                       as_stream(stream), x, nb, static_cast<uint8_t *>(xq));
+    return launch_status();
+}
+
+extern "C" int fellm_rocm_gate_up_swiglu_q8k(const void *gate_w, uint32_t gate_dtype, const void *up_w,
+                                             uint32_t up_dtype, uint32_t rows, uint32_t cols, const void *xq,
+                                             float *out, void *stream) {
+    using namespace fellm;
+    if (rows == 0 && kquant_ok(gate_dtype) && kquant_ok(up_dtype) && cols % 256 == 0) return FELLM_OK;
+    int rc = check_gemv(gate_w, gate_dtype, xq, out, cols);
+    if (rc == FELLM_OK) rc = check_gemv(up_w, up_dtype, xq, out, cols);
+    if (rc != FELLM_OK) return rc;
+    hipStream_t s = as_stream(stream);
+#define FELLM_GU(GT, GD, UT, UD) \
+    if (gate_dtype == GD && up_dtype == UD) return launch_gemv<GT, UT, true, true>(gate_w, up_w, xq, out, rows, cols, s);
+#define FELLM_GU_ROW(GT, GD)                 \
+    FELLM_GU(GT, GD, Q4K, FELLM_DTYPE_Q4K)   \
+    FELLM_GU(GT, GD, Q5K, FELLM_DTYPE_Q5K)   \
+    FELLM_GU(GT, GD, Q6K, FELLM_DTYPE_Q6K)
+    FELLM_GU_ROW(Q4K, FELLM_DTYPE_Q4K)
+    FELLM_GU_ROW(Q5K, FELLM_DTYPE_Q5K)
+    FELLM_GU_ROW(Q6K, FELLM_DTYPE_Q6K)
+#undef FELLM_GU_ROW
+#undef FELLM_GU
+    return FELLM_ERR_DTYPE;
+}
+
+extern "C" int fellm_rocm_matvec_kquant_q8k(const void *w, uint32_t w_dtype, uint32_t rows, uint32_t cols,
+                                            const void *xq, float *y, void *stream) {
+    using namespace fellm;
+    if (rows == 0 && kquant_ok(w_dtype) && cols % 256 == 0) return FELLM_OK;
+    const int rc = check_gemv(w, w_dtype, xq, y, cols);
+    if (rc != FELLM_OK) return rc;
+    hipStream_t s = as_stream(stream);
+    if (w_dtype == FELLM_DTYPE_Q4K) return launch_gemv<Q4K, Q4K, false, true>(w, nullptr, xq, y, rows, cols, s);
+    if (w_dtype == FELLM_DTYPE_Q5K) return launch_gemv<Q5K, Q5K, false, true>(w, nullptr, xq, y, rows, cols, s);
+    return launch_gemv<Q6K, Q6K, false, true>(w, nullptr, xq, y, rows, cols, s);
 }

@@ -321,6 +321,47 @@ def moe_combine(expert_out, weights, *, ids=None, inv=None, y0=None, out=None):
     return out
 
 
+def quantize_q8k(x, out=None):
+    """x (f32 vector, cols % 256 == 0) -> Q8_K blob (uint8 tensor) for the
+    *_q8k GEMVs: qs int8 [cols], bsums int16 [cols/16], d f32 [cols/256]."""
+    _dev(x)
+    if x.dtype != torch.float32 or x.dim() != 1:
+        raise TypeError("x must be a float32 vector")
+    n = _lib.lib().fellm_rocm_q8k_bytes(x.numel())
+    out = out if out is not None else torch.empty(n, dtype=torch.uint8, device=x.device)
+    _lib.call("fellm_rocm_quantize_q8k", _p(x), x.numel(), _p(out), _stream())
+    return out
+
+
+def _q8k_cols(xq) -> int:
+    if xq.dtype != torch.uint8 or xq.numel() % 292:
+        raise ValueError("xq must be a Q8_K blob from quantize_q8k")
+    return xq.numel() // 292 * 256
+
+
+def gate_up_swiglu_q8k(gate_w, up_w, xq, *, qtype: str = "q4k", up_qtype: str | None = None, out=None):
+    """gate_up_swiglu over an activation already quantized by quantize_q8k."""
+    _dev(gate_w, up_w, xq)
+    cols = _q8k_cols(xq)
+    rows = gate_w.shape[0]
+    g = _kquant_code(qtype, gate_w, cols)
+    u = _kquant_code(up_qtype or qtype, up_w, cols)
+    out = out if out is not None else torch.empty(rows, dtype=torch.float32, device=xq.device)
+    _lib.call("fellm_rocm_gate_up_swiglu_q8k", _p(gate_w), g, _p(up_w), u, rows, cols, _p(xq), _p(out), _stream())
+    return out
+
+
+def matvec_kquant_q8k(w, xq, *, qtype: str = "q4k", out=None):
+    """matvec_kquant over an activation already quantized by quantize_q8k."""
+    _dev(w, xq)
+    cols = _q8k_cols(xq)
+    rows = w.shape[0]
+    code = _kquant_code(qtype, w, cols)
+    out = out if out is not None else torch.empty(rows, dtype=torch.float32, device=xq.device)
+    _lib.call("fellm_rocm_matvec_kquant_q8k", _p(w), code, rows, cols, _p(xq), _p(out), _stream())
+    return out
+
+
 def step_kv_position(params, block_size: int, out=None):
     """KV position of the single decode row from a device DeviceStepParams
     block (uint8 [48] tensor): ((sequence_length - 1) // block_size) *

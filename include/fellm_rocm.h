@@ -213,6 +213,23 @@ int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void *out, uint3
                                void *stream);
 
 /*
+ * x quantized once to Q8_K for any number of K-quant GEMVs over it, as the
+ * CPU backend does per matmul (matmul.rs:213-270 quantize_row_q8_k_avx2; the
+ * CUDA plugin's quantize_q8_32 plays the same role for its own format).
+ * The blob holds qs[cols] int8, bsums[cols / 16] int16, d[cols / 256] f32
+ * (fellm_rocm_q8k_bytes(cols) = cols / 256 * 292 bytes, 16-byte aligned).
+ * The _q8k GEMVs take the blob instead of x and give the same bits as
+ * fellm_rocm_gate_up_swiglu / fellm_rocm_matvec_kquant on that x; their
+ * workgroups copy the blob instead of quantizing x each.
+ */
+uint64_t fellm_rocm_q8k_bytes(uint32_t cols);
+int fellm_rocm_quantize_q8k(const float *x, uint32_t cols, void *xq, void *stream);
+int fellm_rocm_gate_up_swiglu_q8k(const void *gate_w, uint32_t gate_dtype, const void *up_w, uint32_t up_dtype,
+                                  uint32_t rows, uint32_t cols, const void *xq, float *out, void *stream);
+int fellm_rocm_matvec_kquant_q8k(const void *w, uint32_t w_dtype, uint32_t rows, uint32_t cols, const void *xq,
+                                 float *y, void *stream);
+
+/*
  * MoE dispatch: group the routed assignments a = token * top_k + slot by expert.
  *   replaces: fill_u32 + moe_count_assignments + moe_prefix_offsets +
  *             moe_scatter_assignments (plugins/cuda_kernels/src/

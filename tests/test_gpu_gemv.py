@@ -113,3 +113,59 @@ def test_gemv_rejects_bad_shapes(ops, dev):
     with pytest.raises(FellmRocmError):
         ops.matvec_kquant(torch.zeros((4, 2 * 144), dtype=torch.uint8, device=dev),
                           torch.zeros(513, device=dev)[1:])  # x not 16-byte aligned
+
+
+# ---- x quantized once: fellm_rocm_quantize_q8k + the _q8k GEMVs ------------------
+
+
+def split_blob(blob: np.ndarray, cols: int):
+    nb = cols // 256
+    qs = blob[: nb * 256].view(np.int8)
+    bs = blob[nb * 256: nb * 288].view(np.int16)
+    d = blob[nb * 288: nb * 292].view(np.float32)
+    return qs, bs, d
+
+
+@pytest.mark.parametrize("cols", [256, 4096, 14336, 49152])
+def test_quantize_q8k_blob(ops, dev, cols):
+    """The blob equals the oracle's Q8_K quantization (qs, bsums, d), with
+    the edge blocks of test_matvec_q8k_edges in it."""
+    rng = np.random.default_rng(cols)
+    x = (rng.normal(size=cols) * rng.uniform(0.01, 20.0, size=cols)).astype(np.float32)
+    if cols >= 1024:
+        x[0:256] = 0.0
+        x[256:512] = rng.integers(-127, 128, size=256).astype(np.float32) + np.float32(0.5)
+        x[256] = 127.0
+        x[512:768] = np.float32(1e-40) * rng.integers(-3, 4, size=256)
+    blob = ops.quantize_q8k(to_dev(x, dev)).cpu().numpy()
+    assert blob.size == cols // 256 * 292
+    qs, bs, d = split_blob(blob, cols)
+    rq, rb, rd = oracle.quantize_q8k(x)
+    assert np.array_equal(qs, rq) and np.array_equal(bs, rb) and np.array_equal(d.view(np.uint32), rd.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [12, 13, 14])
+@pytest.mark.parametrize("cols", [256, 3584, 4096, 4352, 8192, 14336, 16640])
+def test_matvec_kquant_q8k_matches(ops, dev, dtype, cols):
+    """Same bits as matvec_kquant (and the oracle), including two- and
+    three-pass rows and the Q6_K rows finished by the direct kernel."""
+    rng = np.random.default_rng(dtype * 11 + cols)
+    rows = 131
+    w = weights(rng, dtype, rows, cols)
+    x = (rng.normal(size=cols) * rng.uniform(0.01, 20.0, size=cols)).astype(np.float32)
+    wd, xd = to_dev(w, dev), to_dev(x, dev)
+    got = ops.matvec_kquant_q8k(wd, ops.quantize_q8k(xd), qtype=NAMES[dtype]).cpu().numpy()
+    assert_exact(got, ops.matvec_kquant(wd, xd, qtype=NAMES[dtype]).cpu().numpy(), "q8k vs in-kernel quantization")
+    assert_exact(got, oracle.matvec_kquant(dtype, w, rows, cols, x), f"matvec_q8k {NAMES[dtype]} cols={cols}")
+
+
+@pytest.mark.parametrize("gt,ut", [(12, 12), (13, 14), (14, 14), (14, 12)])
+def test_gate_up_swiglu_q8k_matches(ops, dev, gt, ut):
+    rng = np.random.default_rng(gt * 17 + ut)
+    rows, cols = 1000, 4096
+    g, u = weights(rng, gt, rows, cols), weights(rng, ut, rows, cols)
+    x = rng.normal(size=cols).astype(np.float32)
+    xq = ops.quantize_q8k(to_dev(x, dev))
+    got = ops.gate_up_swiglu_q8k(to_dev(g, dev), to_dev(u, dev), xq, qtype=NAMES[gt], up_qtype=NAMES[ut])
+    assert_exact(got.cpu().numpy(), oracle.gate_up_swiglu(gt, g, ut, u, rows, cols, x),
+                 f"gate_up_q8k {NAMES[gt]}/{NAMES[ut]}")
