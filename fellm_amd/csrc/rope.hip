@@ -201,10 +201,13 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
     const typename A::T *x2, typename A::T *out2, uint32_t nh2,
     const typename A::T *__restrict__ x3, uint32_t rows, uint32_t head_dim, uint32_t rope_dim, uint32_t pairing,
     const float *__restrict__ inv_freqs, const uint32_t *__restrict__ rope_pos, uint32_t pos0,
-    const uint32_t *__restrict__ kv_pos, KvDev kv, uint32_t *__restrict__ err) {
+    const uint32_t *__restrict__ kv_pos, KvDev kv, uint32_t *__restrict__ err, uint32_t hsplit) {
     __shared__ float2 cs_all[R][kMaxHalf / R];
     __shared__ uint64_t kbase_all[R];
-    const uint32_t row0 = blockIdx.x * R;
+    // hsplit workgroups share a row group, each taking a contiguous range of
+    // its (q, k, v) heads.
+    const uint32_t part = blockIdx.x % hsplit;
+    const uint32_t row0 = blockIdx.x / hsplit * R;
     const uint32_t half = rope_dim / 2;
     for (uint32_t t = threadIdx.x; t < R * half; t += kRopeBlock) {
         const uint32_t rr = t / half, i = t % half;
@@ -243,7 +246,9 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
     const uint32_t items_head = head_dim / (2 * PV);  // all items of a head
     const uint32_t nh_x2 = x2 ? nh2 : 0;
     const uint32_t nh_v = (MODE == 1) ? nh2 : 0;
-    const uint32_t heads = nh1 + nh_x2 + nh_v;       // q heads, k heads, v heads
+    const uint32_t all_heads = nh1 + nh_x2 + nh_v;   // q heads, k heads, v heads
+    const uint32_t h0 = part * all_heads / hsplit;
+    const uint32_t heads = (part + 1) * all_heads / hsplit - h0;  // this workgroup's heads
     const size_t w1 = (size_t)nh1 * head_dim, w2 = (size_t)nh2 * head_dim;
     const uint64_t v_off = (uint64_t)kv.block_size * kv.stride * 2;
     const uint32_t nrows = rows - row0 < (uint32_t)R ? rows - row0 : (uint32_t)R;
@@ -268,8 +273,8 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
                 srr[uu] = rr;
                 shd[uu] = hd;
                 if (slot + uu * step < total_slots)
-                    rope_load<A, PV>(x1, x2, x3, nh1, nh_x2, w1, w2, row0 + rr, hd, it, head_dim, rope_dim, pairing, n_rot,
-                                     e[uu]);
+                    rope_load<A, PV>(x1, x2, x3, nh1, nh_x2, w1, w2, row0 + rr, h0 + hd, it, head_dim, rope_dim,
+                                     pairing, n_rot, e[uu]);
                 hd += step;
                 while (hd >= heads) {
                     hd -= heads;
@@ -279,7 +284,7 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
 #pragma unroll
             for (int uu = 0; uu < FELLM_ROPE_UNROLL; ++uu) {
                 if (slot + uu * step < total_slots)
-                    rope_finish<A, C, PV, MODE>(x1, out1, x2, out2, nh1, nh_x2, w1, w2, row0 + srr[uu], shd[uu], it,
+                    rope_finish<A, C, PV, MODE>(x1, out1, x2, out2, nh1, nh_x2, w1, w2, row0 + srr[uu], h0 + shd[uu], it,
                                                 head_dim, rope_dim, pairing, n_rot, cs_all[srr[uu]], e[uu],
                                                 kbase_all[srr[uu]], kv, v_off);
             }
@@ -287,7 +292,7 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
     } else {
         for (uint32_t t = threadIdx.x; t < total_slots * items_head; t += kRopeBlock) {
             const uint32_t it = t % items_head, slot = t / items_head;
-            const uint32_t rr = slot / heads, hd = slot % heads;
+            const uint32_t rr = slot / heads, hd = h0 + slot % heads;
             float e[2 * PV];
             rope_load<A, PV>(x1, x2, x3, nh1, nh_x2, w1, w2, row0 + rr, hd, it, head_dim, rope_dim, pairing, n_rot, e);
             rope_finish<A, C, PV, MODE>(x1, out1, x2, out2, nh1, nh_x2, w1, w2, row0 + rr, hd, it, head_dim, rope_dim,
@@ -307,6 +312,17 @@ inline int rope_rows_per_block(uint32_t rows, uint32_t rope_dim) {
     if (rows >= 16384 && half <= kMaxHalf / 4) return 4;
     if (rows >= 8192 && half <= kMaxHalf / 2) return 2;
     return 1;
+}
+
+// Workgroups per row group.  With few rows, one workgroup per row leaves most
+// CUs idle while each thread walks many (row, head) slots one memory latency
+// at a time; the row's heads are then split so that about 1024 workgroups
+// run, each keeping at least 8 heads.
+inline uint32_t rope_head_split(uint32_t row_groups, uint32_t heads) {
+    if (row_groups >= 1024) return 1;
+    const uint32_t want = (1024 + row_groups - 1) / row_groups;
+    const uint32_t cap = heads / 8 > 0 ? heads / 8 : 1;
+    return want < cap ? want : cap;
 }
 
 // Standalone KvWrite: one workgroup per batch row, items of VEC elements.
@@ -385,10 +401,12 @@ extern "C" int fellm_rocm_rope(const void *x1, void *out1, uint32_t n_heads1, co
         const bool vec = rope_vec_ok(head_dim, rope_dim, pairing, sizeof(T), {x1, out1, x2, out2});
         const int R = rope_rows_per_block(rows, rope_dim);
         auto go = [&]<int PV, int RR>() {
-            hipLaunchKernelGGL((rope_kernel<A, F16, PV, 0, RR>), dim3((rows + RR - 1) / RR), dim3(kRopeBlock), 0, s,
+            const uint32_t groups = (rows + RR - 1) / RR;
+            const uint32_t hs = rope_head_split(groups, n_heads1 + (x2 ? n_heads2 : 0));
+            hipLaunchKernelGGL((rope_kernel<A, F16, PV, 0, RR>), dim3(groups * hs), dim3(kRopeBlock), 0, s,
                                (const T *)x1, (T *)out1, n_heads1, (const T *)x2, (T *)out2, x2 ? n_heads2 : 0,
                                nullptr, rows, head_dim, rope_dim, pairing, inv_freqs, positions, position0, nullptr,
-                               KvDev{}, nullptr);
+                               KvDev{}, nullptr, hs);
             return launch_status();
         };
         auto go_r = [&]<int PV>() {
@@ -475,10 +493,11 @@ extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q
             const bool vec = rope_vec_ok(head_dim, rope_dim, pairing, sizeof(T), {q, q_out, k, k_out, v}) &&
                              aligned_to(kvp->arena, 16) && kv.block_bytes % 16 == 0;
             auto go = [&]<int PV>() {
-                hipLaunchKernelGGL((rope_kernel<A, C, PV, 1, 1>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)q,
-                                   (T *)q_out, n_q_heads, (const T *)k, (T *)k_out, n_kv_heads, (const T *)v, batch,
-                                   head_dim, rope_dim, pairing, inv_freqs, rope_positions, 0u, kv_positions, kv,
-                                   err_flag);
+                const uint32_t hs = rope_head_split(batch, n_q_heads + 2 * n_kv_heads);
+                hipLaunchKernelGGL((rope_kernel<A, C, PV, 1, 1>), dim3(batch * hs), dim3(kRopeBlock), 0, s,
+                                   (const T *)q, (T *)q_out, n_q_heads, (const T *)k, (T *)k_out, n_kv_heads,
+                                   (const T *)v, batch, head_dim, rope_dim, pairing, inv_freqs, rope_positions, 0u,
+                                   kv_positions, kv, err_flag, hs);
                 return launch_status();
             };
             return vec ? go.template operator()<4>() : go.template operator()<1>();
