@@ -145,6 +145,12 @@ __global__ __launch_bounds__(kRouterBlock) void router_topk_grouped(
         const uint32_t e = e0 + j;
         key[j] = (active && e < n_exp) ? ((uint64_t)total_order_key(s[j]) << 32) | (uint64_t)(0xffffffffu - e) : 0ull;
     }
+    // Rank r's expert and raw score stay in registers of lane r % G (ranks
+    // past kHeld * G go to memory and are rescaled from there), so the final
+    // rescale needs no read-back of what was just written.
+    constexpr uint32_t kHeld = 4;
+    uint32_t held_e[kHeld];
+    float held_w[kHeld];
     float sum = 0.0f;
     for (uint32_t r = 0; r < k; ++r) {
         uint64_t best = key[0];
@@ -167,15 +173,35 @@ __global__ __launch_bounds__(kRouterBlock) void router_topk_grouped(
         }
         const float raw = total_order_inv((uint32_t)(best >> 32));
         sum += raw;  // rank order, as finish_selected sums
-        if (active && sub == 0) {
+        if (r < kHeld * G) {
+#pragma unroll
+            for (uint32_t i = 0; i < kHeld; ++i)
+                if (r == i * G + sub) {
+                    held_e[i] = e;
+                    held_w[i] = raw;
+                }
+        } else if (active && sub == 0) {
             ids[(size_t)token * k + r] = e;
             weights[(size_t)token * k + r] = raw;
         }
     }
-    // The lane that wrote the raw scores rescales them (same thread, program order).
     const float scale = rsf == 0.0f ? 1.0f : rsf;
+    if (active) {
+#pragma unroll
+        for (uint32_t i = 0; i < kHeld; ++i) {
+            const uint32_t r = i * G + sub;
+            if (r < k) {
+                float v = held_w[i];
+                if (norm && sum > 0.0f) v = v / sum;
+                ids[(size_t)token * k + r] = held_e[i];
+                weights[(size_t)token * k + r] = v * scale;
+            }
+        }
+    }
+    // Ranks beyond the held ones: the lane that wrote them rescales them
+    // (same thread, program order).
     if (active && sub == 0) {
-        for (uint32_t r = 0; r < k; ++r) {
+        for (uint32_t r = kHeld * G; r < k; ++r) {
             float v = weights[(size_t)token * k + r];
             if (norm && sum > 0.0f) v = v / sum;
             weights[(size_t)token * k + r] = v * scale;
