@@ -62,6 +62,7 @@ _SIGNATURES = {
     "fellm_rocm_paged_attention_workspace": (U64, [U32, U32, U32, U32, U32]),
     "fellm_rocm_paged_attention": (I32, [P, U32, P, U32, U32, U32, U32, U32, P, U32, F32, U32, U32,
                                          C.POINTER(FellmRocmPagedKv), P, U64, P]),
+    "fellm_rocm_cast": (I32, [P, U32, P, U32, U64, P]),
     "fellm_rocm_q8k_bytes": (U64, [U32]),
     "fellm_rocm_quantize_q8k": (I32, [P, U32, P, P]),
     "fellm_rocm_gate_up_swiglu_q8k": (I32, [P, U32, P, U32, U32, U32, P, P, P]),

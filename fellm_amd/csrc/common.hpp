@@ -52,6 +52,15 @@ struct BF16 {
     }
 };
 
+// bf16 by truncation: the CPU backend's Cast f32 -> bf16 keeps the top 16
+// bits (backend.rs:1648-1656).  Store-only policy.
+struct BF16Trunc {
+    using T = uint16_t;
+    static constexpr uint32_t code = FELLM_DTYPE_BF16;
+    __device__ __forceinline__ static float load(T v) { return __uint_as_float((uint32_t)v << 16); }
+    __device__ __forceinline__ static T store(float v) { return (T)(__float_as_uint(v) >> 16); }
+};
+
 // Host-side dispatch helper: call f.template operator()<Type>() for a dtype code.
 template <typename Fn>
 inline int dispatch_act(uint32_t dtype, Fn &&f) {

@@ -157,7 +157,7 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
     uint32_t *__restrict__ err) {
     __shared__ float red[kEmbBlock / kWave];
     const uint32_t row = blockIdx.x;
-    const uint32_t id = ids[row];
+    const uint32_t id = ids ? ids[row] : row;  // no ids: row r of the table (Cast's dequantization)
     const bool bad = id >= vocab;
     if (bad && threadIdx.x == 0 && err) atomicOr(err, 1u);
     const uint64_t rb = D::row_bytes(dim);
@@ -308,4 +308,69 @@ extern "C" int fellm_rocm_embedding_rmsnorm(const void *table, uint32_t table_dt
     if (!norm_weight || !y) return FELLM_ERR_ARITY;
     return fellm::embedding_common(table, table_dtype, vocab, dim, ids, n_ids, h_out, y, out_dtype,
                                    norm_weight, eps, err_flag, stream);
+}
+
+namespace fellm {
+namespace {
+
+// Rows of `dim` elements covering n: the widest of 4096 .. `unit` that divides n.
+uint32_t cast_dim(uint64_t n, uint32_t unit) {
+    for (uint32_t d = 4096; d >= unit; d /= 2)
+        if (n % d == 0 && n / d <= 0x7fffffffull) return d;
+    return 0;
+}
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" int fellm_rocm_cast(const void *src, uint32_t src_dtype, void *dst, uint32_t dst_dtype, uint64_t n_elems,
+                               void *stream) {
+    using namespace fellm;
+    if (n_elems == 0) return FELLM_OK;
+    if (!src || !dst) return FELLM_ERR_ARITY;
+    hipStream_t s = as_stream(stream);
+    const bool out_vec = aligned_to(dst, 16);
+    // Dense pairs of the CPU backend's Cast (backend.rs:1616-1656): f32 copy,
+    // f16 / bf16 widening, f32 -> f16 round-to-nearest-even, f32 -> bf16 truncation.
+    auto dense = [&]<typename A, typename O>() -> int {
+        constexpr int VEC = 8;
+        const bool vec = out_vec && n_elems % VEC == 0 && aligned_to(src, sizeof(typename A::T) * VEC);
+        const uint32_t dim = cast_dim(n_elems, vec ? VEC : 1);
+        if (!dim) return FELLM_ERR_SHAPE;
+        const uint64_t rows = n_elems / dim;
+        if (vec)
+            return launch_emb<DenseDec<A, VEC>, O>(src, rows, dim, nullptr, (uint32_t)rows, dst, nullptr, nullptr,
+                                                   0.0f, nullptr, s);
+        return launch_emb<DenseDec<A, 1>, O>(src, rows, dim, nullptr, (uint32_t)rows, dst, nullptr, nullptr, 0.0f,
+                                             nullptr, s);
+    };
+    if (dst_dtype == FELLM_DTYPE_F32) {
+        switch (src_dtype) {
+            case FELLM_DTYPE_F32: return dense.template operator()<F32, F32>();
+            case FELLM_DTYPE_F16: return dense.template operator()<F16, F32>();
+            case FELLM_DTYPE_BF16: return dense.template operator()<BF16, F32>();
+            case FELLM_DTYPE_Q4K:
+            case FELLM_DTYPE_Q6K: {
+                // Quantized -> f32 via the row dequantization (backend.rs:1657-1661,
+                // dequant.rs:19-55): the block stream as rows of `dim` elements.
+                if (n_elems % 256 || !out_vec) return FELLM_ERR_SHAPE;
+                const uint32_t dim = cast_dim(n_elems, 256);
+                if (!dim) return FELLM_ERR_SHAPE;
+                const uint64_t rows = n_elems / dim;
+                if (src_dtype == FELLM_DTYPE_Q4K) {
+                    if (!aligned_to(src, 16)) return FELLM_ERR_SHAPE;
+                    return launch_emb<Q4KDec, F32>(src, rows, dim, nullptr, (uint32_t)rows, dst, nullptr, nullptr, 0.0f,
+                                                   nullptr, s);
+                }
+                if (!aligned_to(src, 2)) return FELLM_ERR_SHAPE;
+                return launch_emb<Q6KDec, F32>(src, rows, dim, nullptr, (uint32_t)rows, dst, nullptr, nullptr, 0.0f,
+                                               nullptr, s);
+            }
+            default: return FELLM_ERR_DTYPE;
+        }
+    }
+    if (src_dtype == FELLM_DTYPE_F32 && dst_dtype == FELLM_DTYPE_F16) return dense.template operator()<F32, F16>();
+    if (src_dtype == FELLM_DTYPE_F32 && dst_dtype == FELLM_DTYPE_BF16)
+        return dense.template operator()<F32, BF16Trunc>();
+    return FELLM_ERR_DTYPE;
 }

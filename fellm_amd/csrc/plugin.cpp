@@ -817,6 +817,25 @@ int launch_gate_up_swiglu(const FellmOpAttrs *attrs, const FellmTensorRef *in, u
     });
 }
 
+// Cast [x] -> y of another dtype, on the device: the CPU backend's
+// conversions (backend.rs:1603-1667, fellm_rocm_cast).  y stays device-valid
+// like every other output (materialise it with a same-dtype Cast).
+int launch_cast_convert(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
+                        uint32_t n_out, FellmStreamHandle) {
+    return guarded(attrs, in, n_in, out, n_out, 1, 1, false, [&](State &st) {
+        const uint32_t sdt = in[0].dtype, ddt = out[0].dtype;
+        const size_t n = elems(out[0], ddt);
+        const bool quant = sdt == FELLM_DTYPE_Q4K || sdt == FELLM_DTYPE_Q6K;
+        const size_t need = quant ? (n % 256 ? 0 : n / 256 * (sdt == FELLM_DTYPE_Q4K ? 144 : 210))
+                                  : n * dtype_size(sdt);
+        if (!need || in[0].byte_len < need) fail(FELLM_ERR_SHAPE);
+        void *src = ensure_input(st, in[0]);
+        void *dst = ensure_output(st, out[0]);
+        check(fellm_rocm_cast(src, sdt, dst, ddt, n, stream_ptr(st)));
+        finish_outputs(st, out, 1);
+    });
+}
+
 // Cast [x] -> host x of the same dtype: materialise a device-valid mirror into
 // host storage (launchers.rs:140-170).
 int launch_materialize(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
@@ -888,6 +907,12 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
             {FELLM_OP_CAST, {F16}, F16, launch_materialize},
             {FELLM_OP_CAST, {BF16}, BF16, launch_materialize},
             {FELLM_OP_CAST, {U32}, U32, launch_materialize},
+            {FELLM_OP_CAST, {F16}, F32, launch_cast_convert},
+            {FELLM_OP_CAST, {BF16}, F32, launch_cast_convert},
+            {FELLM_OP_CAST, {F32}, F16, launch_cast_convert},
+            {FELLM_OP_CAST, {F32}, BF16, launch_cast_convert},
+            {FELLM_OP_CAST, {Q4K}, F32, launch_cast_convert},
+            {FELLM_OP_CAST, {Q6K}, F32, launch_cast_convert},
             {FELLM_OP_RMSNORM, {F32, F32}, F32, launch_rmsnorm},
             {FELLM_OP_SILU_GATE, {F32, F32}, F32, launch_silu_gate},
             {FELLM_OP_ROPE, {F32, F32}, F32, launch_rope},

@@ -213,6 +213,17 @@ int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void *out, uint3
                                void *stream);
 
 /*
+ * Cast: dst = src converted elementwise, n_elems elements.
+ *   replaces: launch_cast (crates/backend-cpu/src/backend.rs:1603-1667).
+ * Pairs (as the CPU backend): F32->F32, F16->F32, BF16->F32 (exact widening),
+ * F32->F16 (round to nearest even), F32->BF16 (truncation: the top 16 bits),
+ * Q4K->F32 and Q6K->F32 (dequantization of the block stream, n_elems % 256 == 0,
+ * dst 16-byte aligned).  Other pairs return FELLM_ERR_DTYPE.
+ */
+int fellm_rocm_cast(const void *src, uint32_t src_dtype, void *dst, uint32_t dst_dtype, uint64_t n_elems,
+                    void *stream);
+
+/*
  * x quantized once to Q8_K for any number of K-quant GEMVs over it, as the
  * CPU backend does per matmul (matmul.rs:213-270 quantize_row_q8_k_avx2; the
  * CUDA plugin's quantize_q8_32 plays the same role for its own format).

@@ -371,3 +371,59 @@ def test_rope_many_rows(ops, dev, rows):
                       position0=3, x2=torch.from_numpy(k).to(dev))
     assert_rope_close(from_dev(qo), qr, pair_magnitude(q, nq, hd, hd, 1), "f32", "q")
     assert_rope_close(from_dev(ko), kr, pair_magnitude(k, nk, hd, hd, 1), "f32", "k")
+
+
+# ---- Cast (backend.rs:1603-1667) ---------------------------------------------------
+def _cast(ops, src, sdt, ddt, n, out_np_dtype, dev):
+    from fellm_amd import _lib
+
+    s = torch.from_numpy(np.ascontiguousarray(src)).to(dev)
+    out = torch.empty(n * np.dtype(out_np_dtype).itemsize, dtype=torch.uint8, device=dev)
+    _lib.call("fellm_rocm_cast", s.data_ptr(), int(sdt), out.data_ptr(), int(ddt), n,
+              torch.cuda.current_stream().cuda_stream)
+    return out.cpu().numpy().view(out_np_dtype)
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 3 * 4096 + 8, 1 << 20])
+def test_cast_dense_pairs(ops, dev, n):
+    """f16/bf16 -> f32 widen exactly, f32 -> f16 rounds to nearest even,
+    f32 -> bf16 truncates (the CPU backend's Cast, unlike the RNE used for
+    kernel outputs); includes ties, subnormals, infinities and NaN."""
+    from fellm_amd.abi import DType
+
+    rng = np.random.default_rng(n)
+    x = (rng.normal(size=n) * np.exp(rng.uniform(-30, 30, size=n))).astype(np.float32)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, 65520.0, 1e-8,
+                         1.0 + 2.0 ** -8, 3.0e38], np.float32)
+    x[: min(n, specials.size)] = specials[: min(n, specials.size)]
+    h = oracle.f32_to_f16_bits(x)
+    b = oracle.f32_to_bf16_bits(x)
+    assert np.array_equal(_cast(ops, x, DType.F32, DType.F32, n, np.uint32, dev), x.view(np.uint32))
+    assert np.array_equal(_cast(ops, x, DType.F32, DType.F16, n, np.uint16, dev), h)
+    assert np.array_equal(_cast(ops, x, DType.F32, DType.BF16, n, np.uint16, dev),
+                          oracle.f32_to_bf16_bits(x, truncate=True))
+    assert np.array_equal(_cast(ops, h, DType.F16, DType.F32, n, np.uint32, dev),
+                          oracle.widen(h, "f16").view(np.uint32))
+    assert np.array_equal(_cast(ops, b, DType.BF16, DType.F32, n, np.uint32, dev),
+                          oracle.widen(b, "bf16").view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype,blocks", [(12, 1), (12, 37), (14, 16), (14, 129)])
+def test_cast_kquant_to_f32(ops, dev, dtype, blocks):
+    from fellm_amd import synth
+
+    rng = np.random.default_rng(dtype * blocks)
+    w = synth.KQUANT_TABLES[dtype](rng, blocks, 256).ravel()
+    got = _cast(ops, w, dtype, 0, blocks * 256, np.float32, dev)  # 0 = F32
+    assert np.array_equal(got.view(np.uint32), oracle.dequantize_row(dtype, w, blocks * 256).view(np.uint32))
+
+
+def test_cast_rejects_other_pairs(ops, dev):
+    from fellm_amd import _lib
+    from fellm_amd.abi import DType
+
+    a = torch.zeros(64, dtype=torch.float16, device=dev)
+    b = torch.zeros(64, dtype=torch.bfloat16, device=dev)
+    rc = _lib.lib().fellm_rocm_cast(a.data_ptr(), int(DType.F16), b.data_ptr(), int(DType.BF16), 64,
+                                    torch.cuda.current_stream().cuda_stream)
+    assert rc == -10

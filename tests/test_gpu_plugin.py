@@ -358,3 +358,19 @@ def test_attention_paged_batch(host):
     for r in range(len(lengths)):
         tol = 2e-5 * np.abs(v16[r]).max() + np.abs(ref[r]) * 2.0 ** -23
         assert np.all(np.abs(got[r] - ref[r]) <= tol), (r, np.abs(got[r] - ref[r]).max())
+
+
+def test_cast_converts_on_device(host):
+    """Cast F32 -> BF16 (truncation) and Q4_K -> F32 (dequantization) through
+    the plugin; the converted outputs are materialised with a same-dtype Cast."""
+    rng = np.random.default_rng(77)
+    x = rng.normal(size=1000).astype(np.float32) * np.float32(3.7)
+    y = np.zeros(1000, np.uint16)
+    run(host, abi.OpKind.CAST, [D.F32], D.BF16, abi.OpAttrs(cast_to=int(D.BF16)), [tref(x, D.F32)],
+        [tmut(y, D.BF16)])
+    assert_exact(materialize(host, y, D.BF16), oracle.f32_to_bf16_bits(x, truncate=True), "f32 -> bf16")
+    w = synth.KQUANT_TABLES[12](rng, 3, 512).ravel()
+    z = np.zeros(3 * 512, np.float32)
+    run(host, abi.OpKind.CAST, [D.Q4K], D.F32, abi.OpAttrs(cast_to=int(D.F32)), [tref(w, D.Q4K)],
+        [tmut(z, D.F32)])
+    assert_exact(materialize(host, z, D.F32), oracle.dequantize_row(12, w, 3 * 512), "q4k -> f32")
