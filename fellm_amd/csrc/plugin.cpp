@@ -89,7 +89,6 @@ struct State {
     void *pinned = nullptr;                                      // host staging for `scratch`
     size_t pinned_bytes = 0;
     bool host_reads_pending = false;  // an H2D copy may still read caller memory
-    Mirror err_flag;                                             // u32 error word
     int sync_outputs = -1;
 };
 
@@ -242,25 +241,6 @@ void *stage_small(State &st, const std::vector<const void *> &srcs, const std::v
     }
     hip_check(hipMemcpyAsync(st.scratch.dev, st.pinned, total, hipMemcpyHostToDevice, stream_locked(st)));
     return st.scratch.dev;
-}
-
-// Error word for kernels that flag bad slots; none while capturing (the
-// check would need a host read).
-uint32_t *err_word(State &st) {
-    if (st.capturing) return nullptr;
-    if (!st.err_flag.dev) {
-        ensure_capacity(st.err_flag, 4);
-    }
-    hip_check(hipMemsetAsync(st.err_flag.dev, 0, 4, stream_locked(st)));
-    return static_cast<uint32_t *>(st.err_flag.dev);
-}
-
-int read_err(State &st) {
-    if (st.capturing) return FELLM_OK;
-    uint32_t v = 0;
-    hip_check(hipMemcpyAsync(&v, st.err_flag.dev, 4, hipMemcpyDeviceToHost, stream_locked(st)));
-    hip_check(hipStreamSynchronize(stream_locked(st)));
-    return v ? FELLM_ERR_PAGED_RANGE : FELLM_OK;
 }
 
 bool snapshot(State &st, FellmPagedKvSnapshot &out) {
@@ -519,6 +499,26 @@ FellmRocmPagedKv paged_geometry(State &st, const FellmPagedKvSnapshot &snap, uin
     return kv;
 }
 
+// Host-side check of every batch row's K/V slot against the snapshot, as the
+// CUDA plugin does before launching (launchers.rs:3913-3945): the table must
+// hold the layer, the logical block must exist, and the slot's block must lie
+// inside the device arena.  The kernels then run without an error word, so
+// no launch waits for a device-to-host read.
+void check_slots(const FellmPagedKvSnapshot &snap, uint32_t layer, const uint32_t *positions, size_t batch) {
+    const size_t n_logical = snap.n_logical_blocks;
+    if (!n_logical || !snap.block_bytes || !snap.block_size || layer >= snap.n_layers) fail(FELLM_ERR_PAGED_RANGE);
+    const uint64_t row_bytes = (uint64_t)snap.tokens_stride * 2;
+    for (size_t b = 0; b < batch; ++b) {
+        const uint64_t pos = positions[b];
+        const uint64_t logical = pos / snap.block_size, slot = pos % snap.block_size;
+        if (logical >= n_logical) fail(FELLM_ERR_PAGED_RANGE);
+        const uint64_t idx = ((uint64_t)b * snap.n_layers + layer) * n_logical + logical;
+        if (idx >= snap.n_block_table) fail(FELLM_ERR_PAGED_RANGE);
+        const uint64_t base = (uint64_t)snap.block_table[idx] * snap.block_bytes + slot * row_bytes;
+        if (base + (uint64_t)snap.block_size * row_bytes + row_bytes > snap.device_arena_len) fail(FELLM_ERR_PAGED_RANGE);
+    }
+}
+
 // KvWrite [row(s), (cache)] -> cache (backend.rs:1734-1793, launchers.rs:3770-3900).
 int launch_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
                     uint32_t n_out, FellmStreamHandle) {
@@ -540,10 +540,12 @@ int launch_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_
             const uint32_t *pos = nullptr;
             FellmRocmPagedKv kv = paged_geometry(st, snap, a.layer_ord, FELLM_DTYPE_F16,
                                                  controlled ? nullptr : snap.row_positions, &pos);
-            if (controlled) pos = step_kv_position(st, kv.block_size);
-            uint32_t *err = err_word(st);
-            check(fellm_rocm_kv_write(rows, dt, (uint32_t)batch, pos, &kv, a.kv_slot != 0, err, stream_ptr(st)));
-            check(read_err(st));
+            if (controlled)
+                pos = step_kv_position(st, kv.block_size);  // device-side slot: out-of-range rows are skipped
+            else
+                check_slots(snap, a.layer_ord, snap.row_positions, batch);
+            check(fellm_rocm_kv_write(rows, dt, (uint32_t)batch, pos, &kv, a.kv_slot != 0, nullptr, stream_ptr(st)));
+            finish_outputs(st, out, 0);
             return;
         }
         // Contiguous layout (also when block_size > 0 but no paged context is
@@ -606,12 +608,11 @@ int launch_rope_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, ui
             kv = paged_geometry(st, snap, a.layer_ord, kv_dt, snap.row_positions, &kv_pos, snap.row_rope_positions,
                                 &rope_pos);
         }
-        uint32_t *err = err_word(st);
+        if (!controlled) check_slots(snap, a.layer_ord, snap.row_positions, batch);
         check(fellm_rocm_rope_kv_write(q, qo, (uint32_t)nq, k, ko, v, (uint32_t)nkv, dt, (uint32_t)batch, (uint32_t)hd,
-                                       a.rope_dim, a.rope_pairing, (const float *)f, rope_pos, kv_pos, &kv, err,
+                                       a.rope_dim, a.rope_pairing, (const float *)f, rope_pos, kv_pos, &kv, nullptr,
                                        stream_ptr(st)));
         finish_outputs(st, out, has_kout ? 2 : 1);
-        check(read_err(st));
     });
 }
 

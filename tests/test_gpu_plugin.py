@@ -206,6 +206,32 @@ def test_kv_write_paged(host):
         host.set_paged_context(None)
 
 
+def test_kv_write_paged_rejects_out_of_range_slot(host):
+    """A row whose position lies past the sequence's logical blocks is refused
+    before anything is enqueued (launchers.rs:3913-3945): the launch fails
+    with the paged-range code and the arena is untouched."""
+    from fellm_amd.plugin_host import PluginError
+    rng = np.random.default_rng(5)
+    batch, nkv, hd, bs, n_blocks = 4, 2, 64, 16, 16
+    ctx, arena, kv_pos, *_ = _paged(rng, batch, nkv, hd, n_blocks, bs, 200, "f16")
+    n_logical = ctx.n_logical_blocks
+    bad = kv_pos.copy()
+    bad[2] = n_logical * bs  # first position past the last logical block
+    ctx.row_positions = bad
+    host.set_paged_context(ctx)
+    try:
+        rows = rng.normal(size=(batch, nkv * hd)).astype(np.float32)
+        with pytest.raises(PluginError) as e:
+            run(host, abi.OpKind.KV_WRITE, [D.F32, D.F32], D.F32,
+                abi.OpAttrs(block_size=bs, kv_slot=0, layer_ord=0), [tref(rows, D.F32)],
+                [tmut(np.zeros(4, np.float32), D.F32)])
+        assert e.value.code == abi.ERR_PAGED_RANGE
+        torch.cuda.synchronize()
+        assert not arena.cpu().numpy().any()
+    finally:
+        host.set_paged_context(None)
+
+
 def test_kv_write_contiguous(host):
     row = np.arange(32, dtype=np.float32)
     cache = np.full((8, 32), -1.0, np.float32)
