@@ -26,6 +26,10 @@
 #ifndef FELLM_ROPE_DOUBLE_TRIG
 #define FELLM_ROPE_DOUBLE_TRIG 1
 #endif
+// Build knob: non-temporal activation loads (bit 0) and stores (bit 1).
+#ifndef FELLM_ROPE_NT
+#define FELLM_ROPE_NT 2
+#endif
 // Build knob: (row, head) slots each thread loads before rotating/storing.
 #ifndef FELLM_ROPE_UNROLL
 #define FELLM_ROPE_UNROLL 1
@@ -68,6 +72,16 @@ __device__ __forceinline__ void store_cache(uint8_t *arena, uint64_t byte_off, u
     store_f32<C, N>(reinterpret_cast<typename C::T *>(arena + byte_off) + elem, v);
 }
 
+template <typename A, int N>
+__device__ __forceinline__ void act_load(const typename A::T *p, float (&v)[N]) {
+    if constexpr (FELLM_ROPE_NT & 1) load_f32_nt<A, N>(p, v); else load_f32<A, N>(p, v);
+}
+
+template <typename A, int N>
+__device__ __forceinline__ void act_store(typename A::T *p, const float (&v)[N]) {
+    if constexpr (FELLM_ROPE_NT & 2) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
+}
+
 // Element offset, within its head, of item `it`'s first run and of its
 // second run (PV elements each).  Items [0, n_rot) are rotated; the rest are
 // the pass-through span.  Adjacent pairings keep both runs contiguous.
@@ -101,17 +115,17 @@ __device__ __forceinline__ void rope_load(const typename A::T *x1, const typenam
         src = x2;
         base = (size_t)row * w2 + (size_t)(hd - nh1) * head_dim;
     } else {  // V head: plain 2*PV-element run
-        load_f32<A, 2 * PV>(x3 + (size_t)row * w2 + (size_t)(hd - nh1 - nh2) * head_dim + it * 2 * PV, e);
+        act_load<A, 2 * PV>(x3 + (size_t)row * w2 + (size_t)(hd - nh1 - nh2) * head_dim + it * 2 * PV, e);
         return;
     }
     uint32_t lo, hi;
     item_offsets(it, n_rot, head_dim, rope_dim, pairing, PV, lo, hi);
     if (hi == lo + PV) {
-        load_f32<A, 2 * PV>(src + base + lo, e);
+        act_load<A, 2 * PV>(src + base + lo, e);
     } else {
         float a[PV], b[PV];
-        load_f32<A, PV>(src + base + lo, a);
-        load_f32<A, PV>(src + base + hi, b);
+        act_load<A, PV>(src + base + lo, a);
+        act_load<A, PV>(src + base + hi, b);
 #pragma unroll
         for (int k = 0; k < PV; ++k) {
             e[k] = a[k];
@@ -165,7 +179,7 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
     const bool write = dst && (dst != src || it < n_rot);
     const bool cache = MODE == 1 && second && kbase != ~0ull;
     if (hi == lo + PV) {
-        if (write) store_f32<A, 2 * PV>(dst + base + lo, e);
+        if (write) act_store<A, 2 * PV>(dst + base + lo, e);
         if constexpr (MODE == 1)
             if (cache) store_cache<C, 2 * PV>(kv.arena, kbase, h * head_dim + lo, e);
     } else {
@@ -176,8 +190,8 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
             b[k] = e[PV + k];
         }
         if (write) {
-            store_f32<A, PV>(dst + base + lo, a);
-            store_f32<A, PV>(dst + base + hi, b);
+            act_store<A, PV>(dst + base + lo, a);
+            act_store<A, PV>(dst + base + hi, b);
         }
         if constexpr (MODE == 1) {
             if (cache) {
