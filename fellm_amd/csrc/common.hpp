@@ -9,6 +9,11 @@
 #include "fellm_abi.h"
 #include "fellm_rocm.h"
 
+// Bit distance bound of silu_fast; kept equal to the measured maximum.
+#ifndef FELLM_SILU_FAST_DIST
+#define FELLM_SILU_FAST_DIST 5
+#endif
+
 namespace fellm {
 
 constexpr int kWave = 64;
@@ -311,6 +316,49 @@ __device__ __forceinline__ float silu_div(float g, float d) {
 
 __device__ __forceinline__ float silu(float g, const uint64_t *tab) {
     return silu_div(g, 1.0f + expf_glibc(-g, tab));
+}
+
+// Fast silu for outputs rounded to 16 bits.  exp(-g) comes from the hardware
+// exp2 after a two-constant reduction by ln 2 (ln 2 = kLn2Hi + kLn2Lo), and
+// the division is one hardware reciprocal and a multiply.  On the fast domain
+// 2^-100 <= |g| < 64 its bit distance to silu() (same sign, normal results)
+// is at most kSiluFastDist; fellm_rocm_silu_fast_bound measures the largest
+// distance over every f32 g in the domain.
+constexpr uint32_t kSiluFastDist = FELLM_SILU_FAST_DIST;
+
+__device__ __forceinline__ bool silu_fast_domain(float g) {
+    const float ag = __builtin_fabsf(g);
+    return ag >= 0x1p-100f && ag < 64.0f;
+}
+
+__device__ __forceinline__ float silu_fast(float g) {
+    constexpr float kLog2e = 0x1.715476p+0f;
+    constexpr float kLn2Hi = 0x1.62e430p-1f;   // ln 2 rounded up to 24 bits
+    constexpr float kLn2Lo = -0x1.05c610p-29f;  // ln 2 - kLn2Hi
+    const float t = -g;
+    const float n = __builtin_rintf(t * kLog2e);
+    float r = __builtin_fmaf(n, -kLn2Hi, t);
+    r = __builtin_fmaf(n, -kLn2Lo, r);
+    const float e = __builtin_ldexpf(__builtin_amdgcn_exp2f(r * kLog2e), (int)n);
+    return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// out = O::store(RN(silu(g) * u)) without evaluating the exact silu when the
+// answer is already fixed: the exact f32 silu s lies within kSiluFastDist
+// steps of the fast value in bit order, hence in [sa, sb]; RN(s * u) then lies
+// between RN(sa * u) and RN(sb * u) (rounding and multiplication by u are
+// monotone), and so does its 16-bit rounding, which therefore equals O::store
+// of either end when those agree.  Returns false (out unset) otherwise, and
+// outside the fast domain.
+template <typename O>
+__device__ __forceinline__ bool silu_mul_fast(float g, float u, typename O::T &out) {
+    static_assert(sizeof(typename O::T) == 2, "the interval test needs a 16-bit output");
+    if (!silu_fast_domain(g)) return false;
+    const uint32_t b = __float_as_uint(silu_fast(g));
+    const typename O::T lo = O::store(__uint_as_float(b - kSiluFastDist) * u);
+    const typename O::T hi = O::store(__uint_as_float(b + kSiluFastDist) * u);
+    out = lo;
+    return __builtin_bit_cast(uint16_t, lo) == __builtin_bit_cast(uint16_t, hi);
 }
 
 // Copies the 32-entry table into LDS once per block; returns the LDS pointer.

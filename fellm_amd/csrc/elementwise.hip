@@ -19,6 +19,26 @@ namespace {
 
 constexpr int kEwBlock = 256;
 
+// Build knob: 16-bit outputs take the interval fast path of silu_mul_fast (1).
+#ifndef FELLM_SWIGLU_FAST
+#define FELLM_SWIGLU_FAST 1
+#endif
+
+// Non-temporal store of VEC already-rounded output elements.
+template <typename O, int VEC>
+__device__ __forceinline__ void store_raw_nt(typename O::T *p, const typename O::T (&v)[VEC]) {
+    using P = Pack<typename O::T, VEC>;
+    constexpr int W = sizeof(P) / 4;
+    P pk;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) pk.v[i] = v[i];
+    uint32_t w[W];
+    memcpy(w, &pk, sizeof(P));
+    uint32_t *dst = reinterpret_cast<uint32_t *>(p);
+#pragma unroll
+    for (int i = 0; i < W; ++i) __builtin_nontemporal_store(w[i], dst + i);
+}
+
 inline uint32_t ew_grid(uint64_t units) {
     uint64_t g = (units + kEwBlock - 1) / kEwBlock;
     const uint64_t cap = 256ull * 32;  // 256 CUs x 32 blocks: enough to saturate HBM
@@ -49,10 +69,21 @@ __global__ __launch_bounds__(kEwBlock) void silu_gate_kernel(const typename I::T
         for (int j = 0; j < UNROLL; ++j) {
             const uint64_t i = base + (uint64_t)j * kEwBlock;
             if (i < nvec) {
-                float o[VEC];
+                if constexpr (FELLM_SWIGLU_FAST && sizeof(typename O::T) == 2 && VEC % 2 == 0) {
+                    // The exact silu runs only for the elements (and only in
+                    // the wavefronts) whose rounding the interval leaves open.
+                    typename O::T o[VEC];
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) o[k] = silu(gv[j][k], tab) * uv[j][k];
-                store_f32_nt<O, VEC>(out + i * VEC, o);
+                    for (int k = 0; k < VEC; ++k)
+                        if (__builtin_expect(!silu_mul_fast<O>(gv[j][k], uv[j][k], o[k]), 0))
+                            o[k] = O::store(silu(gv[j][k], tab) * uv[j][k]);
+                    store_raw_nt<O, VEC>(out + i * VEC, o);
+                } else {
+                    float o[VEC];
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) o[k] = silu(gv[j][k], tab) * uv[j][k];
+                    store_f32_nt<O, VEC>(out + i * VEC, o);
+                }
             }
         }
     }
@@ -90,6 +121,29 @@ __global__ __launch_bounds__(kEwBlock) void expf_kernel(const float *__restrict_
     const uint64_t stride = (uint64_t)gridDim.x * kEwBlock;
     for (uint64_t i = (uint64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += stride)
         out[i] = expf_glibc(in[i], tab);
+}
+
+// Largest bit distance between silu_fast and silu over every f32 g of the
+// fast domain, one grid-stride sweep of all 2^32 patterns.
+__global__ __launch_bounds__(kEwBlock) void silu_fast_bound_kernel(uint32_t *__restrict__ max_dist) {
+    __shared__ uint64_t tab_lds[32];
+    const uint64_t *tab = stage_expf_table(tab_lds);
+    uint32_t m = 0;
+    const uint64_t stride = (uint64_t)gridDim.x * kEwBlock;
+    for (uint64_t i = (uint64_t)blockIdx.x * kEwBlock + threadIdx.x; i < (1ull << 32); i += stride) {
+        const float g = __uint_as_float((uint32_t)i);
+        if (!silu_fast_domain(g)) continue;
+        const uint32_t a = __float_as_uint(silu_fast(g)), b = __float_as_uint(silu(g, tab));
+        // Opposite signs give a distance of at least 2^31, far above any bound.
+        const uint32_t d = a > b ? a - b : b - a;
+        m = d > m ? d : m;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const uint32_t o = __shfl_xor(m, off, kWave);
+        m = o > m ? o : m;
+    }
+    if (threadIdx.x % kWave == 0) atomicMax(max_dist, m);
 }
 
 // VEC = 8 elements: 16 B for 16-bit types, 32 B for f32.
@@ -166,3 +220,12 @@ extern "C" int fellm_rocm_expf(const float *in, float *out, uint64_t n, void *st
     hipLaunchKernelGGL(expf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), in, out, n);
     return launch_status();
 }
+
+extern "C" int fellm_rocm_silu_fast_bound(uint32_t *max_dist, void *stream) {
+    using namespace fellm;
+    if (!max_dist) return FELLM_ERR_ARITY;
+    hipLaunchKernelGGL(silu_fast_bound_kernel, dim3(256 * 16), dim3(kEwBlock), 0, as_stream(stream), max_dist);
+    return launch_status();
+}
+
+extern "C" uint32_t fellm_rocm_silu_fast_dist(void) { return fellm::kSiluFastDist; }

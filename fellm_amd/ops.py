@@ -427,6 +427,15 @@ def expf(x):
     return out
 
 
+def silu_fast_bound():
+    """(largest measured bit distance between the fast and the exact silu over
+    every f32 gate of the fast domain, the distance the SwiGLU 16-bit path
+    assumes).  The path is bit-exact iff the first does not exceed the second."""
+    m = torch.zeros(1, dtype=torch.int32, device="cuda")
+    _lib.call("fellm_rocm_silu_fast_bound", _p(m), _stream())
+    return int(m.cpu().item()) & 0xFFFFFFFF, int(_lib.lib().fellm_rocm_silu_fast_dist())
+
+
 def rope_inv_freqs(theta: float, rope_dim: int) -> torch.Tensor:
     """inv_freq[i] = theta ** (-(2i) / rope_dim) in f32 with libm powf
     (crates/fellm-model/src/rope.rs:13-40, no scaling), as a CPU tensor."""

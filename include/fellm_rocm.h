@@ -331,6 +331,19 @@ int fellm_rocm_stream_is_capturing(void *stream);
  */
 int fellm_rocm_expf(const float *in, float *out, uint64_t n, void *stream);
 
+/*
+ * Verification hook for fellm_rocm_silu_gate's 16-bit output path (no
+ * counterpart in the reference).  That path skips the exact silu when an
+ * interval of +-fellm_rocm_silu_fast_dist() steps around a fast f32 silu
+ * already fixes the rounded output.  fellm_rocm_silu_fast_bound atomically
+ * raises *max_dist (device u32, caller zeroes it) to the largest bit distance
+ * between the fast and the exact silu over every f32 gate value of the fast
+ * domain (2^-100 <= |g| < 64).  The path is bit-exact iff that maximum does
+ * not exceed fellm_rocm_silu_fast_dist().
+ */
+int fellm_rocm_silu_fast_bound(uint32_t *max_dist, void *stream);
+uint32_t fellm_rocm_silu_fast_dist(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,36 @@ def test_silu_gate(ops, dev, kind, n):
     assert_exact(got, ref, f"silu_gate {kind} n={n}")
 
 
+def test_silu_fast_bound_covers_every_gate(ops, dev):
+    """The 16-bit SwiGLU outputs skip the exact silu when an interval of
+    +-D bit steps around a fast f32 silu fixes the rounded result.  That is
+    bit-exact iff the exact silu lies within D steps of the fast one for every
+    gate of the fast domain: the device sweep over all 2^32 f32 patterns
+    measures the largest distance."""
+    measured, assumed = ops.silu_fast_bound()
+    assert 0 < measured <= assumed, (measured, assumed)
+
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+def test_silu_gate_rounding_boundaries(ops, dev, kind):
+    """Pairs whose f32 product lies within 64 f32 steps of a 16-bit rounding
+    midpoint, where the fast interval cannot decide and the exact silu runs,
+    mixed with random pairs decided by the interval alone."""
+    rng = np.random.default_rng(29)
+    n = 1 << 23
+    g = random_stored(rng, n, kind)
+    u = random_stored(rng, n, kind)
+    p = oracle.silu_gate(oracle.widen(g, kind), oracle.widen(u, kind))
+    low = 13 if kind == "f16" else 16
+    r = (p.view(np.uint32) & ((1 << low) - 1)).astype(np.int64)
+    near = np.abs(r - (1 << (low - 1))) <= 64
+    keep = near | (rng.random(n) < 0.01)
+    assert near.sum() > 1000
+    g, u, p = g[keep], u[keep], p[keep]
+    got = from_dev(ops.silu_gate(to_dev(g, kind, dev), to_dev(u, kind, dev)))
+    assert_exact(got, oracle.narrow(p, kind), f"silu_gate {kind} near rounding midpoints")
+
+
 def test_silu_gate_unaligned_and_extremes(ops, dev):
     g = np.array([0.0, -0.0, 100.0, -100.0, 20.0, -20.0, 88.0, -88.0, 1e-30, np.inf, -np.inf, 3.5], np.float32)
     u = np.full_like(g, 1.5)
