@@ -13,6 +13,10 @@
 // The sum of squares is one wavefront shuffle reduction plus one LDS exchange.
 #include "common.hpp"
 
+#ifndef FELLM_NORM_W_EARLY
+#define FELLM_NORM_W_EARLY 1
+#endif
+
 namespace fellm {
 
 // x and residual are read once with non-temporal loads, and h and y are
@@ -60,16 +64,26 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_kernel(
             for (int i = 0; i < VEC; ++i) ss += v[c][i] * v[c][i];
         }
     }
+    // The weights do not depend on the reduction: with FELLM_NORM_W_EARLY they
+    // are requested before the barrier, so their (cache) latency overlaps it.
+    float wv[NCHUNK][VEC];
+    if constexpr (FELLM_NORM_W_EARLY) {
+#pragma unroll
+        for (int c = 0; c < NCHUNK; ++c) {
+            const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
+            if (base < group) load_f32<F32, VEC>(w + base, wv[c]);
+        }
+    }
     ss = block_sum<BLOCK>(ss, red);
     const float scale = 1.0f / sqrtf(ss / (float)group + eps);
 #pragma unroll
     for (int c = 0; c < NCHUNK; ++c) {
         const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
         if (base < group) {
-            float wv[VEC], o[VEC];
-            load_f32<F32, VEC>(w + base, wv);
+            float o[VEC];
+            if constexpr (!FELLM_NORM_W_EARLY) load_f32<F32, VEC>(w + base, wv[c]);
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) o[i] = (v[c][i] * scale) * wv[i];
+            for (int i = 0; i < VEC; ++i) o[i] = (v[c][i] * scale) * wv[c][i];
             norm_store<O, VEC, true>(y + row * group + base, o);
         }
     }
