@@ -190,8 +190,8 @@ int launch_add(const void *a, const void *b, void *out, uint64_t n, hipStream_t 
 extern "C" int fellm_rocm_silu_gate(const void *gate, const void *up, uint32_t in_dtype, void *out,
                                     uint32_t out_dtype, uint64_t n_elems, void *stream) {
     using namespace fellm;
-    if (!gate || !up || !out) return FELLM_ERR_ARITY;
     if (n_elems == 0) return FELLM_OK;
+    if (!gate || !up || !out) return FELLM_ERR_ARITY;
     hipStream_t s = as_stream(stream);
     return dispatch_act(in_dtype, [&]<typename I>() -> int {
         if (out_dtype == in_dtype) return launch_silu<I, I>(gate, up, out, n_elems, s);
@@ -203,8 +203,8 @@ extern "C" int fellm_rocm_silu_gate(const void *gate, const void *up, uint32_t i
 extern "C" int fellm_rocm_add(const void *a, const void *b, uint32_t in_dtype, void *out,
                               uint32_t out_dtype, uint64_t n_elems, void *stream) {
     using namespace fellm;
-    if (!a || !b || !out) return FELLM_ERR_ARITY;
     if (n_elems == 0) return FELLM_OK;
+    if (!a || !b || !out) return FELLM_ERR_ARITY;
     hipStream_t s = as_stream(stream);
     return dispatch_act(in_dtype, [&]<typename I>() -> int {
         if (out_dtype == in_dtype) return launch_add<I, I>(a, b, out, n_elems, s);

@@ -292,9 +292,9 @@ int dispatch_table(const void *table, uint32_t table_dtype, uint64_t vocab, uint
 int embedding_common(const void *table, uint32_t table_dtype, uint64_t vocab, uint32_t dim,
                      const uint32_t *ids, uint32_t n_ids, void *h, void *y, uint32_t out_dtype,
                      const float *w, float eps, uint32_t *err, void *stream) {
-    if (!table || !ids) return FELLM_ERR_ARITY;
     if (dim == 0 || vocab == 0) return FELLM_ERR_SHAPE;
     if (n_ids == 0) return FELLM_OK;
+    if (!table || !ids) return FELLM_ERR_ARITY;
     // Output runs are up to 8 elements: 16-byte alignment covers every case.
     if ((h && !aligned_to(h, 16)) || (y && !aligned_to(y, 16))) return FELLM_ERR_SHAPE;
     hipStream_t s = as_stream(stream);
@@ -309,7 +309,7 @@ int embedding_common(const void *table, uint32_t table_dtype, uint64_t vocab, ui
 extern "C" int fellm_rocm_embedding(const void *table, uint32_t table_dtype, uint64_t vocab,
                                     uint32_t dim, const uint32_t *ids, uint32_t n_ids, void *out,
                                     uint32_t out_dtype, uint32_t *err_flag, void *stream) {
-    if (!out) return FELLM_ERR_ARITY;
+    if (!out && n_ids) return FELLM_ERR_ARITY;
     return fellm::embedding_common(table, table_dtype, vocab, dim, ids, n_ids, out, nullptr, out_dtype,
                                    nullptr, 0.0f, err_flag, stream);
 }
@@ -318,7 +318,7 @@ extern "C" int fellm_rocm_embedding_rmsnorm(const void *table, uint32_t table_dt
                                             uint32_t dim, const uint32_t *ids, uint32_t n_ids,
                                             const float *norm_weight, float eps, void *h_out, void *y,
                                             uint32_t out_dtype, uint32_t *err_flag, void *stream) {
-    if (!norm_weight || !y) return FELLM_ERR_ARITY;
+    if ((!norm_weight || !y) && n_ids) return FELLM_ERR_ARITY;
     return fellm::embedding_common(table, table_dtype, vocab, dim, ids, n_ids, h_out, y, out_dtype,
                                    norm_weight, eps, err_flag, stream);
 }

@@ -176,9 +176,10 @@ extern "C" int fellm_rocm_add_rmsnorm(const void *x, const void *residual, void 
                                       void *y, uint32_t y_dtype, uint64_t n_elems, float eps,
                                       void *stream) {
     using namespace fellm;
+    if (group == 0 || n_elems % group != 0) return FELLM_ERR_SHAPE;
+    if (n_elems == 0) return FELLM_OK;  // no rows: nothing to do, as on the CPU (backend.rs:1125-1128)
     if (!x || !weight || !y) return FELLM_ERR_ARITY;
     if (!residual && h_out) return FELLM_ERR_ARITY;
-    if (group == 0 || n_elems == 0 || n_elems % group != 0) return FELLM_ERR_SHAPE;
     const uint64_t rows = n_elems / group;
     if (rows > 0x7fffffffull) return FELLM_ERR_SHAPE;
     hipStream_t s = as_stream(stream);

@@ -405,10 +405,10 @@ extern "C" int fellm_rocm_rope(const void *x1, void *out1, uint32_t n_heads1, co
                                uint32_t rope_dim, uint32_t pairing, const float *inv_freqs,
                                const uint32_t *positions, uint32_t position0, void *stream) {
     using namespace fellm;
-    if (!x1 || !out1 || (rope_dim && !inv_freqs) || n_heads1 == 0) return FELLM_ERR_ARITY;
-    if (x2 && (!out2 || n_heads2 == 0)) return FELLM_ERR_ARITY;
     if (int rc = check_rope_shape(head_dim, rope_dim, pairing)) return rc;
     if (rows == 0) return FELLM_OK;
+    if (!x1 || !out1 || (rope_dim && !inv_freqs) || n_heads1 == 0) return FELLM_ERR_ARITY;
+    if (x2 && (!out2 || n_heads2 == 0)) return FELLM_ERR_ARITY;
     hipStream_t s = as_stream(stream);
     return dispatch_act(act_dtype, [&]<typename A>() -> int {
         using T = typename A::T;

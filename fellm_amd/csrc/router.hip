@@ -217,12 +217,12 @@ extern "C" int fellm_rocm_router_topk(const float *logits, uint32_t tokens, uint
                                       float routed_scaling_factor, uint32_t *ids, float *weights,
                                       void *stream) {
     using namespace fellm;
-    if (!logits || !ids || !weights) return FELLM_ERR_ARITY;
     if (n_experts == 0 || n_experts > kMaxExperts) return FELLM_ERR_SHAPE;
     if (gating_func == 4) return FELLM_ERR_DTYPE;  // sqrt-softplus gating not implemented
     const uint32_t k = n_expert_used < n_experts ? n_expert_used : n_experts;
     if (k == 0 || k > kMaxTopK) return FELLM_ERR_SHAPE;
     if (tokens == 0) return FELLM_OK;
+    if (!logits || !ids || !weights) return FELLM_ERR_ARITY;
     const dim3 block(kRouterBlock);
     hipStream_t s = as_stream(stream);
     // Grouped path: EPL experts per lane, G lanes per token (G a power of two

@@ -138,11 +138,11 @@ def rope(x1, inv_freqs, *, head_dim: int, rope_dim: int | None = None, pairing: 
     _dev(x1, x2, inv_freqs, positions)
     rope_dim = head_dim if rope_dim is None else rope_dim
     rows = x1.shape[0]
-    nh1 = x1.numel() // (rows * head_dim)
+    nh1 = x1.shape[-1] // head_dim
     out1 = x1 if inplace else (out1 if out1 is not None else torch.empty_like(x1))
     nh2 = 0
     if x2 is not None:
-        nh2 = x2.numel() // (rows * head_dim)
+        nh2 = x2.shape[-1] // head_dim
         out2 = x2 if inplace else (out2 if out2 is not None else torch.empty_like(x2))
     _lib.call("fellm_rocm_rope", _p(x1), _p(out1), nh1, _p(x2), _p(out2), nh2, _code(x1), rows, head_dim, rope_dim,
               pairing, _p(inv_freqs), _p(positions), position0, _stream())

@@ -457,3 +457,24 @@ def test_cast_rejects_other_pairs(ops, dev):
     rc = _lib.lib().fellm_rocm_cast(a.data_ptr(), int(DType.F16), b.data_ptr(), int(DType.BF16), 64,
                                     torch.cuda.current_stream().cuda_stream)
     assert rc == -10
+
+
+def test_zero_rows_are_noops(ops, dev):
+    """Empty inputs succeed and write nothing, as the CPU backend's loops run
+    zero times (backend.rs:1026-1046, 1104-1133, 1135-1172, 1174-1184;
+    moe.rs:820-855)."""
+    H, hd = 256, 64
+    f16 = torch.float16
+    e = torch.empty(0, H, dtype=f16, device=dev)
+    w = torch.ones(H, device=dev)
+    assert ops.silu_gate(e.view(-1), e.view(-1)).numel() == 0
+    ops.add_rmsnorm(e, e, w, 1e-5, h_out=torch.empty_like(e), y_out=torch.empty_like(e))
+    ops.rmsnorm(e, w, 1e-5, out=torch.empty_like(e))
+    table = torch.randn(16, H, device=dev).half()
+    assert ops.embedding(table, torch.empty(0, dtype=torch.int32, device=dev)).numel() == 0
+    inv = ops.rope_inv_freqs(10000.0, hd).to(dev)
+    assert ops.rope(e, inv, head_dim=hd).numel() == 0
+    ids, wts = ops.router_topk(torch.empty(0, 8, device=dev), 2)
+    assert ids.numel() == 0 and wts.numel() == 0
+    torch.cuda.synchronize()
+
