@@ -57,6 +57,19 @@ def test_silu_gate(ops, dev, kind, n):
     assert_exact(got, ref, f"silu_gate {kind} n={n}")
 
 
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+def test_silu_gate_16bit_in_f32_out(ops, dev, kind):
+    """16-bit gate/up with an f32 output: the exact silu path (the interval
+    test only decides 16-bit outputs), bit-exact against the oracle."""
+    rng = np.random.default_rng(31)
+    n = 65536 + 3
+    g = random_stored(rng, n, kind, sigma=4.0)
+    u = random_stored(rng, n, kind)
+    ref = oracle.silu_gate(oracle.widen(g, kind), oracle.widen(u, kind))
+    got = from_dev(ops.silu_gate(to_dev(g, kind, dev), to_dev(u, kind, dev), out_dtype=torch.float32))
+    assert_exact(got, ref, f"silu_gate {kind} -> f32")
+
+
 def test_silu_fast_bound_covers_every_gate(ops, dev):
     """The 16-bit SwiGLU outputs skip the exact silu when an interval of
     +-D bit steps around a fast f32 silu fixes the rounded result.  That is
