@@ -11,7 +11,11 @@
 // division uses silu_div below, so the f32 result equals the CPU reference
 // bit for bit.  With ~30 ALU ops per element the kernel sits close to the
 // ALU/HBM balance point, which is why the division is not left to the
-// default 13-instruction IEEE sequence.
+// default 13-instruction IEEE sequence.  For 16-bit outputs most elements
+// skip that exact evaluation altogether: a fast f32 silu whose distance to
+// the exact one is bounded over every input decides the rounded output
+// whenever the interval it implies holds a single 16-bit value
+// (silu_mul_fast, common.hpp); the rest take the exact path.
 #include "common.hpp"
 
 namespace fellm {
