@@ -54,12 +54,25 @@ def _compile(src: str, build_dir: Path = BUILD, extra=()) -> Path:
     return obj
 
 
-def build(verbose: bool = False, out: Path = LIB_PATH, build_dir: Path = BUILD, defines=()) -> Path:
-    """Compile every source and link ``out``; ``defines`` are extra -D flags."""
+def _stale(src: str, build_dir: Path) -> bool:
+    obj = build_dir / (Path(src).stem + ".o")
+    if not obj.exists():
+        return True
+    deps = [CSRC / src, CSRC / "common.hpp", ROOT / "include" / "fellm_abi.h", ROOT / "include" / "fellm_rocm.h"]
+    return any(d.stat().st_mtime > obj.stat().st_mtime for d in deps if d.exists())
+
+
+def build(verbose: bool = False, out: Path = LIB_PATH, build_dir: Path = BUILD, defines=(),
+          incremental: bool = False) -> Path:
+    """Compile every source and link ``out``; ``defines`` are extra -D flags.
+    ``incremental`` recompiles only sources newer than their objects (headers
+    included); the default rebuilds everything."""
     build_dir.mkdir(parents=True, exist_ok=True)
     extra = [f"-D{d}" for d in defines]
+    todo = [s for s in SOURCES if not incremental or _stale(s, build_dir)]
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as ex:
-        objs = list(ex.map(lambda src: _compile(src, build_dir, extra), SOURCES))
+        list(ex.map(lambda src: _compile(src, build_dir, extra), todo))
+    objs = [build_dir / (Path(src).stem + ".o") for src in SOURCES]
     tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), *DEVICE_FLAGS, "-shared", "-fPIC", f"-Wl,--version-script={CSRC / 'exports.map'}",
            "-o", str(tmp), *map(str, objs)]
@@ -73,5 +86,5 @@ def build(verbose: bool = False, out: Path = LIB_PATH, build_dir: Path = BUILD, 
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv)
     sys.exit(0)

@@ -283,6 +283,101 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
     return (float)y;
 }
 
+// ---------------------------------------------------------------------------
+// sinf / cosf, bit-exact with glibc >= 2.28 on x86_64 (Rust's f32::sin_cos on
+// linux-gnu calls these; kernels/rope.rs:46-58 rotates with them).  Algorithm:
+// Szabolcs Nagy's sinf/cosf from ARM optimized-routines (MIT), as glibc ships
+// it.  All arithmetic in double, one final rounding:
+//  * |x| < pi/4: odd polynomial (sin) or even polynomial (cos) in x directly;
+//  * |x| < 120: n = nearest integer to x * 2/pi (taken from the top bits of
+//    x * 2^24 * 2/pi), r = x - n * pi/2 with one FMA;
+//  * larger: Payne-Hanek reduction with 96 bits of 4/pi picked by exponent
+//    (kInvPio4 below), r = (fraction in 2^62 units) * pi/2^62;
+//  * quadrant n selects sin or cos polynomial, its sign and whether the cos
+//    coefficients are negated.
+// glibc's x86_64 FMA variant (chosen at load time on FMA hosts) contracts the
+// Horner steps and r = x - n*pi/2 into FMAs; this restatement does the same.
+// kInvPio4[i] = floor((4/pi) * 2^(8i+7)) mod 2^32, i.e. 32-bit windows of the
+// binary expansion of 4/pi stepping 8 bits (recomputed from an integer pi in
+// the CPU test suite).  The polynomial coefficients are the published ones of
+// that source.  Checked against the host's glibc on all 2^32 inputs.
+// ---------------------------------------------------------------------------
+__device__ __constant__ inline constexpr uint32_t kInvPio4[24] = {
+    0xa2u,       0xa2f9u,     0xa2f983u,   0xa2f9836eu, 0xf9836e4eu, 0x836e4e44u, 0x6e4e4415u, 0x4e441529u,
+    0x441529fcu, 0x1529fc27u, 0x29fc2757u, 0xfc2757d1u, 0x2757d1f5u, 0x57d1f534u, 0xd1f534ddu, 0xf534ddc0u,
+    0x34ddc0dbu, 0xddc0db62u, 0xc0db6295u, 0xdb629599u, 0x6295993cu, 0x95993c43u, 0x993c4390u, 0x3c439041u};
+
+// One of the two polynomials of the optimized-routines sinf/cosf on the
+// reduced argument x (x2 = x*x).  odd: sin polynomial; else cos polynomial,
+// whose coefficients are negated when neg_cos (quadrants 2 and 3).
+__device__ __forceinline__ float sincosf_poly(double x, double x2, bool odd, bool neg_cos) {
+    if (odd) {
+        const double S1 = -0x1.555545995a603p-3, S2 = 0x1.1107605230bc4p-7, S3 = -0x1.994eb3774cf24p-13;
+        const double x3 = __dmul_rn(x, x2);
+        const double s1 = __fma_rn(x2, S3, S2);
+        const double x7 = __dmul_rn(x3, x2);
+        const double s = __fma_rn(x3, S1, x);
+        return (float)__fma_rn(x7, s1, s);
+    }
+    const double g = neg_cos ? -1.0 : 1.0;  // exact sign flip of every coefficient
+    const double C0 = g * 0x1p0, C1 = g * -0x1.ffffffd0c621cp-2, C2 = g * 0x1.55553e1068f19p-5,
+                 C3 = g * -0x1.6c087e89a359dp-10, C4 = g * 0x1.99343027bf8c3p-16;
+    const double x4 = __dmul_rn(x2, x2);
+    const double c2 = __fma_rn(x2, C4, C3);
+    const double c1 = __fma_rn(x2, C1, C0);
+    const double x6 = __dmul_rn(x4, x2);
+    const double c = __fma_rn(x4, C2, c1);
+    return (float)__fma_rn(x6, c2, c);
+}
+
+__device__ __forceinline__ void sincosf_glibc(float y, float *sp, float *cp) {
+    const uint32_t xi = __float_as_uint(y);
+    const uint32_t top = (xi >> 20) & 0x7ffu;
+    double x = (double)y;
+    if (top < 0x3f4u) {      // |y| < pi/4 (abstop12 of 0x1.921FB6p-1f)
+        if (top < 0x398u) {  // |y| < 2^-12
+            *sp = y;
+            *cp = 1.0f;
+            return;
+        }
+        const double x2 = __dmul_rn(x, x);
+        *sp = sincosf_poly(x, x2, true, false);
+        *cp = sincosf_poly(x, x2, false, false);
+        return;
+    }
+    if (top >= 0x7f8u) {  // inf or NaN
+        *sp = *cp = y - y;
+        return;
+    }
+    int n, q;  // n: polynomial parity; q: quadrant of the signs and coefficient set
+    if (top < 0x42fu) {  // |y| < 120
+        const double r = __dmul_rn(x, 0x1.45F306DC9C883p+23);
+        n = ((int32_t)r + 0x800000) >> 24;
+        x = __fma_rn(-(double)n, 0x1.921FB54442D18p0, x);
+        q = n & 3;
+    } else {
+        const uint32_t *arr = &kInvPio4[(xi >> 26) & 15];
+        const int shift = (xi >> 23) & 7;
+        const uint32_t m = ((xi & 0xffffffu) | 0x800000u) << shift;
+        uint64_t r0 = (uint64_t)(uint32_t)(m * arr[0]);
+        const uint64_t r1 = (uint64_t)m * arr[4];
+        const uint64_t r2 = (uint64_t)m * arr[8];
+        r0 = (r2 >> 32) | (r0 << 32);
+        r0 += r1;
+        const uint64_t nn = (r0 + (1ull << 61)) >> 62;
+        r0 -= nn << 62;
+        x = __dmul_rn((double)(int64_t)r0, 0x1.921FB54442D18p-62);
+        n = (int)nn;
+        q = (n + (int)(xi >> 31)) & 3;  // the reduction took |y|: its sign joins the quadrant
+    }
+    const double s = (q == 1 || q == 2) ? -1.0 : 1.0;
+    const double xs = __dmul_rn(x, s), x2 = __dmul_rn(x, x);
+    const bool neg = (q & 2) != 0;
+    // Quadrant parity swaps the roles of the two polynomials.
+    *sp = sincosf_poly(xs, x2, (n & 1) == 0, neg);
+    *cp = sincosf_poly(xs, x2, (n & 1) != 0, neg);
+}
+
 // get_scale_min_k4 (dequant.rs:295-305): 6-bit scale and min j (0..7) of a
 // Q4_K/Q5_K block from its 12 scale bytes held as 3 little-endian dwords.
 __device__ __forceinline__ void k4_scale_min(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,

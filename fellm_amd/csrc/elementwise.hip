@@ -1,4 +1,5 @@
-// Elementwise kernels for gfx950: SwiGLU (SiLU-gate * up), Add, expf check.
+// Elementwise kernels for gfx950: SwiGLU (SiLU-gate * up), Add, expf and
+// sinf/cosf checks.
 //
 // SiluGate reference: crates/backend-cpu/src/kernels/swiglu.rs:5-16
 //   out[i] = (g / (1 + exp(-g))) * u       (f32, libm expf)
@@ -127,6 +128,17 @@ __global__ __launch_bounds__(kEwBlock) void expf_kernel(const float *__restrict_
         out[i] = expf_glibc(in[i], tab);
 }
 
+__global__ __launch_bounds__(kEwBlock) void sincosf_kernel(const float *__restrict__ in, float *__restrict__ sin_out,
+                                                           float *__restrict__ cos_out, uint64_t n) {
+    const uint64_t stride = (uint64_t)gridDim.x * kEwBlock;
+    for (uint64_t i = (uint64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += stride) {
+        float sv, cv;
+        sincosf_glibc(in[i], &sv, &cv);
+        sin_out[i] = sv;
+        cos_out[i] = cv;
+    }
+}
+
 // Largest bit distance between silu_fast and silu over every f32 g of the
 // fast domain, one grid-stride sweep of all 2^32 patterns.
 __global__ __launch_bounds__(kEwBlock) void silu_fast_bound_kernel(uint32_t *__restrict__ max_dist) {
@@ -215,6 +227,15 @@ extern "C" int fellm_rocm_add(const void *a, const void *b, uint32_t in_dtype, v
         if (out_dtype == FELLM_DTYPE_F32) return launch_add<I, F32>(a, b, out, n_elems, s);
         return FELLM_ERR_DTYPE;
     });
+}
+
+extern "C" int fellm_rocm_sincosf(const float *in, float *sin_out, float *cos_out, uint64_t n, void *stream) {
+    using namespace fellm;
+    if (n == 0) return FELLM_OK;
+    if (!in || !sin_out || !cos_out) return FELLM_ERR_ARITY;
+    hipLaunchKernelGGL(sincosf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), in, sin_out, cos_out,
+                       n);
+    return launch_status();
 }
 
 extern "C" int fellm_rocm_expf(const float *in, float *out, uint64_t n, void *stream) {

@@ -11,8 +11,8 @@
 //   block bytes from crates/backend-cuda/src/vram_pool.rs:31-35.
 //
 // One workgroup handles one token row.  The rope_dim/2 (sin, cos) pairs for
-// that row's position are computed once into LDS (in double precision, then
-// rounded to f32, which matches the correctly-rounded libm values) and shared
+// that row's position are computed once into LDS (a bit-exact restatement of
+// glibc's sinf/cosf, the libm behind Rust's f32::sin_cos) and shared
 // by every head of q and k, instead of once per (head, pair) as on the CPU.
 // The row is then cut into items of PV pairs (PV = 4: one 16-byte access per
 // item for 16-bit activations) spread over the block.  In KV mode the rotated
@@ -22,10 +22,6 @@
 
 #include "common.hpp"
 
-// Build knob: sin/cos of theta evaluated in double then rounded (1) or with f32 sincosf (0).
-#ifndef FELLM_ROPE_DOUBLE_TRIG
-#define FELLM_ROPE_DOUBLE_TRIG 1
-#endif
 // Build knob: non-temporal activation loads (bit 0) and stores (bit 1).
 #ifndef FELLM_ROPE_NT
 #define FELLM_ROPE_NT 2
@@ -233,15 +229,9 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
         else
             pos = rope_pos ? rope_pos[row] : pos0 + row;
         const float theta = (float)pos * inv_freqs[i];
-        if constexpr (FELLM_ROPE_DOUBLE_TRIG) {
-            double sd, cd;
-            sincos((double)theta, &sd, &cd);
-            cs_all[rr][i] = make_float2((float)sd, (float)cd);
-        } else {
-            float sf, cf;
-            sincosf(theta, &sf, &cf);
-            cs_all[rr][i] = make_float2(sf, cf);
-        }
+        float sf, cf;
+        sincosf_glibc(theta, &sf, &cf);
+        cs_all[rr][i] = make_float2(sf, cf);
     }
     if constexpr (MODE == 1) {
         if (threadIdx.x < R) {

@@ -427,6 +427,14 @@ def expf(x):
     return out
 
 
+def sincosf(x):
+    """Device glibc-exact (sinf(x), cosf(x)) (self-check of the restatement RoPE uses)."""
+    _dev(x)
+    s, c = torch.empty_like(x), torch.empty_like(x)
+    _lib.call("fellm_rocm_sincosf", _p(x), _p(s), _p(c), x.numel(), _stream())
+    return s, c
+
+
 def silu_fast_bound():
     """(largest measured bit distance between the fast and the exact silu over
     every f32 gate of the fast domain, the distance the SwiGLU 16-bit path

@@ -332,6 +332,13 @@ int fellm_rocm_stream_is_capturing(void *stream);
 int fellm_rocm_expf(const float *in, float *out, uint64_t n, void *stream);
 
 /*
+ * Self-check of the device sinf/cosf restatement that builds RoPE's per-row
+ * (sin, cos) table: sin_out[i] = sinf(in[i]), cos_out[i] = cosf(in[i]).
+ * Diagnostic only (no counterpart in the reference).
+ */
+int fellm_rocm_sincosf(const float *in, float *sin_out, float *cos_out, uint64_t n, void *stream);
+
+/*
  * Verification hook for fellm_rocm_silu_gate's 16-bit output path (no
  * counterpart in the reference).  That path skips the exact silu when an
  * interval of +-fellm_rocm_silu_fast_dist() steps around a fast f32 silu

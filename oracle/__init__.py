@@ -40,6 +40,7 @@ def lib() -> C.CDLL:
             "oracle_bf16_to_f32": (None, [P, P, S]),
             "oracle_f32_to_bf16": (None, [P, P, S, C.c_int]),
             "oracle_expf": (None, [P, P, S]),
+            "oracle_sincosf": (None, [P, P, P, S]),
             "oracle_get_scale_min_k4": (None, [S, P, P, P]),
             "oracle_row_bytes": (S, [U32, S]),
             "oracle_dequantize_row": (C.c_int, [U32, P, P, S]),
@@ -134,6 +135,14 @@ def expf(x: np.ndarray) -> np.ndarray:
     out = np.empty_like(a)
     lib().oracle_expf(_p(a), _p(out), a.size)
     return out
+
+
+def sincosf(x: np.ndarray):
+    """(sinf(x), cosf(x)) from the host's glibc, as f32::sin_cos gives them."""
+    a = _c(x, np.float32)
+    s, c = np.empty_like(a), np.empty_like(a)
+    lib().oracle_sincosf(_p(a), _p(s), _p(c), a.size)
+    return s, c
 
 
 # ---- ops ---------------------------------------------------------------------

@@ -126,6 +126,14 @@ void oracle_expf(const float *in, float *out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = expf(in[i]);
 }
 
+/* f32::sin_cos as rope.rs:46-58 calls it: glibc sinf and cosf. */
+void oracle_sincosf(const float *in, float *s, float *c, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        s[i] = sinf(in[i]);
+        c[i] = cosf(in[i]);
+    }
+}
+
 /* ---- a1: dequant + embedding -------------------------------------------- */
 
 /* dequant.rs:295-305 */

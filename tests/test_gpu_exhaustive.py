@@ -2,6 +2,9 @@
 
 * the device expf restatement against the host's glibc expf (the libm the
   reference's f32::exp calls), all 2^32 inputs;
+* the device sinf/cosf restatement (RoPE's per-row sin/cos table) against
+  the host's glibc sinf and cosf (f32::sin_cos, kernels/rope.rs:46-58), all
+  2^32 inputs;
 * SwiGLU's silu(g) = g / (1 + exp(-g)) (kernels/swiglu.rs:5-7) through the
   product kernel with up = 1, against the oracle, all 2^32 values of g.
   silu depends on g alone, so this proves the kernel's exp + division path
@@ -32,6 +35,11 @@ def _bits(start: int) -> np.ndarray:
 
 def _host_expf(start: int) -> np.ndarray:
     return oracle.expf(_bits(start))
+
+
+def _host_sincosf(start: int) -> np.ndarray:
+    s, c = oracle.sincosf(_bits(start))
+    return np.concatenate([s, c])
 
 
 def _host_silu(start: int) -> np.ndarray:
@@ -79,3 +87,13 @@ def test_silu_all_inputs(dev):
         return ops.silu_gate(g, ones).cpu().numpy()
 
     _sweep(dev_fn, _host_silu, "silu")
+
+
+def test_sincosf_all_inputs(dev):
+    from fellm_amd import ops
+
+    def dev_fn(start):
+        s, c = ops.sincosf(torch.from_numpy(_bits(start)).to(dev))
+        return torch.cat([s, c]).cpu().numpy()
+
+    _sweep(dev_fn, _host_sincosf, "sincosf")

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from parity_util import (KINDS, assert_close, assert_exact, assert_rope_close, from_dev, pair_magnitude,
+from parity_util import (KINDS, assert_close, assert_exact, from_dev,
                          random_stored, to_dev)
 
 pytestmark = pytest.mark.gpu
@@ -43,6 +43,26 @@ def test_device_expf_matches_glibc(ops, dev):
     nan = np.isnan(ref)
     assert np.array_equal(np.isnan(got), nan)
     assert_exact(got[~nan], ref[~nan], "expf")
+
+
+def test_device_sincosf_matches_glibc(ops, dev):
+    """RoPE's sin/cos table entries: every reduction path (|x| < 2^-12, < pi/4,
+    < 120, Payne-Hanek) and the RoPE angle range, bit for bit."""
+    rng = np.random.default_rng(2)
+    bits = rng.integers(0, 2**32, size=1 << 22, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0.0, -0.0, 2.0 ** -12, -(2.0 ** -12), 0.785398, 0.7853982, 119.99999, 120.0, -120.0, 1e30,
+                        3.4e38, np.inf, -np.inf, np.nan, 1e-45], np.float32)
+    dense = np.linspace(-40000.0, 40000.0, 1 << 21, dtype=np.float32)
+    pos = np.arange(32768, dtype=np.float32)
+    inv = oracle.rope_inv_freqs(500000.0, 128)
+    angles = (pos[:, None] * inv[None, :]).astype(np.float32).ravel()
+    x = np.concatenate([bits.view(np.float32), special, dense, angles])
+    s, c = ops.sincosf(torch.from_numpy(x).to(dev))
+    rs, rc = oracle.sincosf(x)
+    for got, ref, what in ((from_dev(s), rs, "sinf"), (from_dev(c), rc, "cosf")):
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(got), nan), what
+        assert_exact(got[~nan], ref[~nan], what)
 
 
 # ---- SwiGLU --------------------------------------------------------------------
@@ -255,10 +275,8 @@ def test_rope_qk(ops, dev, kind, pairing, head_dim, rope_dim):
     qo, ko = ops.rope(to_dev(q, kind, dev), torch.from_numpy(inv).to(dev), head_dim=head_dim, rope_dim=rope_dim,
                       pairing=pairing, positions=torch.from_numpy(pos.view(np.int32)).to(dev),
                       x2=to_dev(k, kind, dev))
-    assert_rope_close(from_dev(qo), qr, pair_magnitude(oracle.widen(q, kind), nq, head_dim, rope_dim, pairing),
-                      kind, "q")
-    assert_rope_close(from_dev(ko), kr, pair_magnitude(oracle.widen(k, kind), nk, head_dim, rope_dim, pairing),
-                      kind, "k")
+    assert_exact(from_dev(qo), qr, "q")
+    assert_exact(from_dev(ko), kr, "k")
     # passthrough dims are copied exactly
     if rope_dim < head_dim:
         qv, rv = from_dev(qo).reshape(rows, nq, head_dim), q.reshape(rows, nq, head_dim)
@@ -274,7 +292,7 @@ def test_rope_position0_inplace(ops, dev):
     ref = oracle.rope(x, nh, hd, hd, 0, inv, None, position0=100)
     xd = torch.from_numpy(x).to(dev)
     ops.rope(xd, torch.from_numpy(inv).to(dev), head_dim=hd, position0=100, inplace=True)
-    assert_rope_close(from_dev(xd), ref, pair_magnitude(x, nh, hd, hd, 0), "f32", "in-place pos0")
+    assert_exact(from_dev(xd), ref, "in-place pos0")
     # position 0 is the identity (rope.rs:69-77)
     x0 = rng.normal(size=(1, nh * hd)).astype(np.float32)
     got = from_dev(ops.rope(torch.from_numpy(x0).to(dev), torch.from_numpy(inv).to(dev), head_dim=hd))
@@ -341,16 +359,14 @@ def test_rope_kv_write_fused(ops, dev, kind, kv_kind, pairing):
     qf, kf = oracle.widen(q, kind), oracle.widen(k, kind)
     q_ref = oracle.rope(qf, nq, hd, hd, pairing, inv, rope_pos)
     k_ref = oracle.rope(kf, nkv, hd, hd, pairing, inv, rope_pos)
-    assert_rope_close(from_dev(qo), oracle.narrow(q_ref, kind), pair_magnitude(qf, nq, hd, hd, pairing), kind, "q")
-    assert_rope_close(from_dev(k_out), oracle.narrow(k_ref, kind), pair_magnitude(kf, nkv, hd, hd, pairing), kind,
-                      "k_out")
-    # V slots: bit-exact.  K slots: the rotated K rounded once to the cache dtype.
+    assert_exact(from_dev(qo), oracle.narrow(q_ref, kind), "q")
+    assert_exact(from_dev(k_out), oracle.narrow(k_ref, kind), "k_out")
+    # V slots and K slots (the rotated K rounded once to the cache dtype): bit-exact.
     ref = np.zeros(arena.numel(), np.uint8)
     oracle.kv_write_paged(k_ref, stride, kv_pos, table, n_logical, 1, 0, bs, bb, ref, False, kv_kind)
     oracle.kv_write_paged(oracle.widen(v, kind), stride, kv_pos, table, n_logical, 1, 0, bs, bb, ref, True, kv_kind)
     got = arena.cpu().numpy()
     row_bytes = stride * 2
-    kmag = pair_magnitude(kf, nkv, hd, hd, pairing)
     for b in range(batch):
         phys = table[kv_pos[b] // bs]
         base = phys * bb + (kv_pos[b] % bs) * row_bytes
@@ -358,7 +374,7 @@ def test_rope_kv_write_fused(ops, dev, kind, kv_kind, pairing):
         assert_exact(got[vbase:vbase + row_bytes], ref[vbase:vbase + row_bytes], f"V row {b}")
         gk = got[base:base + row_bytes].view(np.uint16)
         rk = ref[base:base + row_bytes].view(np.uint16)
-        assert_rope_close(gk, rk, kmag[b], kv_kind, f"K row {b}")
+        assert_exact(gk, rk, f"K row {b}")
         got[base:base + row_bytes] = ref[base:base + row_bytes]
         got[vbase:vbase + row_bytes] = ref[vbase:vbase + row_bytes]
     assert_exact(got, ref, "untouched arena bytes")
@@ -400,20 +416,60 @@ def test_router_topk(ops, dev, n_exp, k, gating, norm, rsf):
     assert_exact(from_dev(w), w_ref, "weights")
 
 
-@pytest.mark.parametrize("rows", [2051, 4099])
-def test_rope_many_rows(ops, dev, rows):
-    """Row counts that select 2 and 4 rows per workgroup, with a ragged tail."""
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+@pytest.mark.parametrize("rows", [2051, 8193, 16385])
+def test_rope_many_rows(ops, dev, kind, rows):
+    """configs[4]'s RoPE shape (head_dim 128, 32 q / 4 kv heads, theta 1e6,
+    positions 0..rows-1) at row counts that select 1, 2 and 4 rows per
+    workgroup (the launcher switches at 8192 and 16384 rows), each with a
+    ragged last workgroup; bit-exact against the oracle."""
     rng = np.random.default_rng(rows)
-    nq, nk, hd = 2, 1, 64
-    inv = oracle.rope_inv_freqs(10000.0, hd)
-    q = rng.normal(size=(rows, nq * hd)).astype(np.float32)
-    k = rng.normal(size=(rows, nk * hd)).astype(np.float32)
-    qr = oracle.rope(q, nq, hd, hd, 1, inv, None, position0=3)
-    kr = oracle.rope(k, nk, hd, hd, 1, inv, None, position0=3)
-    qo, ko = ops.rope(torch.from_numpy(q).to(dev), torch.from_numpy(inv).to(dev), head_dim=hd, pairing=1,
-                      position0=3, x2=torch.from_numpy(k).to(dev))
-    assert_rope_close(from_dev(qo), qr, pair_magnitude(q, nq, hd, hd, 1), "f32", "q")
-    assert_rope_close(from_dev(ko), kr, pair_magnitude(k, nk, hd, hd, 1), "f32", "k")
+    nq, nk, hd = 32, 4, 128
+    inv = oracle.rope_inv_freqs(1.0e6, hd)
+    q = random_stored(rng, (rows, nq * hd), kind)
+    k = random_stored(rng, (rows, nk * hd), kind)
+    qr = oracle.narrow(oracle.rope(oracle.widen(q, kind), nq, hd, hd, 0, inv, None, position0=0), kind)
+    kr = oracle.narrow(oracle.rope(oracle.widen(k, kind), nk, hd, hd, 0, inv, None, position0=0), kind)
+    pos = torch.arange(rows, dtype=torch.int32, device=dev)
+    qo, ko = ops.rope(to_dev(q, kind, dev), torch.from_numpy(inv).to(dev), head_dim=hd, pairing=0,
+                      positions=pos, x2=to_dev(k, kind, dev))
+    assert_exact(from_dev(qo), qr, f"q {rows} rows")
+    assert_exact(from_dev(ko), kr, f"k {rows} rows")
+    # split-half pairing and the position0 form through the same variants
+    q1 = random_stored(rng, (rows, 2 * 64), "f32")
+    r1 = oracle.rope(q1, 2, 64, 64, 1, oracle.rope_inv_freqs(10000.0, 64), None, position0=3)
+    g1 = ops.rope(torch.from_numpy(q1).to(dev), torch.from_numpy(oracle.rope_inv_freqs(10000.0, 64)).to(dev),
+                  head_dim=64, pairing=1, position0=3)
+    assert_exact(from_dev(g1), r1, f"split-half {rows} rows")
+
+
+@pytest.mark.parametrize("kind", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("rows,group", [(1024, 2048), (1031, 1000), (1024, 8192), (1029, 16384), (1024, 12288)])
+def test_add_rmsnorm_many_rows(ops, dev, kind, rows, group):
+    """>= 1024 rows select the 256-thread layouts: NCHUNK = 1 (group <= 2048),
+    4 (<= 8192) and 8 (<= 16384) chunks of 8 elements per thread, plus the
+    two-pass fallback for a group that is not a multiple of 8."""
+    rng = np.random.default_rng(rows * 31 + group)
+    x = random_stored(rng, (rows, group), kind)
+    r = random_stored(rng, (rows, group), kind, sigma=2.0)
+    w = rng.normal(1.0, 0.1, size=group).astype(np.float32)
+    h_ref, y_ref = oracle.add_rmsnorm(x, r, w, 1e-6, kind)
+    h, y = ops.add_rmsnorm(to_dev(x, kind, dev), to_dev(r, kind, dev), torch.from_numpy(w).to(dev), 1e-6)
+    assert_exact(from_dev(h), h_ref, f"h {kind}")
+    assert_close(from_dev(y), y_ref, kind, what=f"y {kind} {rows}x{group}")
+    y_plain = ops.rmsnorm(to_dev(x, kind, dev), torch.from_numpy(w).to(dev), 1e-6)
+    assert_close(from_dev(y_plain), oracle.narrow(oracle.rmsnorm(oracle.widen(x, kind), w, 1e-6), kind), kind,
+                 what=f"plain {kind} {rows}x{group}")
+
+
+def test_rmsnorm_c5_shape(ops, dev):
+    """configs[4]'s RMSNorm as the bench times it: 16384 x 2048 bf16, eps 1e-6."""
+    rng = np.random.default_rng(16384)
+    x = random_stored(rng, (16384, 2048), "bf16")
+    w = rng.normal(1.0, 0.1, size=2048).astype(np.float32)
+    y = ops.rmsnorm(to_dev(x, "bf16", dev), torch.from_numpy(w).to(dev), 1e-6)
+    ref = oracle.narrow(oracle.rmsnorm(oracle.widen(x, "bf16"), w, 1e-6), "bf16")
+    assert_close(from_dev(y), ref, "bf16", what="c5 rmsnorm")
 
 
 # ---- Cast (backend.rs:1603-1667) ---------------------------------------------------

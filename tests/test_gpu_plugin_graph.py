@@ -24,7 +24,7 @@ torch = pytest.importorskip("torch")
 import oracle  # noqa: E402
 from fellm_amd import abi  # noqa: E402
 from fellm_amd.plugin_host import PagedKvContext, PluginError, PluginHost  # noqa: E402
-from parity_util import assert_rope_close, pair_magnitude  # noqa: E402
+from parity_util import assert_exact  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 D = abi.DType
@@ -93,8 +93,7 @@ def test_graph_smoke_add_and_controlled_rope(host):
     host.launch(rope, attrs, rins, [tmut(y, D.F32)])
     sync(host)
     got1 = materialize(host, y, D.F32)
-    assert_rope_close(got1, oracle.rope(x, 1, 4, 4, 0, inv, np.array([1], np.uint32)),
-                      pair_magnitude(x, 1, 4, 4, 0), "f32", "eager rope at the step position")
+    assert_exact(got1, oracle.rope(x, 1, 4, 4, 0, inv, np.array([1], np.uint32)), "eager rope at the step position")
     cap = host.begin_graph_capture()
     host.launch(rope, attrs, rins, [tmut(y, D.F32)])
     g = cap.finish()
@@ -104,7 +103,7 @@ def test_graph_smoke_add_and_controlled_rope(host):
         sync(host)
         got = materialize(host, y, D.F32)
         ref = oracle.rope(x, 1, 4, 4, 0, inv, np.array([pos], np.uint32))
-        assert_rope_close(got, ref, pair_magnitude(x, 1, 4, 4, 0), "f32", f"replay at position {pos}")
+        assert_exact(got, ref, f"replay at position {pos}")
     exp2 = np.array([np.cos(2.0), np.sin(2.0), np.cos(0.2), np.sin(0.2)], np.float32)
     host.update_step_params(abi.DeviceStepParams(position=2))
     g.launch(host.stream())

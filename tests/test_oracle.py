@@ -306,6 +306,46 @@ def test_oracle_expf_is_libm():
     assert all(got[i] == np.float32(libm.expf(float(x[i]))) for i in range(x.size))
 
 
+def test_oracle_sincosf_is_libm():
+    import ctypes
+    import ctypes.util
+
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    for fn in (libm.sinf, libm.cosf):
+        fn.restype = ctypes.c_float
+        fn.argtypes = [ctypes.c_float]
+    x = np.concatenate([np.linspace(-3e4, 3e4, 997), [0.0, 1e-5, 100.0, 1e20]]).astype(np.float32)
+    s, c = oracle.sincosf(x)
+    assert all(s[i] == np.float32(libm.sinf(float(x[i]))) for i in range(x.size))
+    assert all(c[i] == np.float32(libm.cosf(float(x[i]))) for i in range(x.size))
+
+
+def test_device_inv_pio4_table_is_4_over_pi():
+    """The Payne-Hanek table of the device sinf/cosf (common.hpp kInvPio4):
+    entry i = floor(4/pi * 2^(8i+7)) mod 2^32, recomputed here from pi by
+    Machin's formula in integer arithmetic (300 decimal digits)."""
+    import re
+    from pathlib import Path
+
+    src = (Path(__file__).resolve().parents[1] / "fellm_amd" / "csrc" / "common.hpp").read_text()
+    body = re.search(r"kInvPio4\[24\] = \{(.*?)\};", src, re.S).group(1)
+    table = [int(v.rstrip("u"), 16) for v in re.findall(r"0x[0-9a-fA-F]+u", body)]
+
+    def arctan_inv(x, one):
+        total, term, n, sign = 0, one // x, 1, 1
+        while term:
+            total += sign * (term // n)
+            term //= x * x
+            n += 2
+            sign = -sign
+        return total
+
+    one = 10 ** 300
+    pi = 4 * (4 * arctan_inv(5, one) - arctan_inv(239, one))  # pi * 10^300
+    want = [((4 * one) << (8 * i + 7)) // pi & 0xFFFFFFFF for i in range(24)]
+    assert table == want
+
+
 # ---- paged kv write -------------------------------------------------------------------
 @pytest.mark.parametrize("elem", ["f16", "bf16"])
 def test_kv_write_addressing(elem):
