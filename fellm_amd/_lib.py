@@ -72,6 +72,8 @@ _SIGNATURES = {
     "fellm_rocm_matvec_kquant_q8k": (I32, [P, U32, U32, U32, P, P, P]),
     "fellm_rocm_moe_dispatch_workspace": (U64, [U64, U32, U32]),
     "fellm_rocm_moe_dispatch": (I32, [P, U64, U32, U32, P, P, P, P, P, P, U64, P]),
+    "fellm_rocm_moe_dispatch_noalloc_max_bytes": (U64, []),
+    "fellm_rocm_moe_dispatch_noalloc": (I32, [P, U64, U32, U32, P, P, P, P, P, P]),
     "fellm_rocm_moe_gather": (I32, [P, U32, U64, U32, U64, P, P, P, P]),
     "fellm_rocm_moe_combine": (I32, [P, P, P, P, P, U64, U32, U64, P, P]),
     "fellm_rocm_step_kv_position": (I32, [P, U32, P, P]),

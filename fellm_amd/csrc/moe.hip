@@ -30,6 +30,8 @@
 // chunk (>= 2048 assignments), a wavefront a quarter of it; pass 1 counts per
 // block, pass 2 turns the counts into cursors and scatters stably.  Up to 2048
 // assignments (decode batches) it is one launch.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace fellm {
@@ -449,30 +451,94 @@ extern "C" uint64_t fellm_rocm_moe_dispatch_workspace(uint64_t tokens, uint32_t 
     return g.nblocks <= 1 ? 0 : (uint64_t)g.nblocks * n_experts * sizeof(uint32_t);
 }
 
-extern "C" int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32_t n_experts,
-                                       uint32_t *counts, uint32_t *offsets, uint32_t *order, uint32_t *inv,
-                                       uint32_t *err_flag, void *workspace, uint64_t workspace_bytes, void *stream) {
-    using namespace fellm;
+// Library-owned per-block count buffer of the allocation-free dispatch
+// (fellm_rocm_moe_dispatch_noalloc): the largest grid (256 blocks) times the
+// most experts (4096), 4 MiB.  Each GPU holds its own copy until the process
+// ends; host code reaches it only through the address hipGetSymbolAddress
+// returns for the current device, never through this name.
+constexpr uint64_t kDispatchScratchWords = 256ull * 4096ull;
+static __device__ __align__(256) uint32_t scratch[kDispatchScratchWords];
+
+namespace fellm {
+namespace {
+
+// Validates the dispatch arguments and enqueues its one or two launches;
+// `bc_ws` holds the per-block counts (at least nblocks * E u32) when the
+// grid has more than one block.
+int dispatch_launch(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32_t n_experts, uint32_t *counts,
+                    uint32_t *offsets, uint32_t *order, uint32_t *inv, uint32_t *err_flag, uint32_t *bc_ws,
+                    uint64_t bc_bytes, hipStream_t st) {
     if (!counts || !offsets) return FELLM_ERR_ARITY;
     if (n_experts == 0 || n_experts > kMoeMaxExperts || top_k == 0 || top_k > kMoeMaxTopK) return FELLM_ERR_SHAPE;
     const uint64_t n = tokens * top_k;
     if (tokens > 0xffffffffull || n >= 0xffffffffull) return FELLM_ERR_SHAPE;
     if (n && (!ids || !order)) return FELLM_ERR_ARITY;
-    hipStream_t st = as_stream(stream);
     const uint32_t E = n_experts, bits = id_bits(E);
     const DispatchGrid g = dispatch_grid(n);
     const uint32_t *bc = nullptr;
     if (g.nblocks > 1) {
-        if (!workspace || workspace_bytes < (uint64_t)g.nblocks * E * sizeof(uint32_t)) return FELLM_ERR_SHAPE;
-        uint32_t *ws = static_cast<uint32_t *>(workspace);
+        if (!bc_ws || bc_bytes < (uint64_t)g.nblocks * E * sizeof(uint32_t)) return FELLM_ERR_SHAPE;
+        // Pass 1 writes every one of the nblocks * E counts before pass 2
+        // reads them, so the buffer needs no clearing between calls.
         hipLaunchKernelGGL(moe_count_blocks, dim3(g.nblocks), dim3(kDispatchBlock), (size_t)E * sizeof(uint32_t),
-                           st, ids, n, E, g.chunk, ws, err_flag);
-        bc = ws;
+                           st, ids, n, E, g.chunk, bc_ws, err_flag);
+        bc = bc_ws;
     }
     const size_t lds = (size_t)(kDispatchWaves + 2) * E * sizeof(uint32_t);
     hipLaunchKernelGGL(moe_scatter_blocks, dim3(g.nblocks), dim3(kDispatchBlock), lds, st, ids, n, E, bits, g.chunk,
                        g.nblocks, bc, counts, offsets, order, inv, err_flag);
     return launch_status();
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint32_t *g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per device.
+static_assert(kDispatchScratchWords == (uint64_t)kMaxDispatchBlocks * kMoeMaxExperts,
+              "the scratch buffer holds the per-block counts of the largest dispatch grid");
+
+int scratch_for_current_device(uint32_t **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FELLM_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return FELLM_ERR_ALLOC;
+        g_scratch_ptr[dev] = static_cast<uint32_t *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return FELLM_OK;
+}
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32_t n_experts,
+                                       uint32_t *counts, uint32_t *offsets, uint32_t *order, uint32_t *inv,
+                                       uint32_t *err_flag, void *workspace, uint64_t workspace_bytes, void *stream) {
+    using namespace fellm;
+    return dispatch_launch(ids, tokens, top_k, n_experts, counts, offsets, order, inv, err_flag,
+                           static_cast<uint32_t *>(workspace), workspace ? workspace_bytes : 0, as_stream(stream));
+}
+
+extern "C" uint64_t fellm_rocm_moe_dispatch_noalloc_max_bytes(void) {
+    return kDispatchScratchWords * sizeof(uint32_t);
+}
+
+extern "C" int fellm_rocm_moe_dispatch_noalloc(const uint32_t *ids, uint64_t tokens, uint32_t top_k,
+                                               uint32_t n_experts, uint32_t *counts, uint32_t *offsets,
+                                               uint32_t *order, uint32_t *inv, uint32_t *err_flag, void *stream) {
+    using namespace fellm;
+    if (n_experts > kMoeMaxExperts || top_k == 0 || top_k > kMoeMaxTopK) return FELLM_ERR_SHAPE;
+    const uint64_t need = fellm_rocm_moe_dispatch_workspace(tokens, top_k, n_experts);
+    if (need > kDispatchScratchWords * sizeof(uint32_t)) return FELLM_ERR_SHAPE;  // beyond the library's buffer
+    uint32_t *ws = nullptr;
+    if (need) {
+        if (int rc = scratch_for_current_device(&ws)) return rc;
+    }
+    return dispatch_launch(ids, tokens, top_k, n_experts, counts, offsets, order, inv, err_flag, ws,
+                           kDispatchScratchWords * sizeof(uint32_t), as_stream(stream));
 }
 
 extern "C" int fellm_rocm_moe_gather(const void *x, uint32_t elem_bytes, uint64_t tokens, uint32_t top_k,

@@ -263,6 +263,25 @@ int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uint32_t top_k
                             uint32_t *err_flag, void *workspace, uint64_t workspace_bytes, void *stream);
 
 /*
+ * Allocation-free MoE dispatch: fellm_rocm_moe_dispatch with the per-block
+ * count buffer taken from a 4 MiB array the library keeps on each GPU
+ * (fellm_rocm_moe_dispatch_noalloc_max_bytes()) instead of a workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops).
+ * Same arguments, results and errors as fellm_rocm_moe_dispatch; a dispatch
+ * whose count buffer would exceed the array returns FELLM_ERR_SHAPE (every
+ * shape the dispatch accepts fits).  It calls no allocator.  The first call
+ * on a device looks the array's address up (hipGetSymbolAddress) with that
+ * device current.  All calls on one GPU share the array: calls that overlap
+ * on one GPU (concurrent streams or host threads) race and must be
+ * serialised by the caller.
+ */
+uint64_t fellm_rocm_moe_dispatch_noalloc_max_bytes(void);
+int fellm_rocm_moe_dispatch_noalloc(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32_t n_experts,
+                                    uint32_t *counts, uint32_t *offsets, uint32_t *order, uint32_t *inv,
+                                    uint32_t *err_flag, void *stream);
+
+/*
  * grouped[p, :] = x[order[p] / top_k, :] for p < A (moe.rs:954-957); rows of
  * `hidden` elements of elem_bytes (1, 2 or 4) bytes, copied bit for bit.  An
  * order entry >= A (0xffffffff) gives a zero row.
