@@ -57,8 +57,12 @@ def parse():
 # Workloads
 # --------------------------------------------------------------------------- #
 class Op:
-    def __init__(self, name, nbytes, fn):
-        self.name, self.nbytes, self.fn = name, nbytes, fn
+    """One timed op: algorithmic bytes per launch, the launch, and the
+    streaming pattern of its ceiling probe: (read streams, bytes per stream)
+    moved to one write stream of the same length (None: no probe)."""
+
+    def __init__(self, name, nbytes, fn, probe=None):
+        self.name, self.nbytes, self.fn, self.probe = name, nbytes, fn, probe
 
 
 def c2_ops(torch, ops, dev, n_sets, seed=1):
@@ -106,8 +110,10 @@ def c2_ops(torch, ops, dev, n_sets, seed=1):
     def op_swiglu(s):
         ops.silu_gate(s["gate"], s["up"], out=s["act"])
 
-    chain = [Op("embedding_f16", bytes_emb, op_emb), Op("add_rmsnorm", bytes_norm, op_norm),
-             Op("rope_qk", bytes_rope, op_rope), Op("swiglu", bytes_swiglu, op_swiglu)]
+    chain = [Op("embedding_f16", bytes_emb, op_emb, (1, T * H * e)),
+             Op("add_rmsnorm", bytes_norm, op_norm, (1, 2 * T * H * e)),
+             Op("rope_qk", bytes_rope, op_rope, (1, T * (nq + nkv) * hd * e)),
+             Op("swiglu", bytes_swiglu, op_swiglu, (2, T * I * e))]
     return chain, sets, T
 
 
@@ -644,16 +650,21 @@ class DeviceEvent:
             pass
 
 
-def run_chain(torch, chain, sets, steps, warmup):
-    """Two timed passes over `steps` steps of the chain.
+def run_chain(torch, chain, sets, steps, warmup, reps=None):
+    """Two timed passes.
 
-    Pass 1 (whole job): no instrumentation, wall clock between two device
-    synchronisations -> elapsed seconds.  Pass 2 (per op): a HIP event pair
-    (device-scope release) around every launch on the launch stream ->
-    per-op kernel times.  Event records between launches cost ~1-3 us each,
-    so they stay out of pass 1.
+    Pass 1 (whole job): `steps` steps of the chain with no instrumentation,
+    wall clock between two device synchronisations -> elapsed seconds.
+    Pass 2 (per op): `reps` (>= 50) more steps of the chain in the same order
+    and input rotation, every op armed with its own event pair through
+    fellm_rocm_timing_arm: the events are attached to the op's kernels
+    (hipExtLaunchKernel), so each pair measures the kernels' device time with
+    nothing inserted between launches.  Per-op time = median over the reps.
     """
-    stream = torch.cuda.current_stream()
+    from fellm_amd import _lib
+
+    lib = _lib.lib()
+    reps = max(steps, 50) if reps is None else reps
     for i in range(warmup):
         for op in chain:
             op.fn(sets[i % len(sets)])
@@ -665,51 +676,146 @@ def run_chain(torch, chain, sets, steps, warmup):
             op.fn(s)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    ev = [[(DeviceEvent(), DeviceEvent()) for _ in chain]
-          for _ in range(steps)]
-    for i in range(steps):
+    ev = [[(DeviceEvent(), DeviceEvent()) for _ in chain] for _ in range(reps)]
+    for i in range(reps):
         s = sets[i % len(sets)]
         for j, op in enumerate(chain):
-            ev[i][j][0].record(stream)
-            op.fn(s)
-            ev[i][j][1].record(stream)
+            a, b = ev[i][j]
+            if lib.fellm_rocm_timing_arm(a.h, b.h) != 0:
+                raise RuntimeError("fellm_rocm_timing_arm failed")
+            try:
+                op.fn(s)
+            finally:
+                lib.fellm_rocm_timing_disarm()
     torch.cuda.synchronize()
     per_op = []
     for j, op in enumerate(chain):
-        ms = sorted(ev[i][j][0].elapsed_time(ev[i][j][1]) for i in range(steps))
+        ms = sorted(ev[i][j][0].elapsed_time(ev[i][j][1]) for i in range(reps))
         per_op.append({"op": op.name, "bytes": op.nbytes, "ms_median": ms[len(ms) // 2],
-                       "ms_mean": sum(ms) / len(ms)})
+                       "ms_mean": sum(ms) / len(ms), "ms_min": ms[0], "reps": reps})
     return (t1 - t0), per_op
 
 
+PROBE_VARIANTS = {0: "U1", 2: "U2", 3: "U4", 4: "U1 nt", 6: "U2 nt", 7: "U4 nt"}
+
+
+def measure_ceilings(torch, chain, reps, min_rotation_bytes=768 << 20):
+    """Same-run copy ceiling of each op: fellm_rocm_stream_probe moving the
+    op's read and write bytes (its `probe` pattern) with no arithmetic, every
+    variant (16-byte units per thread 1/2/4, regular or non-temporal), each
+    timed like the ops (kernel-attached events, median of `reps`), buffers
+    rotating over enough sets (>= 3, together >= min_rotation_bytes, three
+    times the 256 MB MALL) that no launch finds its inputs cached.  The
+    ceiling is the fastest variant."""
+    from fellm_amd import _lib
+
+    lib = _lib.lib()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    out = {}
+    for op in chain:
+        if op.probe is None:
+            continue
+        nr, length = op.probe
+        n_sets = max(3, -(-min_rotation_bytes // ((nr + 1) * length)))
+        bufs = [[torch.empty(length, dtype=torch.uint8, device=dev) for _ in range(nr + 1)] for _ in range(n_sets)]
+        for b in bufs:
+            for t in b[:nr]:
+                t.random_(0, 255)
+        best = None
+        for var, vname in PROBE_VARIANTS.items():
+            ev = [(DeviceEvent(), DeviceEvent()) for _ in range(reps)]
+            for i in range(reps + 3):
+                b = bufs[i % n_sets]
+                args = (b[0].data_ptr(), b[1].data_ptr() if nr == 2 else None, b[nr].data_ptr(), length, var,
+                        stream.cuda_stream)
+                if i < 3:
+                    lib.fellm_rocm_stream_probe(*args)
+                    continue
+                e0, e1 = ev[i - 3]
+                lib.fellm_rocm_timing_arm(e0.h, e1.h)
+                try:
+                    if lib.fellm_rocm_stream_probe(*args) != 0:
+                        raise RuntimeError("stream probe failed")
+                finally:
+                    lib.fellm_rocm_timing_disarm()
+            torch.cuda.synchronize()
+            ms = sorted(a.elapsed_time(b) for a, b in ev)[reps // 2]
+            if best is None or ms < best[0]:
+                best = (ms, vname)
+        moved = (nr + 1) * length
+        out[op.name] = {"probe_bytes": moved, "probe_us": round(best[0] * 1e3, 2), "probe_variant": best[1],
+                        "probe_GBps": round(moved / (best[0] * 1e-3) / 1e9, 1),
+                        "probe_frac_of_peak": round(moved / (best[0] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        del bufs
+    return out
+
+
 def op_report(per_op):
+    """Per-op GB/s from the median kernel time (algorithmic bytes / time)."""
     out = {}
     for r in per_op:
-        gbps = r["bytes"] / (r["ms_mean"] * 1e-3) / 1e9
-        out[r["op"]] = {"bytes": r["bytes"], "us_mean": round(r["ms_mean"] * 1e3, 2),
-                        "us_median": round(r["ms_median"] * 1e3, 2), "GBps": round(gbps, 1),
-                        "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4)}
+        gbps = r["bytes"] / (r["ms_median"] * 1e-3) / 1e9
+        out[r["op"]] = {"bytes": r["bytes"], "us_median": round(r["ms_median"] * 1e3, 2),
+                        "us_mean": round(r["ms_mean"] * 1e3, 2), "us_min": round(r["ms_min"] * 1e3, 2),
+                        "reps": r["reps"], "GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4)}
     return out
 
 
 # --------------------------------------------------------------------------- #
 # CPU baseline: the oracle (C restatement of backend-cpu), 1 thread
 # --------------------------------------------------------------------------- #
-def cpu_baseline(budget_s: float, threads: int = 1):
-    """The oracle's f32 restatement of the c2 chain on 64-token samples, timed
-    on this host.  threads > 1: that many workers each run their own samples
-    concurrently (the C oracle releases the GIL), i.e. rows spread over cores;
-    the reference's own launchers are serial, so threads = 1 is the faithful
-    figure."""
+def host_cpu_info(flags: str) -> dict:
+    """CPU model, logical CPUs available to this process, and the vector ISA
+    the -march=native build targets (from gcc's resolved target options)."""
+    import re
+    import subprocess
+
+    info = {"cpu": platform.processor() or "unknown", "host_logical_cpus": len(os.sched_getaffinity(0))}
+    try:
+        cpuinfo = Path("/proc/cpuinfo").read_text()
+        info["cpu"] = next((l.split(":", 1)[1].strip() for l in cpuinfo.splitlines() if l.startswith("model name")),
+                           info["cpu"])
+    except OSError:
+        pass
+    try:
+        q = subprocess.run(["gcc", *flags.split(), "-Q", "--help=target"], capture_output=True, text=True,
+                           check=True).stdout
+        enabled = set(re.findall(r"^\s+-m(\S+)\s+\[enabled\]", q, re.M))
+        march = re.search(r"^\s+-march=\s+(\S+)", q, re.M)
+        isa = "AVX-512" if "avx512f" in enabled else ("AVX2" if "avx2" in enabled else "SSE2")
+        info["isa"] = (f"{isa} (gcc {' '.join(flags.split()[1:3])} resolved to -march={march.group(1) if march else '?'}"
+                       f"; fma {'on' if 'fma' in enabled else 'off'}, f16c {'on' if 'f16c' in enabled else 'off'})")
+    except (OSError, subprocess.CalledProcessError):
+        info["isa"] = "unknown"
+    return info
+
+
+def cpu_baseline(budget_s: float, threads: int = 1, _native=None):
+    """CPU baseline: the oracle's restatement of backend-cpu's c2 chain
+    (f32 ops, as the CPU backend computes them) on 64-token samples, compiled
+    for this host with -march=native the way the reference is built
+    (.cargo/config.toml:1-7): RMSNorm's sum of squares in 8-lane f32
+    vectors (norm.rs:12-19), add at the widest width, silu/RoPE through
+    libm expf/sinf/cosf, scalar as in the reference.  threads > 1: that many
+    workers each run their own samples concurrently (the C code releases the
+    GIL), i.e. rows spread over cores; the reference's own launchers are
+    serial, so threads = 1 is the faithful figure."""
+    import tempfile
+
     import numpy as np
 
     import oracle
 
+    if _native is None:
+        path, flags = oracle.build_native(Path(tempfile.mkdtemp(prefix="oracle_native_")))
+        oracle.use_library(path)
+        _native = flags
     if threads > 1:
         from concurrent.futures import ThreadPoolExecutor
 
         with ThreadPoolExecutor(max_workers=threads) as ex:
-            parts = list(ex.map(lambda _: cpu_baseline(budget_s, 1), range(threads)))
+            parts = list(ex.map(lambda _: cpu_baseline(budget_s, 1, _native), range(threads)))
         out = dict(parts[0])
         out["value"] = round(sum(p["value"] for p in parts), 1)
         out["cores"] = threads
@@ -732,7 +838,6 @@ def cpu_baseline(budget_s: float, threads: int = 1):
     pos = np.arange(T, dtype=np.uint32)
     gt = rng.normal(size=(T, I)).astype(np.float32)
     up = rng.normal(size=(T, I)).astype(np.float32)
-    oracle.lib()
     iters, t0 = 0, time.perf_counter()
     while True:
         oracle.embedding(table.view(np.uint8), 1, V, H, ids)
@@ -745,17 +850,13 @@ def cpu_baseline(budget_s: float, threads: int = 1):
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
-    isa = "unknown"
-    try:
-        flags = Path("/proc/cpuinfo").read_text()
-        isa = "AVX-512" if "avx512f" in flags else ("AVX2" if "avx2" in flags else "SSE")
-        model = next((l.split(":", 1)[1].strip() for l in flags.splitlines() if l.startswith("model name")), "")
-    except OSError:
-        model = platform.processor()
-    return {"value": round(T * iters / el, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{iters} x 64-token c2 chain (embedding f16->f32, add, rmsnorm, rope q+k, swiglu) in "
-                      f"{el:.1f}s, f32 ops as backend-cpu, 1 thread",
-            "cpu": model, "isa": isa}
+    out = {"value": round(T * iters / el, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+           "sample": f"{iters} x 64-token c2 chain (embedding f16->f32, add, rmsnorm, rope q+k, swiglu) in "
+                     f"{el:.1f}s, f32 ops as backend-cpu, 1 thread",
+           "code": "oracle/fellm_oracle.c, a C restatement of backend-cpu in its operation order, "
+                   f"compiled on this host: gcc {_native}"}
+    out.update(host_cpu_info(_native))
+    return out
 
 
 # --------------------------------------------------------------------------- #
@@ -811,10 +912,16 @@ def main():
     chain, sets, T = c2_ops(torch, ops, dev, args.sets)
     elapsed, per_op = run_chain(torch, chain, sets, args.steps, args.warmup)
     rep = op_report(per_op)
+    del sets
+    torch.cuda.empty_cache()
+    ceilings = measure_ceilings(torch, chain, max(args.steps, 50))
+    for name, c in ceilings.items():
+        rep[name].update(c)
+        rep[name]["frac_of_probe"] = round(rep[name]["GBps"] / c["probe_GBps"], 4)
     ms_step = elapsed / args.steps * 1e3
-    kernel_sum_ms = sum(r["ms_mean"] for r in per_op)
+    kernel_sum_ms = sum(r["ms_median"] for r in per_op)
     dom = max(per_op, key=lambda r: r["bytes"])
-    achieved = dom["bytes"] / (dom["ms_mean"] * 1e-3) / 1e9
+    achieved = dom["bytes"] / (dom["ms_median"] * 1e-3) / 1e9
     traffic = read_traffic()
     line = {
         "metric": METRIC,
@@ -834,7 +941,13 @@ def main():
                    "rotating_input_sets": args.sets},
         "roofline": {"bound": "hbm", "kernel": dom["op"], "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic},
+                     "traffic": traffic,
+                     "traffic_source": "committed constant, not measured in this run: HBM bytes per SwiGLU "
+                                       "launch from profiles/swiglu_c2_pmc_traffic.txt (rocprofv3 --pmc "
+                                       "FETCH_SIZE and WRITE_SIZE, calibrated on a plain device copy)",
+                     "time_source": "median of the per-op pass's kernel-attached HIP events "
+                                    "(fellm_rocm_timing_arm)",
+                     "same_run_probe_frac": rep[dom["op"]].get("frac_of_probe")},
         "ops": rep,
         "chain_tokens_per_s_kernel_sum": round(T / (kernel_sum_ms * 1e-3), 1),
         "chain_GBps_kernel_sum": round(sum(r["bytes"] for r in per_op) / (kernel_sum_ms * 1e-3) / 1e9, 1),

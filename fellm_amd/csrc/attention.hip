@@ -487,16 +487,16 @@ int launch_decode(const void *q, void *out, uint32_t batch, uint32_t n_heads, ui
     // Two blocks in flight pay off on long walks (256 sequences x 4096 keys:
     // 754 -> 720 us); splits of a few blocks do better with one.
     if (bps >= kDeepWalk)
-        hipLaunchKernelGGL((paged_decode_kernel<Q, O, C, HD, GM, 2>), dim3(batch * n_kv * splits), dim3(kWave), 0,
+        FELLM_LAUNCH((paged_decode_kernel<Q, O, C, HD, GM, 2>), dim3(batch * n_kv * splits), dim3(kWave), 0,
                            st, static_cast<const typename Q::T *>(q), static_cast<typename O::T *>(out), ws, lens,
                            geo.table, geo, n_heads, n_kv, scale, causal, window, splits, bps);
     else
-        hipLaunchKernelGGL((paged_decode_kernel<Q, O, C, HD, GM, 1>), dim3(batch * n_kv * splits), dim3(kWave), 0,
+        FELLM_LAUNCH((paged_decode_kernel<Q, O, C, HD, GM, 1>), dim3(batch * n_kv * splits), dim3(kWave), 0,
                            st, static_cast<const typename Q::T *>(q), static_cast<typename O::T *>(out), ws, lens,
                            geo.table, geo, n_heads, n_kv, scale, causal, window, splits, bps > 0 ? bps : 1);
     int rc = launch_status();
     if (rc != FELLM_OK || splits == 1) return rc;
-    hipLaunchKernelGGL((paged_decode_combine<O, HD, GM>), dim3(batch * n_heads), dim3(kCombineThreads), 0, st, ws,
+    FELLM_LAUNCH((paged_decode_combine<O, HD, GM>), dim3(batch * n_heads), dim3(kCombineThreads), 0, st, ws,
                        static_cast<typename O::T *>(out), n_heads, n_kv, splits);
     return launch_status();
 }

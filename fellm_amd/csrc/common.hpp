@@ -2,6 +2,7 @@
 // reductions, bit-exact glibc expf, launch bookkeeping.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
@@ -121,6 +122,30 @@ __device__ __forceinline__ void load_f32_nt(const typename A::T *p, float (&out)
 #pragma unroll
         for (int i = 0; i < N; ++i) out[i] = A::load(pk.v[i]);
     }
+}
+
+// Raw N-element packs with non-temporal access (N * sizeof(T) a multiple of 4).
+template <typename T, int N>
+__device__ __forceinline__ Pack<T, N> load_pack_nt(const T *p) {
+    using P = Pack<T, N>;
+    constexpr int W = sizeof(P) / 4;
+    uint32_t w[W];
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(p);
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = __builtin_nontemporal_load(src + i);
+    P pk;
+    memcpy(&pk, w, sizeof(P));
+    return pk;
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_pack_nt(T *p, const Pack<T, N> &pk) {
+    constexpr int W = sizeof(Pack<T, N>) / 4;
+    uint32_t w[W];
+    memcpy(w, &pk, sizeof(w));
+    uint32_t *dst = reinterpret_cast<uint32_t *>(p);
+#pragma unroll
+    for (int i = 0; i < W; ++i) __builtin_nontemporal_store(w[i], dst + i);
 }
 
 template <typename A, int N>
@@ -468,6 +493,31 @@ __device__ __forceinline__ const uint64_t *stage_expf_table(uint64_t *lds) {
 // ---------------------------------------------------------------------------
 // Host helpers.
 // ---------------------------------------------------------------------------
+// Kernel timing for measurement.  fellm_rocm_timing_arm(start, stop) arms the
+// calling thread: until fellm_rocm_timing_disarm(), the first kernel this
+// library launches records `start` at its beginning and every kernel records
+// `stop` at its end (hipExtLaunchKernel attaches the events to the kernel
+// itself, so no marker packet runs between kernels).  The elapsed time of
+// the pair is then the device time of the op's kernels, as a profiler's
+// kernel trace reports it.  Unarmed launches are plain hipLaunchKernelGGL.
+struct LaunchTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool armed = false, started = false;
+};
+inline thread_local LaunchTiming g_launch_timing;
+
+#define FELLM_LAUNCH(kernel, grid, block, lds, stream, ...)                                                   \
+    do {                                                                                                     \
+        ::fellm::LaunchTiming &lt_ = ::fellm::g_launch_timing;                                               \
+        if (lt_.armed) {                                                                                     \
+            hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, lt_.started ? nullptr : lt_.start, lt_.stop, \
+                                  0, __VA_ARGS__);                                                           \
+            lt_.started = true;                                                                              \
+        } else {                                                                                             \
+            hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                               \
+        }                                                                                                    \
+    } while (0)
+
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline int launch_status() {

@@ -128,6 +128,39 @@ __global__ __launch_bounds__(kEwBlock) void expf_kernel(const float *__restrict_
         out[i] = expf_glibc(in[i], tab);
 }
 
+// Streaming probe: out = a (1 read stream) or a ^ b (2 read streams), n
+// 16-byte units, U units per thread in one pass (all loads issued before the
+// stores), non-temporal or regular accesses.  No arithmetic: the speed of
+// moving the same read and write bytes as an op, the ceiling the op is
+// measured against.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NR, int U, bool NT>
+__global__ __launch_bounds__(kEwBlock) void stream_probe_kernel(const u32x4 *__restrict__ a,
+                                                                const u32x4 *__restrict__ b,
+                                                                u32x4 *__restrict__ out, uint64_t n) {
+    const uint64_t base = (uint64_t)blockIdx.x * kEwBlock * U + threadIdx.x;
+    u32x4 v[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint64_t i = base + (uint64_t)k * kEwBlock;
+        if (i < n) {
+            v[k] = NT ? __builtin_nontemporal_load(a + i) : a[i];
+            if constexpr (NR == 2) v[k] ^= NT ? __builtin_nontemporal_load(b + i) : b[i];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint64_t i = base + (uint64_t)k * kEwBlock;
+        if (i < n) {
+            if (NT)
+                __builtin_nontemporal_store(v[k], out + i);
+            else
+                out[i] = v[k];
+        }
+    }
+}
+
 __global__ __launch_bounds__(kEwBlock) void sincosf_kernel(const float *__restrict__ in, float *__restrict__ sin_out,
                                                            float *__restrict__ cos_out, uint64_t n) {
     const uint64_t stride = (uint64_t)gridDim.x * kEwBlock;
@@ -170,7 +203,7 @@ int launch_silu(const void *g, const void *u, void *out, uint64_t n, hipStream_t
     using TO = typename O::T;
     if (!aligned_to(g, sizeof(TI) * VEC) || !aligned_to(u, sizeof(TI) * VEC) ||
         !aligned_to(out, sizeof(TO) * VEC)) {
-        hipLaunchKernelGGL((silu_gate_kernel<I, O, 1, 1>), dim3(ew_grid(n)), dim3(kEwBlock), 0, s,
+        FELLM_LAUNCH((silu_gate_kernel<I, O, 1, 1>), dim3(ew_grid(n)), dim3(kEwBlock), 0, s,
                            (const TI *)g, (const TI *)u, (TO *)out, n);
         return launch_status();
     }
@@ -179,7 +212,7 @@ int launch_silu(const void *g, const void *u, void *out, uint64_t n, hipStream_t
     uint64_t blocks = (units + kEwBlock * UNROLL - 1) / (kEwBlock * UNROLL);
     if (blocks == 0) blocks = 1;
     if (blocks > 0x7fffffffull) blocks = 0x7fffffffull;
-    hipLaunchKernelGGL((silu_gate_kernel<I, O, VEC, UNROLL>), dim3((uint32_t)blocks), dim3(kEwBlock), 0, s,
+    FELLM_LAUNCH((silu_gate_kernel<I, O, VEC, UNROLL>), dim3((uint32_t)blocks), dim3(kEwBlock), 0, s,
                        (const TI *)g, (const TI *)u, (TO *)out, n);
     return launch_status();
 }
@@ -191,11 +224,11 @@ int launch_add(const void *a, const void *b, void *out, uint64_t n, hipStream_t 
     using TO = typename O::T;
     if (!aligned_to(a, sizeof(TI) * VEC) || !aligned_to(b, sizeof(TI) * VEC) ||
         !aligned_to(out, sizeof(TO) * VEC)) {
-        hipLaunchKernelGGL((add_kernel<I, O, 1>), dim3(ew_grid(n)), dim3(kEwBlock), 0, s,
+        FELLM_LAUNCH((add_kernel<I, O, 1>), dim3(ew_grid(n)), dim3(kEwBlock), 0, s,
                            (const TI *)a, (const TI *)b, (TO *)out, n);
         return launch_status();
     }
-    hipLaunchKernelGGL((add_kernel<I, O, VEC>), dim3(ew_grid(n / VEC)), dim3(kEwBlock), 0, s,
+    FELLM_LAUNCH((add_kernel<I, O, VEC>), dim3(ew_grid(n / VEC)), dim3(kEwBlock), 0, s,
                        (const TI *)a, (const TI *)b, (TO *)out, n);
     return launch_status();
 }
@@ -229,11 +262,50 @@ extern "C" int fellm_rocm_add(const void *a, const void *b, uint32_t in_dtype, v
     });
 }
 
+extern "C" int fellm_rocm_stream_probe(const void *a, const void *b, void *out, uint64_t bytes, uint32_t variant,
+                                       void *stream) {
+    using namespace fellm;
+    if (bytes == 0) return FELLM_OK;
+    if (!a || !out || bytes % 16 || !aligned_to(a, 16) || !aligned_to(out, 16) || (b && !aligned_to(b, 16)))
+        return FELLM_ERR_SHAPE;
+    const uint64_t n = bytes / 16;
+    hipStream_t s = as_stream(stream);
+    const int u = variant & 3 ? 1 << (variant & 3) >> 1 : 1;  // variant bits 0-1: U = 1, 1, 2, 4
+    const bool nt = (variant & 4) != 0;
+    auto go = [&]<int U>() -> int {
+        const uint64_t blocks = (n + (uint64_t)kEwBlock * U - 1) / ((uint64_t)kEwBlock * U);
+        if (blocks > 0x7fffffffull) return FELLM_ERR_SHAPE;
+        const dim3 grid((uint32_t)blocks);
+        const u32x4 *pa = static_cast<const u32x4 *>(a), *pb = static_cast<const u32x4 *>(b);
+        u32x4 *po = static_cast<u32x4 *>(out);
+        if (b) {
+            if (nt) FELLM_LAUNCH((stream_probe_kernel<2, U, true>), grid, dim3(kEwBlock), 0, s, pa, pb, po, n);
+            else FELLM_LAUNCH((stream_probe_kernel<2, U, false>), grid, dim3(kEwBlock), 0, s, pa, pb, po, n);
+        } else {
+            if (nt) FELLM_LAUNCH((stream_probe_kernel<1, U, true>), grid, dim3(kEwBlock), 0, s, pa, pb, po, n);
+            else FELLM_LAUNCH((stream_probe_kernel<1, U, false>), grid, dim3(kEwBlock), 0, s, pa, pb, po, n);
+        }
+        return launch_status();
+    };
+    if (u == 4) return go.template operator()<4>();
+    if (u == 2) return go.template operator()<2>();
+    return go.template operator()<1>();
+}
+
+extern "C" int fellm_rocm_timing_arm(void *start_event, void *stop_event) {
+    if (!start_event || !stop_event) return FELLM_ERR_ARITY;
+    fellm::g_launch_timing = fellm::LaunchTiming{static_cast<hipEvent_t>(start_event),
+                                                 static_cast<hipEvent_t>(stop_event), true, false};
+    return FELLM_OK;
+}
+
+extern "C" void fellm_rocm_timing_disarm(void) { fellm::g_launch_timing = fellm::LaunchTiming{}; }
+
 extern "C" int fellm_rocm_sincosf(const float *in, float *sin_out, float *cos_out, uint64_t n, void *stream) {
     using namespace fellm;
     if (n == 0) return FELLM_OK;
     if (!in || !sin_out || !cos_out) return FELLM_ERR_ARITY;
-    hipLaunchKernelGGL(sincosf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), in, sin_out, cos_out,
+    FELLM_LAUNCH(sincosf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), in, sin_out, cos_out,
                        n);
     return launch_status();
 }
@@ -242,14 +314,14 @@ extern "C" int fellm_rocm_expf(const float *in, float *out, uint64_t n, void *st
     using namespace fellm;
     if (!in || !out) return FELLM_ERR_ARITY;
     if (n == 0) return FELLM_OK;
-    hipLaunchKernelGGL(expf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), in, out, n);
+    FELLM_LAUNCH(expf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), in, out, n);
     return launch_status();
 }
 
 extern "C" int fellm_rocm_silu_fast_bound(uint32_t *max_dist, void *stream) {
     using namespace fellm;
     if (!max_dist) return FELLM_ERR_ARITY;
-    hipLaunchKernelGGL(silu_fast_bound_kernel, dim3(256 * 16), dim3(kEwBlock), 0, as_stream(stream), max_dist);
+    FELLM_LAUNCH(silu_fast_bound_kernel, dim3(256 * 16), dim3(kEwBlock), 0, as_stream(stream), max_dist);
     return launch_status();
 }
 

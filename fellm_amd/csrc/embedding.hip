@@ -41,6 +41,18 @@
 #ifndef FELLM_EMB_LOOP
 #define FELLM_EMB_LOOP 1
 #endif
+// Build knob: token rows per workgroup of the plain dense gather (0: one row
+// per workgroup through embedding_kernel) and of the plain quantized gather.
+#ifndef FELLM_EMB_TPW
+#define FELLM_EMB_TPW 0
+#endif
+#ifndef FELLM_EMB_QTPW
+#define FELLM_EMB_QTPW 0
+#endif
+// Build knob: parts per thread held in registers by the multi-row gather.
+#ifndef FELLM_EMB_U
+#define FELLM_EMB_U 4
+#endif
 
 namespace fellm {
 namespace {
@@ -232,6 +244,47 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
     }
 }
 
+// Plain gather of TPW token rows per workgroup: the rows' parts form one
+// list of TPW * parts items; each thread decodes up to U of them (items t,
+// t + block, ...) into registers, every load in flight together, then
+// stores them.  Fewer, longer-lived workgroups than one row each, and the
+// dependent id loads of all TPW rows are issued at once.
+template <typename D, typename O, int U>
+__global__ __launch_bounds__(kEmbBlock) void gather_rows_kernel(
+    const uint8_t *__restrict__ table, uint64_t vocab, uint32_t dim, const uint32_t *__restrict__ ids,
+    uint32_t n_ids, uint32_t tpw, typename O::T *__restrict__ out, uint32_t *__restrict__ err) {
+    const uint32_t parts = D::parts(dim);
+    const uint64_t rb = D::row_bytes(dim);
+    const uint32_t tok0 = blockIdx.x * tpw;
+    const uint32_t ntok = n_ids - tok0 < tpw ? n_ids - tok0 : tpw;
+    const uint32_t items = ntok * parts;
+    for (uint32_t i0 = 0; i0 < items; i0 += U * kEmbBlock) {
+        float v[U][D::OUT];
+        uint32_t tk[U], pp[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t it = i0 + u * kEmbBlock + threadIdx.x;
+            tk[u] = it / parts;
+            pp[u] = it - tk[u] * parts;
+            if (it < items) {
+                const uint32_t id = ids[tok0 + tk[u]];
+                const bool bad = id >= vocab;
+                D::decode(table + (bad ? 0 : (uint64_t)id * rb), pp[u], v[u]);
+                if (bad) {
+                    if (err) atomicOr(err, 1u);
+#pragma unroll
+                    for (int k = 0; k < D::OUT; ++k) v[u][k] = 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t it = i0 + u * kEmbBlock + threadIdx.x;
+            if (it < items) store_part<D, O, true>(out + (size_t)(tok0 + tk[u]) * dim, pp[u], v[u]);
+        }
+    }
+}
+
 template <typename D, typename O>
 int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids,
                void *h, void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
@@ -241,13 +294,21 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
     const uint32_t chunks = (D::parts(dim) + kEmbBlock - 1) / kEmbBlock;
 #define FELLM_EMB(C, NORM)                                                                          \
     if (chunks <= C) {                                                                              \
-        hipLaunchKernelGGL((embedding_kernel<D, O, C, NORM>), grid, block, 0, s, tb, vocab, dim, ids,  \
+        FELLM_LAUNCH((embedding_kernel<D, O, C, NORM>), grid, block, 0, s, tb, vocab, dim, ids,  \
                            (TO *)h, (TO *)y, w, eps, err);                                          \
         return launch_status();                                                                     \
     }
     if (!w) {
+        constexpr bool dense = D::OUT == 8 && D::RUNS == 1;
+        constexpr uint32_t tpw = dense ? FELLM_EMB_TPW : FELLM_EMB_QTPW;
+        if (tpw > 0 && ids) {
+            const uint32_t groups = (n_ids + tpw - 1) / tpw;
+            FELLM_LAUNCH((gather_rows_kernel<D, O, FELLM_EMB_U>), dim3(groups), block, 0, s, tb, vocab, dim, ids,
+                         n_ids, tpw, (TO *)h, err);
+            return launch_status();
+        }
         if (FELLM_EMB_LOOP) {
-            hipLaunchKernelGGL((embedding_kernel<D, O, 0, false>), grid, block, 0, s, tb, vocab, dim, ids, (TO *)h,
+            FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, 0, s, tb, vocab, dim, ids, (TO *)h,
                                nullptr, nullptr, 0.0f, err);
             return launch_status();
         }
@@ -255,7 +316,7 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
         FELLM_EMB(2, false)
         FELLM_EMB(4, false)
         FELLM_EMB(8, false)
-        hipLaunchKernelGGL((embedding_kernel<D, O, 0, false>), grid, block, 0, s, tb, vocab, dim, ids, (TO *)h,
+        FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, 0, s, tb, vocab, dim, ids, (TO *)h,
                            nullptr, nullptr, 0.0f, err);
         return launch_status();
     }

@@ -662,13 +662,13 @@ int launch_gemv(const void *gw, const void *uw, const void *x, float *out, uint3
             uint32_t grid = (n + kGemvWaves * rp - 1) / (kGemvWaves * rp);
             if (grid > max_grid) grid = max_grid;
             const uint32_t lds = gemv_lds_bytes(nb, mats * rp * nbp) + kGemvWaves * kStagePerWave<GW, UW, FUSED>;
-            hipLaunchKernelGGL((kquant_gemv_kernel<GW, UW, FUSED, false, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
+            FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, false, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
                                out + r0, n, nb, rp);
         } else {
             uint32_t grid = (n + kGemvWaves - 1) / kGemvWaves;
             if (grid > max_grid) grid = max_grid;
             const uint32_t lds = gemv_lds_bytes(nb, mats * nbp) + kGemvWaves * kStagePerWave<GW, UW, FUSED>;
-            hipLaunchKernelGGL((kquant_gemv_kernel<GW, UW, FUSED, true, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
+            FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, true, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
                                out + r0, n, nb, 1u);
         }
         const int rc = launch_status();
@@ -678,7 +678,7 @@ int launch_gemv(const void *gw, const void *uw, const void *x, float *out, uint3
         const uint32_t n = rows - rows_main;
         const uint8_t *g = g8 + (uint64_t)rows_main * nb * GW::kBytes;
         const uint8_t *u = FUSED ? u8 + (uint64_t)rows_main * nb * UW::kBytes : nullptr;
-        hipLaunchKernelGGL((kquant_gemv_direct<GW, UW, FUSED, PREQ>), dim3((n + kGemvWaves - 1) / kGemvWaves),
+        FELLM_LAUNCH((kquant_gemv_direct<GW, UW, FUSED, PREQ>), dim3((n + kGemvWaves - 1) / kGemvWaves),
                            dim3(kGemvBlock), gemv_lds_bytes(nb, mats * nbp), s, g, u, x, out + rows_main, n, nb);
         const int rc = launch_status();
         if (rc != FELLM_OK) return rc;
@@ -747,7 +747,7 @@ extern "C" int fellm_rocm_quantize_q8k(const float *x, uint32_t cols, void *xq, 
     if (cols == 0 || cols % 256 != 0 || cols > kGemvMaxCols) return FELLM_ERR_SHAPE;
     if (!aligned_to(x, 16) || !aligned_to(xq, 16)) return FELLM_ERR_SHAPE;
     const uint32_t nb = cols / 256;
-    hipLaunchKernelGGL(quantize_q8k_kernel, dim3((nb + kGemvWaves - 1) / kGemvWaves), dim3(kGemvBlock), 0,
+    FELLM_LAUNCH(quantize_q8k_kernel, dim3((nb + kGemvWaves - 1) / kGemvWaves), dim3(kGemvBlock), 0,
                        as_stream(stream), x, nb, static_cast<uint8_t *>(xq));
     return launch_status();
 }

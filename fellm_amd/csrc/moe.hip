@@ -480,12 +480,12 @@ int dispatch_launch(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32
         if (!bc_ws || bc_bytes < (uint64_t)g.nblocks * E * sizeof(uint32_t)) return FELLM_ERR_SHAPE;
         // Pass 1 writes every one of the nblocks * E counts before pass 2
         // reads them, so the buffer needs no clearing between calls.
-        hipLaunchKernelGGL(moe_count_blocks, dim3(g.nblocks), dim3(kDispatchBlock), (size_t)E * sizeof(uint32_t),
+        FELLM_LAUNCH(moe_count_blocks, dim3(g.nblocks), dim3(kDispatchBlock), (size_t)E * sizeof(uint32_t),
                            st, ids, n, E, g.chunk, bc_ws, err_flag);
         bc = bc_ws;
     }
     const size_t lds = (size_t)(kDispatchWaves + 2) * E * sizeof(uint32_t);
-    hipLaunchKernelGGL(moe_scatter_blocks, dim3(g.nblocks), dim3(kDispatchBlock), lds, st, ids, n, E, bits, g.chunk,
+    FELLM_LAUNCH(moe_scatter_blocks, dim3(g.nblocks), dim3(kDispatchBlock), lds, st, ids, n, E, bits, g.chunk,
                        g.nblocks, bc, counts, offsets, order, inv, err_flag);
     return launch_status();
 }
@@ -558,23 +558,23 @@ extern "C" int fellm_rocm_moe_gather(const void *x, uint32_t elem_bytes, uint64_
         const uint64_t row_vecs = row_bytes / 16;
         const uint32_t grid = grid_cap(tokens, 16384);
         if (row_vecs <= 256)
-            hipLaunchKernelGGL(moe_scatter_rows<1>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x), order,
+            FELLM_LAUNCH(moe_scatter_rows<1>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x), order,
                                inv, tokens, top_k, row_vecs, static_cast<uint4 *>(grouped));
         else
-            hipLaunchKernelGGL(moe_scatter_rows<4>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x), order,
+            FELLM_LAUNCH(moe_scatter_rows<4>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x), order,
                                inv, tokens, top_k, row_vecs, static_cast<uint4 *>(grouped));
         return launch_status();
     }
     const uint32_t grid = grid_cap(n, 8192);
     if (vec16)
-        hipLaunchKernelGGL(moe_gather_rows<uint4>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x),
+        FELLM_LAUNCH(moe_gather_rows<uint4>, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(x),
                            order, n, top_k, row_bytes / 16, static_cast<uint4 *>(grouped));
     else if (row_bytes % 4 == 0 && aligned_to(x, 4) && aligned_to(grouped, 4))
-        hipLaunchKernelGGL(moe_gather_rows<uint32_t>, dim3(grid), dim3(256), 0, st,
+        FELLM_LAUNCH(moe_gather_rows<uint32_t>, dim3(grid), dim3(256), 0, st,
                            static_cast<const uint32_t *>(x), order, n, top_k, row_bytes / 4,
                            static_cast<uint32_t *>(grouped));
     else
-        hipLaunchKernelGGL(moe_gather_rows<uint8_t>, dim3(grid), dim3(256), 0, st, static_cast<const uint8_t *>(x),
+        FELLM_LAUNCH(moe_gather_rows<uint8_t>, dim3(grid), dim3(256), 0, st, static_cast<const uint8_t *>(x),
                            order, n, top_k, row_bytes, static_cast<uint8_t *>(grouped));
     return launch_status();
 }
@@ -592,7 +592,7 @@ extern "C" int fellm_rocm_moe_combine(const float *y0, const float *expert_out, 
     const uint32_t grid = grid_cap(tokens, FELLM_MOE_COMBINE_CAP);
     const bool vec = hidden % 4 == 0 && aligned_to(expert_out, 16) && aligned_to(y, 16) && (!y0 || aligned_to(y0, 16));
 #define FELLM_MOE_COMBINE(ORD, V)                                                                                   \
-    hipLaunchKernelGGL((moe_combine_rows<ORD, V>), dim3(grid), dim3(FELLM_MOE_COMBINE_BLOCK), 0, st, y0, expert_out, ids, weights, inv, \
+    FELLM_LAUNCH((moe_combine_rows<ORD, V>), dim3(grid), dim3(FELLM_MOE_COMBINE_BLOCK), 0, st, y0, expert_out, ids, weights, inv, \
                        tokens, top_k, hidden, n, y)
     if (inv) {
         if (vec)

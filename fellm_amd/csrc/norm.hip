@@ -16,6 +16,15 @@
 #ifndef FELLM_NORM_W_EARLY
 #define FELLM_NORM_W_EARLY 1
 #endif
+// Build knob: rows of at most 8 KB take one wavefront per row (1) instead of
+// one workgroup per row (0) when there are many rows.  Measured on MI355X
+// inside the op chain: 4096 x 4096 f16 add+RMSNorm 28.4 us (wavefront per
+// row) against 25.2 us (workgroup per row), and the RoPE launched after it
+// slowed from 15.6 to 19.5 us; 16384 x 2048 bf16 RMSNorm 26.4 against
+// 27.1-27.6 us.  Off.
+#ifndef FELLM_NORM_WAVE
+#define FELLM_NORM_WAVE 0
+#endif
 
 namespace fellm {
 
@@ -45,18 +54,28 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_kernel(
     const typename A::T *xr = x + row * group;
     float v[NCHUNK][VEC];
     float ss = 0.0f;
+    // Every chunk's x and r are requested before the first h store: h may
+    // alias x or r, so the compiler cannot move a later chunk's loads above
+    // an earlier chunk's store by itself, which would expose one memory
+    // latency per chunk.
+    float rv[ADD ? NCHUNK : 1][VEC];
 #pragma unroll
     for (int c = 0; c < NCHUNK; ++c) {
         const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
         if (base < group) {
             norm_load<A, VEC>(xr + base, v[c]);
+            if constexpr (ADD) norm_load<A, VEC>(r + row * group + base, rv[c]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NCHUNK; ++c) {
+        const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
+        if (base < group) {
             if constexpr (ADD) {
-                float rv[VEC];
-                norm_load<A, VEC>(r + row * group + base, rv);
 #pragma unroll
                 for (int i = 0; i < VEC; ++i) {
                     // h is stored in the activation dtype and normalised as stored.
-                    v[c][i] = A::load(A::store(v[c][i] + rv[i]));
+                    v[c][i] = A::load(A::store(v[c][i] + rv[c][i]));
                 }
                 if constexpr (STORE_H) norm_store<A, VEC, true>(h + row * group + base, v[c]);
             }
@@ -87,6 +106,86 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_kernel(
             norm_store<O, VEC, true>(y + row * group + base, o);
         }
     }
+}
+
+// One wavefront per row, four rows per workgroup, for rows of at most 8 KB
+// (NCH 16-byte chunks per lane, chunk c of the row at lanes' c * 1 KB).  Every
+// lane requests all of its x and r chunks before any arithmetic; the sum of
+// squares is one wavefront reduction (no LDS, no barrier), so a row's stores
+// follow its loads by one reduction and nothing waits on other rows.  x and r
+// stay in registers in storage form, h is rounded in place, and y is formed
+// from it with the weights read per chunk.
+template <typename A, typename O, int NCH, bool ADD, bool STORE_H>
+__global__ __launch_bounds__(256) void add_rmsnorm_wave_kernel(
+    const typename A::T *x, const typename A::T *r, typename A::T *h, const float *__restrict__ w,
+    typename O::T *y, uint32_t group, uint32_t rows, float eps) {
+    using T = typename A::T;
+    constexpr int VEC = 16 / sizeof(T);
+    using P = Pack<T, VEC>;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t row = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+    if (row >= rows) return;  // whole wavefronts only: no block-level barrier follows
+    const size_t off = (size_t)row * group;
+    const uint32_t nvec = group / VEC;
+    P xv[NCH], rv[ADD ? NCH : 1];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t i = c * kWave + lane;
+        if (i < nvec) {
+            xv[c] = load_pack_nt<T, VEC>(x + off + (size_t)i * VEC);
+            if constexpr (ADD) rv[c] = load_pack_nt<T, VEC>(r + off + (size_t)i * VEC);
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t i = c * kWave + lane;
+        if (i < nvec) {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                float hv = A::load(xv[c].v[k]);
+                if constexpr (ADD) {
+                    // h is stored in the activation dtype and normalised as stored.
+                    xv[c].v[k] = A::store(hv + A::load(rv[c].v[k]));
+                    hv = A::load(xv[c].v[k]);
+                }
+                ss += hv * hv;
+            }
+            if constexpr (STORE_H) store_pack_nt<T, VEC>(h + off + (size_t)i * VEC, xv[c]);
+        }
+    }
+    ss = wave_sum(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)group + eps);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t i = c * kWave + lane;
+        if (i < nvec) {
+            float wv[VEC], o[VEC];
+            load_f32<F32, VEC>(w + (size_t)i * VEC, wv);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) o[k] = (A::load(xv[c].v[k]) * scale) * wv[k];
+            store_f32_nt<O, VEC>(y + off + (size_t)i * VEC, o);
+        }
+    }
+}
+
+template <typename A, typename O, int NCH>
+int launch_wave(const void *x, const void *r, void *h, const float *w, void *y, uint32_t group, uint64_t rows,
+                float eps, hipStream_t s) {
+    using TA = typename A::T;
+    using TO = typename O::T;
+    const dim3 grid((uint32_t)((rows + 3) / 4)), block(256);
+    if (r == nullptr) {
+        FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, false, false>), grid, block, 0, s, (const TA *)x, nullptr,
+                     nullptr, w, (TO *)y, group, (uint32_t)rows, eps);
+    } else if (h == nullptr) {
+        FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, true, false>), grid, block, 0, s, (const TA *)x,
+                     (const TA *)r, nullptr, w, (TO *)y, group, (uint32_t)rows, eps);
+    } else {
+        FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, true, true>), grid, block, 0, s, (const TA *)x,
+                     (const TA *)r, (TA *)h, w, (TO *)y, group, (uint32_t)rows, eps);
+    }
+    return launch_status();
 }
 
 // Generic fallback for rows that do not fit the register-resident layout
@@ -128,13 +227,13 @@ int launch_fast(const void *x, const void *r, void *h, const float *w, void *y, 
     using TO = typename O::T;
     dim3 grid((uint32_t)rows), block(BLOCK);
     if (r == nullptr) {
-        hipLaunchKernelGGL((add_rmsnorm_kernel<A, O, BLOCK, VEC, NCHUNK, false, false>), grid, block, 0, s,
+        FELLM_LAUNCH((add_rmsnorm_kernel<A, O, BLOCK, VEC, NCHUNK, false, false>), grid, block, 0, s,
                            (const TA *)x, nullptr, nullptr, w, (TO *)y, group, eps);
     } else if (h == nullptr) {
-        hipLaunchKernelGGL((add_rmsnorm_kernel<A, O, BLOCK, VEC, NCHUNK, true, false>), grid, block, 0, s,
+        FELLM_LAUNCH((add_rmsnorm_kernel<A, O, BLOCK, VEC, NCHUNK, true, false>), grid, block, 0, s,
                            (const TA *)x, (const TA *)r, nullptr, w, (TO *)y, group, eps);
     } else {
-        hipLaunchKernelGGL((add_rmsnorm_kernel<A, O, BLOCK, VEC, NCHUNK, true, true>), grid, block, 0, s,
+        FELLM_LAUNCH((add_rmsnorm_kernel<A, O, BLOCK, VEC, NCHUNK, true, true>), grid, block, 0, s,
                            (const TA *)x, (const TA *)r, (TA *)h, w, (TO *)y, group, eps);
     }
     return launch_status();
@@ -152,6 +251,15 @@ int launch_typed(const void *x, const void *r, void *h, const float *w, void *y,
             if (group <= 1024 * VEC) return launch_fast<A, O, 1024, VEC, 1>(x, r, h, w, y, group, rows, eps, s);
             return launch_fast<A, O, 1024, VEC, 2>(x, r, h, w, y, group, rows, eps, s);
         }
+        // Many rows of at most 8 KB: one wavefront per row.
+        constexpr uint32_t WV = 16 / sizeof(typename A::T);  // elements per 16-byte chunk
+        if (FELLM_NORM_WAVE && group % WV == 0 && group * sizeof(typename A::T) <= 8192) {
+            const uint32_t nch = (group / WV + kWave - 1) / kWave;
+            if (nch <= 1) return launch_wave<A, O, 1>(x, r, h, w, y, group, rows, eps, s);
+            if (nch <= 2) return launch_wave<A, O, 2>(x, r, h, w, y, group, rows, eps, s);
+            if (nch <= 4) return launch_wave<A, O, 4>(x, r, h, w, y, group, rows, eps, s);
+            return launch_wave<A, O, 8>(x, r, h, w, y, group, rows, eps, s);
+        }
         if (group <= 256 * VEC) return launch_fast<A, O, 256, VEC, 1>(x, r, h, w, y, group, rows, eps, s);
         if (group <= 256 * VEC * 2) return launch_fast<A, O, 256, VEC, 2>(x, r, h, w, y, group, rows, eps, s);
         if (group <= 256 * VEC * 4) return launch_fast<A, O, 256, VEC, 4>(x, r, h, w, y, group, rows, eps, s);
@@ -160,10 +268,10 @@ int launch_typed(const void *x, const void *r, void *h, const float *w, void *y,
     using TA = typename A::T;
     using TO = typename O::T;
     if (r == nullptr)
-        hipLaunchKernelGGL((add_rmsnorm_generic<A, O, false>), dim3((uint32_t)rows), dim3(256), 0, s,
+        FELLM_LAUNCH((add_rmsnorm_generic<A, O, false>), dim3((uint32_t)rows), dim3(256), 0, s,
                            (const TA *)x, nullptr, nullptr, w, (TO *)y, group, eps);
     else
-        hipLaunchKernelGGL((add_rmsnorm_generic<A, O, true>), dim3((uint32_t)rows), dim3(256), 0, s,
+        FELLM_LAUNCH((add_rmsnorm_generic<A, O, true>), dim3((uint32_t)rows), dim3(256), 0, s,
                            (const TA *)x, (const TA *)r, (TA *)h, w, (TO *)y, group, eps);
     return launch_status();
 }

@@ -28,7 +28,7 @@
 #endif
 // Build knob: (row, head) slots each thread loads before rotating/storing.
 #ifndef FELLM_ROPE_UNROLL
-#define FELLM_ROPE_UNROLL 1
+#define FELLM_ROPE_UNROLL 3
 #endif
 
 namespace fellm {
@@ -407,7 +407,7 @@ extern "C" int fellm_rocm_rope(const void *x1, void *out1, uint32_t n_heads1, co
         auto go = [&]<int PV, int RR>() {
             const uint32_t groups = (rows + RR - 1) / RR;
             const uint32_t hs = rope_head_split(groups, n_heads1 + (x2 ? n_heads2 : 0));
-            hipLaunchKernelGGL((rope_kernel<A, F16, PV, 0, RR>), dim3(groups * hs), dim3(kRopeBlock), 0, s,
+            FELLM_LAUNCH((rope_kernel<A, F16, PV, 0, RR>), dim3(groups * hs), dim3(kRopeBlock), 0, s,
                                (const T *)x1, (T *)out1, n_heads1, (const T *)x2, (T *)out2, x2 ? n_heads2 : 0,
                                nullptr, rows, head_dim, rope_dim, pairing, inv_freqs, positions, position0, nullptr,
                                KvDev{}, nullptr, hs);
@@ -437,10 +437,10 @@ extern "C" int fellm_rocm_kv_write(const void *rows, uint32_t act_dtype, uint32_
             const bool vec = kv.stride % 8 == 0 && aligned_to(rows, sizeof(T) * 8) && aligned_to(kvp->arena, 16) &&
                              kv.block_bytes % 16 == 0;
             if (vec)
-                hipLaunchKernelGGL((kv_write_kernel<A, C, 8>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)rows,
+                FELLM_LAUNCH((kv_write_kernel<A, C, 8>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)rows,
                                    kv_positions, kv, is_v, err_flag);
             else
-                hipLaunchKernelGGL((kv_write_kernel<A, C, 1>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)rows,
+                FELLM_LAUNCH((kv_write_kernel<A, C, 1>), dim3(batch), dim3(kRopeBlock), 0, s, (const T *)rows,
                                    kv_positions, kv, is_v, err_flag);
             return launch_status();
         });
@@ -471,7 +471,7 @@ extern "C" int fellm_rocm_step_kv_position(const FellmDeviceStepParams *params, 
     using namespace fellm;
     if (!params || !kv_pos) return FELLM_ERR_ARITY;
     if (block_size == 0) return FELLM_ERR_SHAPE;
-    hipLaunchKernelGGL(step_kv_position_kernel, dim3(1), dim3(kWave), 0, as_stream(stream), params, block_size,
+    FELLM_LAUNCH(step_kv_position_kernel, dim3(1), dim3(kWave), 0, as_stream(stream), params, block_size,
                        kv_pos);
     return launch_status();
 }
@@ -498,7 +498,7 @@ extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q
                              aligned_to(kvp->arena, 16) && kv.block_bytes % 16 == 0;
             auto go = [&]<int PV>() {
                 const uint32_t hs = rope_head_split(batch, n_q_heads + 2 * n_kv_heads);
-                hipLaunchKernelGGL((rope_kernel<A, C, PV, 1, 1>), dim3(batch * hs), dim3(kRopeBlock), 0, s,
+                FELLM_LAUNCH((rope_kernel<A, C, PV, 1, 1>), dim3(batch * hs), dim3(kRopeBlock), 0, s,
                                    (const T *)q, (T *)q_out, n_q_heads, (const T *)k, (T *)k_out, n_kv_heads,
                                    (const T *)v, batch, head_dim, rope_dim, pairing, inv_freqs, rope_positions, 0u,
                                    kv_positions, kv, err_flag, hs);

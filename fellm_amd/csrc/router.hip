@@ -236,7 +236,7 @@ extern "C" int fellm_rocm_router_topk(const float *logits, uint32_t tokens, uint
         const dim3 ggrid((tokens + tpb - 1) / tpb);
 #define FELLM_ROUTER_G(GG)                                                                                 \
         if (g == GG) {                                                                                     \
-            hipLaunchKernelGGL((router_topk_grouped<EPL, GG>), ggrid, block, 0, s, logits, tokens, n_experts, k, \
+            FELLM_LAUNCH((router_topk_grouped<EPL, GG>), ggrid, block, 0, s, logits, tokens, n_experts, k, \
                                gating_func, norm_topk_prob, routed_scaling_factor, ids, weights);          \
             return launch_status();                                                                        \
         }

@@ -351,6 +351,29 @@ int fellm_rocm_stream_is_capturing(void *stream);
 int fellm_rocm_expf(const float *in, float *out, uint64_t n, void *stream);
 
 /*
+ * Kernel timing (measurement only; no counterpart in the reference).
+ * fellm_rocm_timing_arm(start, stop) takes two hipEvent_t handles; until
+ * fellm_rocm_timing_disarm() the calling thread's launches through this
+ * library record `start` at the beginning of the first kernel and `stop` at
+ * the end of each kernel (hipExtLaunchKernel), so hipEventElapsedTime(start,
+ * stop) is the device time of the op's kernels without marker packets in
+ * between.  Not for use under graph capture.
+ */
+int fellm_rocm_timing_arm(void *start_event, void *stop_event);
+void fellm_rocm_timing_disarm(void);
+
+/*
+ * Streaming probe (measurement only; no counterpart in the reference):
+ * out = a, or a ^ b when b != NULL, over `bytes` (a multiple of 16, 16-byte
+ * aligned buffers), no arithmetic.  It moves the read and write bytes of an
+ * op with nothing else, the ceiling the bench compares the op against.
+ * variant bits 0-1: units of 16 bytes per thread (0, 1: one; 2: two; 3:
+ * four), bit 2: non-temporal loads and stores.
+ */
+int fellm_rocm_stream_probe(const void *a, const void *b, void *out, uint64_t bytes, uint32_t variant,
+                            void *stream);
+
+/*
  * Self-check of the device sinf/cosf restatement that builds RoPE's per-row
  * (sin, cos) table: sin_out[i] = sinf(in[i]), cos_out[i] = cosf(in[i]).
  * Diagnostic only (no counterpart in the reference).

@@ -27,12 +27,30 @@ def build() -> Path:
     return LIB_PATH
 
 
-def lib() -> C.CDLL:
+def build_native(out_dir: Path) -> tuple[Path, str]:
+    """Compile the restatement for this host (-march=native, as the reference
+    is built) into out_dir; returns (library path, compiler flags)."""
+    out = Path(out_dir) / "liboracle_native.so"
+    subprocess.run(["make", "-s", "-C", str(HERE), "native", f"NATIVE_OUT={out}"], check=True)
+    flags = subprocess.run(["make", "-s", "-C", str(HERE), "native-flags"], check=True, capture_output=True,
+                           text=True).stdout.strip()
+    return out, flags
+
+
+def use_library(path: Path | None) -> None:
+    """Route every wrapper below through the library at `path` (None: the
+    default checker build)."""
+    global _lib
+    _lib = None
+    lib(path)
+
+
+def lib(path: Path | None = None) -> C.CDLL:
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
+        if path is None and not LIB_PATH.exists():
             build()
-        l = C.CDLL(str(LIB_PATH))
+        l = C.CDLL(str(path or LIB_PATH))
         P, S, U32, F = C.c_void_p, C.c_size_t, C.c_uint32, C.c_float
         sigs = {
             "oracle_f16_to_f32": (None, [P, P, S]),

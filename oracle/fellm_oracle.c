@@ -31,7 +31,14 @@
 
 /* ---- dtype edges (a8) ---------------------------------------------------- */
 
-/* half::f16::to_f32: exact IEEE binary16 widening (dequant.rs:29-35). */
+/* half::f16::to_f32: exact IEEE binary16 widening (dequant.rs:29-35).  With
+ * F16C available (a -march=native build on such a host) the hardware
+ * conversion, as the half crate uses under that target feature; both are
+ * exact. */
+#ifdef __F16C__
+#include <immintrin.h>
+static float f16_to_f32(uint16_t h) { return _cvtsh_ss(h); }
+#else
 static float f16_to_f32(uint16_t h) {
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
     const uint32_t exp = (h >> 10) & 0x1fu;
@@ -57,6 +64,7 @@ static float f16_to_f32(uint16_t h) {
     memcpy(&f, &bits, 4);
     return f;
 }
+#endif
 
 /* half::f16::from_f32: IEEE round-to-nearest-even (backend.rs:1645, :1765). */
 static uint16_t f32_to_f16(float f) {

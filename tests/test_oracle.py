@@ -426,3 +426,34 @@ def test_router_k_clamped_and_sigmoid_monotone():
     assert ids.shape == (5, 6)
     for i in range(5):
         assert ids[i].tolist() == sorted(range(6), key=lambda j: (-logits[i, j], j))
+
+
+def test_native_build_matches_checker(tmp_path):
+    """The -march=native build the bench times as the CPU baseline computes the
+    same bits as the checker build (vectorisation without reassociation, and
+    F16C widening, which is exact)."""
+    path, flags = oracle.build_native(tmp_path)
+    assert "-march=native" in flags
+    rng = np.random.default_rng(17)
+    table = rng.normal(0, 0.02, size=(64, 4096)).astype(np.float16)
+    ids = rng.integers(0, 64, size=16, dtype=np.uint32)
+    x = rng.normal(size=(16, 4096)).astype(np.float32)
+    r = (2 * rng.normal(size=(16, 4096))).astype(np.float32)
+    w = rng.normal(1, 0.1, size=4096).astype(np.float32)
+    q = rng.normal(size=(16, 32 * 128)).astype(np.float32)
+    inv = oracle.rope_inv_freqs(500000.0, 128)
+    g = rng.normal(size=(16, 14336)).astype(np.float32)
+
+    def run():
+        return [oracle.embedding(table.view(np.uint8), 1, 64, 4096, ids), oracle.add(x, r),
+                oracle.rmsnorm(x, w, 1e-5), oracle.rope(q, 32, 128, 128, 0, inv, np.arange(16, dtype=np.uint32)),
+                oracle.silu_gate(g, g)]
+
+    ref = run()
+    try:
+        oracle.use_library(path)
+        got = run()
+    finally:
+        oracle.use_library(None)
+    for a, b in zip(got, ref):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
