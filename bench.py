@@ -58,8 +58,8 @@ def parse():
 # --------------------------------------------------------------------------- #
 class Op:
     """One timed op: algorithmic bytes per launch, the launch, and the
-    streaming pattern of its ceiling probe: (read streams, bytes per stream)
-    moved to one write stream of the same length (None: no probe)."""
+    streaming pattern of its ceiling probe: (read streams, bytes read per
+    stream, bytes written) (None: no probe)."""
 
     def __init__(self, name, nbytes, fn, probe=None):
         self.name, self.nbytes, self.fn, self.probe = name, nbytes, fn, probe
@@ -110,10 +110,10 @@ def c2_ops(torch, ops, dev, n_sets, seed=1):
     def op_swiglu(s):
         ops.silu_gate(s["gate"], s["up"], out=s["act"])
 
-    chain = [Op("embedding_f16", bytes_emb, op_emb, (1, T * H * e)),
-             Op("add_rmsnorm", bytes_norm, op_norm, (1, 2 * T * H * e)),
-             Op("rope_qk", bytes_rope, op_rope, (1, T * (nq + nkv) * hd * e)),
-             Op("swiglu", bytes_swiglu, op_swiglu, (2, T * I * e))]
+    chain = [Op("embedding_f16", bytes_emb, op_emb, (1, T * H * e, T * H * e)),
+             Op("add_rmsnorm", bytes_norm, op_norm, (2, T * H * e, 2 * T * H * e)),
+             Op("rope_qk", bytes_rope, op_rope, (1, T * (nq + nkv) * hd * e, T * (nq + nkv) * hd * e)),
+             Op("swiglu", bytes_swiglu, op_swiglu, (2, T * I * e, T * I * e))]
     return chain, sets, T
 
 
@@ -134,12 +134,12 @@ def c3_ops(torch, ops, dev, n_sets, seed=3):
     out_b = T * D * 2
     chain = [
         Op("q4k_gather", T * 2016 + out_b + T * 4, lambda s: ops.embedding(q4, s["ids"], dim=D, qtype="q4k",
-                                                                           out=s["out"])),
+                                                                           out=s["out"]), (1, T * 2016, out_b)),
         Op("q6k_gather", T * 2940 + out_b + T * 4, lambda s: ops.embedding(q6, s["ids"], dim=D, qtype="q6k",
-                                                                           out=s["out"])),
+                                                                           out=s["out"]), (1, T * 2940, out_b)),
         Op("q4k_gather_rmsnorm", T * 2016 + 2 * out_b + T * 4,
            lambda s: ops.embedding_rmsnorm(q4, s["ids"], w, 1e-6, dim=D, qtype="q4k", h_out=s["out"],
-                                           y_out=s["y"])),
+                                           y_out=s["y"]), (1, T * 2016, 2 * out_b)),
     ]
     return chain, sets, T
 
@@ -182,10 +182,10 @@ def c4_ops(torch, ops, dev, n_sets, seed=4):
     chain = [
         Op("rope_kv_write", B * (nq * hd * 2 + 2 * stride) * 2 + B * 2 * stride * 2 + B * 4,
            lambda s: ops.rope_kv_write(s["q"], s["k"], s["v"], inv, s["pos"], s["cache"], head_dim=hd,
-                                       q_out=s["qo"])),
+                                       q_out=s["qo"]), (1, B * (nq * hd + 2 * stride) * 2, B * (nq * hd + 2 * stride) * 2)),
         Op("add_rmsnorm", B * H * 2 * 4, lambda s: ops.add_rmsnorm(s["x"], s["r"], w, 1e-5, h_out=s["h"],
-                                                                   y_out=s["y"])),
-        Op("swiglu", B * I * 2 * 3, lambda s: ops.silu_gate(s["gate"], s["up"], out=s["act"])),
+                                                                   y_out=s["y"]), (2, B * H * 2, 2 * B * H * 2)),
+        Op("swiglu", B * I * 2 * 3, lambda s: ops.silu_gate(s["gate"], s["up"], out=s["act"]), (2, B * I * 2, B * I * 2)),
     ]
     return chain, sets, B
 
@@ -218,11 +218,13 @@ def c5_ops(torch, ops, dev, n_sets, seed=5):
         })
     chain = [
         Op("router_topk", T * E * 4 + T * K * 8, lambda s: ops.router_topk(s["logits"], K, ids=s["ids"],
-                                                                          weights=s["wts"])),
-        Op("swiglu_routed", T * K * Iexp * 2 * 3, lambda s: ops.silu_gate(s["gate"], s["up"], out=s["act"])),
-        Op("rmsnorm", T * H * 2 * 2, lambda s: ops.rmsnorm(s["x"], w, 1e-6, out=s["y"])),
+                                                                          weights=s["wts"]), (1, T * E * 4, T * K * 8)),
+        Op("swiglu_routed", T * K * Iexp * 2 * 3, lambda s: ops.silu_gate(s["gate"], s["up"], out=s["act"]),
+           (2, T * K * Iexp * 2, T * K * Iexp * 2)),
+        Op("rmsnorm", T * H * 2 * 2, lambda s: ops.rmsnorm(s["x"], w, 1e-6, out=s["y"]), (1, T * H * 2, T * H * 2)),
         Op("rope_qk", T * (nq + nkv) * hd * 2 * 2 + T * 4,
-           lambda s: ops.rope(s["q"], inv, head_dim=hd, positions=pos, x2=s["k"], out1=s["qo"], out2=s["ko"])),
+           lambda s: ops.rope(s["q"], inv, head_dim=hd, positions=pos, x2=s["k"], out1=s["qo"], out2=s["ko"]),
+           (1, T * (nq + nkv) * hd * 2, T * (nq + nkv) * hd * 2)),
     ]
     return chain, sets, T
 
@@ -716,9 +718,11 @@ def measure_ceilings(torch, chain, reps, min_rotation_bytes=768 << 20):
     for op in chain:
         if op.probe is None:
             continue
-        nr, length = op.probe
-        n_sets = max(3, -(-min_rotation_bytes // ((nr + 1) * length)))
-        bufs = [[torch.empty(length, dtype=torch.uint8, device=dev) for _ in range(nr + 1)] for _ in range(n_sets)]
+        nr, rlen, wlen = op.probe
+        moved = nr * rlen + wlen
+        n_sets = max(3, -(-min_rotation_bytes // moved))
+        bufs = [[torch.empty(rlen, dtype=torch.uint8, device=dev) for _ in range(nr)] +
+                [torch.empty(wlen, dtype=torch.uint8, device=dev)] for _ in range(n_sets)]
         for b in bufs:
             for t in b[:nr]:
                 t.random_(0, 255)
@@ -727,7 +731,7 @@ def measure_ceilings(torch, chain, reps, min_rotation_bytes=768 << 20):
             ev = [(DeviceEvent(), DeviceEvent()) for _ in range(reps)]
             for i in range(reps + 3):
                 b = bufs[i % n_sets]
-                args = (b[0].data_ptr(), b[1].data_ptr() if nr == 2 else None, b[nr].data_ptr(), length, var,
+                args = (b[0].data_ptr(), b[1].data_ptr() if nr == 2 else None, rlen, b[nr].data_ptr(), wlen, var,
                         stream.cuda_stream)
                 if i < 3:
                     lib.fellm_rocm_stream_probe(*args)
@@ -743,7 +747,6 @@ def measure_ceilings(torch, chain, reps, min_rotation_bytes=768 << 20):
             ms = sorted(a.elapsed_time(b) for a, b in ev)[reps // 2]
             if best is None or ms < best[0]:
                 best = (ms, vname)
-        moved = (nr + 1) * length
         out[op.name] = {"probe_bytes": moved, "probe_us": round(best[0] * 1e3, 2), "probe_variant": best[1],
                         "probe_GBps": round(moved / (best[0] * 1e-3) / 1e9, 1),
                         "probe_frac_of_peak": round(moved / (best[0] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
@@ -902,7 +905,12 @@ def main():
             chain, sets, _ = make(torch, ops, dev, args.sets)
             _, per_op = run_chain(torch, chain, sets, args.steps, args.warmup)
             result[name] = op_report(per_op)
-            del chain, sets
+            del sets
+            torch.cuda.empty_cache()
+            for op_name, c in measure_ceilings(torch, chain, max(args.steps, 50)).items():
+                result[name][op_name].update(c)
+                result[name][op_name]["frac_of_probe"] = round(result[name][op_name]["GBps"] / c["probe_GBps"], 4)
+            del chain
             torch.cuda.empty_cache()
         if not args.only or "next_graph" in args.only.split(","):
             result["next_graph"] = decode_graph_report(torch, ops, dev, max(args.steps, 50), args.warmup)

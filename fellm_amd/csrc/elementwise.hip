@@ -128,23 +128,25 @@ __global__ __launch_bounds__(kEwBlock) void expf_kernel(const float *__restrict_
         out[i] = expf_glibc(in[i], tab);
 }
 
-// Streaming probe: out = a (1 read stream) or a ^ b (2 read streams), n
-// 16-byte units, U units per thread in one pass (all loads issued before the
-// stores), non-temporal or regular accesses.  No arithmetic: the speed of
-// moving the same read and write bytes as an op, the ceiling the op is
+// Streaming probe: reads nr units of 16 bytes from a (and b), writes nw
+// units to out (out[i] = a[i] ^ b[i] where both exist, else whatever was
+// read or a constant), U units per thread in one pass, all loads issued
+// before the stores, non-temporal or regular accesses.  No arithmetic: the
+// speed of moving an op's read and write bytes, the ceiling the op is
 // measured against.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int NR, int U, bool NT>
 __global__ __launch_bounds__(kEwBlock) void stream_probe_kernel(const u32x4 *__restrict__ a,
-                                                                const u32x4 *__restrict__ b,
-                                                                u32x4 *__restrict__ out, uint64_t n) {
+                                                                const u32x4 *__restrict__ b, uint64_t nr,
+                                                                u32x4 *__restrict__ out, uint64_t nw) {
     const uint64_t base = (uint64_t)blockIdx.x * kEwBlock * U + threadIdx.x;
     u32x4 v[U];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
         const uint64_t i = base + (uint64_t)k * kEwBlock;
-        if (i < n) {
+        v[k] = u32x4{(uint32_t)i, 0u, 0u, 0u};
+        if (i < nr) {
             v[k] = NT ? __builtin_nontemporal_load(a + i) : a[i];
             if constexpr (NR == 2) v[k] ^= NT ? __builtin_nontemporal_load(b + i) : b[i];
         }
@@ -152,11 +154,13 @@ __global__ __launch_bounds__(kEwBlock) void stream_probe_kernel(const u32x4 *__r
 #pragma unroll
     for (int k = 0; k < U; ++k) {
         const uint64_t i = base + (uint64_t)k * kEwBlock;
-        if (i < n) {
+        if (i < nw) {
             if (NT)
                 __builtin_nontemporal_store(v[k], out + i);
             else
                 out[i] = v[k];
+        } else if (i < nr && v[k].x == 0x9e3779b9u && v[k].y == 0x7f4a7c15u) {
+            out[0] = v[k];  // keeps reads past the write range live; practically never taken
         }
     }
 }
@@ -262,13 +266,14 @@ extern "C" int fellm_rocm_add(const void *a, const void *b, uint32_t in_dtype, v
     });
 }
 
-extern "C" int fellm_rocm_stream_probe(const void *a, const void *b, void *out, uint64_t bytes, uint32_t variant,
-                                       void *stream) {
+extern "C" int fellm_rocm_stream_probe(const void *a, const void *b, uint64_t read_bytes, void *out,
+                                       uint64_t write_bytes, uint32_t variant, void *stream) {
     using namespace fellm;
-    if (bytes == 0) return FELLM_OK;
-    if (!a || !out || bytes % 16 || !aligned_to(a, 16) || !aligned_to(out, 16) || (b && !aligned_to(b, 16)))
+    if (read_bytes == 0 && write_bytes == 0) return FELLM_OK;
+    if ((read_bytes && !a) || !out || read_bytes % 16 || write_bytes % 16 || !aligned_to(a, 16) ||
+        !aligned_to(out, 16) || (b && !aligned_to(b, 16)))
         return FELLM_ERR_SHAPE;
-    const uint64_t n = bytes / 16;
+    const uint64_t nr = read_bytes / 16, nw = write_bytes / 16, n = nr > nw ? nr : nw;
     hipStream_t s = as_stream(stream);
     const int u = variant & 3 ? 1 << (variant & 3) >> 1 : 1;  // variant bits 0-1: U = 1, 1, 2, 4
     const bool nt = (variant & 4) != 0;
@@ -279,11 +284,11 @@ extern "C" int fellm_rocm_stream_probe(const void *a, const void *b, void *out, 
         const u32x4 *pa = static_cast<const u32x4 *>(a), *pb = static_cast<const u32x4 *>(b);
         u32x4 *po = static_cast<u32x4 *>(out);
         if (b) {
-            if (nt) FELLM_LAUNCH((stream_probe_kernel<2, U, true>), grid, dim3(kEwBlock), 0, s, pa, pb, po, n);
-            else FELLM_LAUNCH((stream_probe_kernel<2, U, false>), grid, dim3(kEwBlock), 0, s, pa, pb, po, n);
+            if (nt) FELLM_LAUNCH((stream_probe_kernel<2, U, true>), grid, dim3(kEwBlock), 0, s, pa, pb, nr, po, nw);
+            else FELLM_LAUNCH((stream_probe_kernel<2, U, false>), grid, dim3(kEwBlock), 0, s, pa, pb, nr, po, nw);
         } else {
-            if (nt) FELLM_LAUNCH((stream_probe_kernel<1, U, true>), grid, dim3(kEwBlock), 0, s, pa, pb, po, n);
-            else FELLM_LAUNCH((stream_probe_kernel<1, U, false>), grid, dim3(kEwBlock), 0, s, pa, pb, po, n);
+            if (nt) FELLM_LAUNCH((stream_probe_kernel<1, U, true>), grid, dim3(kEwBlock), 0, s, pa, pb, nr, po, nw);
+            else FELLM_LAUNCH((stream_probe_kernel<1, U, false>), grid, dim3(kEwBlock), 0, s, pa, pb, nr, po, nw);
         }
         return launch_status();
     };

@@ -36,23 +36,17 @@
 #ifndef FELLM_EMB_BLOCK
 #define FELLM_EMB_BLOCK 256
 #endif
+// Build knob: Q4_K / Q6_K scale factors staged in LDS once per row (1) or
+// decoded from the block header by every part (0).
+#ifndef FELLM_EMB_STAGE
+#define FELLM_EMB_STAGE 1
+#endif
 // Build knob: plain gathers decode and store part by part (1) or decode all
 // parts into registers first (0).
 #ifndef FELLM_EMB_LOOP
 #define FELLM_EMB_LOOP 1
 #endif
-// Build knob: token rows per workgroup of the plain dense gather (0: one row
-// per workgroup through embedding_kernel) and of the plain quantized gather.
-#ifndef FELLM_EMB_TPW
-#define FELLM_EMB_TPW 0
-#endif
-#ifndef FELLM_EMB_QTPW
-#define FELLM_EMB_QTPW 0
-#endif
-// Build knob: parts per thread held in registers by the multi-row gather.
-#ifndef FELLM_EMB_U
-#define FELLM_EMB_U 4
-#endif
+
 
 namespace fellm {
 namespace {
@@ -64,6 +58,7 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
 // ---- decoders --------------------------------------------------------------
 template <typename A, int VEC>
 struct DenseDec {
+    static constexpr bool STAGED = false;
     static constexpr int OUT = VEC, RUNS = 1, RUNLEN = VEC;
     __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)dim * sizeof(typename A::T); }
     __host__ __device__ static uint32_t parts(uint32_t dim) { return dim / VEC; }
@@ -77,6 +72,7 @@ struct DenseDec {
 };
 
 struct Q4KDec {
+    static constexpr bool STAGED = false;
     static constexpr int OUT = 16, RUNS = 2, RUNLEN = 8;
     __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)(dim / 256) * 144; }
     __host__ __device__ static uint32_t parts(uint32_t dim) { return (dim / 256) * 16; }
@@ -106,6 +102,7 @@ struct Q4KDec {
 };
 
 struct Q6KDec {
+    static constexpr bool STAGED = false;
     static constexpr int OUT = 16, RUNS = 4, RUNLEN = 4;
     __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)(dim / 256) * 210; }
     __host__ __device__ static uint32_t parts(uint32_t dim) { return (dim / 256) * 16; }
@@ -152,6 +149,87 @@ struct Q6KDec {
     }
 };
 
+// Staged decoders: the row's per-group scale factors are computed once per
+// workgroup into LDS (4 float4 slots per 256-element block), so a part reads
+// 16 bytes of LDS instead of the block header from global memory and skips
+// the scale unpacking.  Same parts, same arithmetic, same order as Q4KDec /
+// Q6KDec:  load() issues the part's quant-byte loads, stage() fills one LDS
+// slot, finish() decodes once the slots are visible.
+struct Q4KStaged {
+    static constexpr bool STAGED = true;
+    static constexpr int OUT = 16, RUNS = 2, RUNLEN = 8;
+    using Raw = uint2;
+    __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)(dim / 256) * 144; }
+    __host__ __device__ static uint32_t parts(uint32_t dim) { return (dim / 256) * 16; }
+    __device__ static uint32_t run_off(uint32_t p, int r) { return Q4KDec::run_off(p, r); }
+    __device__ static Raw load(const uint8_t *row, uint32_t p) {
+        const uint32_t q = p % 16;
+        return *reinterpret_cast<const uint2 *>(row + (size_t)(p / 16) * 144 + 16 + 32 * (q / 4) + 8 * (q % 4));
+    }
+    // Slot 4b + c: (d * sc[2c], dmin * m[2c], d * sc[2c+1], dmin * m[2c+1]) of block b.
+    __device__ static float4 stage(const uint8_t *row, uint32_t slot) {
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(row + (size_t)(slot / 4) * 144);
+        const uint32_t c = slot % 4;
+        const float d = half_bits_to_f32(hdr.x & 0xffffu);
+        const float dmin = half_bits_to_f32(hdr.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        k4_scale_min(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
+        k4_scale_min(2 * c + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+        return make_float4(d * (float)sc0, dmin * (float)m0, d * (float)sc1, dmin * (float)m1);
+    }
+    __device__ static void finish(Raw qs, uint32_t p, const float4 *lds, float (&v)[OUT]) {
+        const float4 f = lds[(p / 16) * 4 + (p % 16) / 4];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t b = ((k < 4 ? qs.x : qs.y) >> (8 * (k % 4))) & 0xffu;
+            v[k] = f.x * (float)(b & 0x0fu) - f.y;
+            v[8 + k] = f.z * (float)(b >> 4) - f.w;
+        }
+    }
+};
+
+struct Q6KStaged {
+    static constexpr bool STAGED = true;
+    static constexpr int OUT = 16, RUNS = 4, RUNLEN = 4;
+    using Raw = uint3;
+    __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)(dim / 256) * 210; }
+    __host__ __device__ static uint32_t parts(uint32_t dim) { return (dim / 256) * 16; }
+    __device__ static uint32_t run_off(uint32_t p, int r) { return Q6KDec::run_off(p, r); }
+    __device__ static Raw load(const uint8_t *row, uint32_t p) {
+        const uint8_t *blk = row + (size_t)(p / 16) * 210;
+        const uint32_t q = p % 16, hh = q / 8, l0 = 4 * (q % 8);
+        return make_uint3(Q6KDec::ld32(blk + 64 * hh + l0), Q6KDec::ld32(blk + 64 * hh + 32 + l0),
+                          Q6KDec::ld32(blk + 128 + 32 * hh + l0));
+    }
+    // Slot 4b + 2hh + is: d * sc[8hh + is + 2k] for k = 0..3 of block b.
+    __device__ static float4 stage(const uint8_t *row, uint32_t slot) {
+        const uint8_t *blk = row + (size_t)(slot / 4) * 210;
+        const uint32_t hh = (slot % 4) / 2, is = slot % 2;
+        const uint32_t s0 = Q6KDec::ld32(blk + 192 + 8 * hh), s1 = Q6KDec::ld32(blk + 196 + 8 * hh);
+        uint16_t dbits;
+        __builtin_memcpy(&dbits, blk + 208, 2);
+        const float d = half_bits_to_f32(dbits);
+        return make_float4(d * (float)(int8_t)(s0 >> (8 * is)), d * (float)(int8_t)(s0 >> (8 * (is + 2))),
+                           d * (float)(int8_t)(s1 >> (8 * is)), d * (float)(int8_t)(s1 >> (8 * (is + 2))));
+    }
+    __device__ static void finish(Raw raw, uint32_t p, const float4 *lds, float (&v)[OUT]) {
+        const uint32_t q = p % 16, hh = q / 8, is = (4 * (q % 8)) / 16;
+        const float4 f = lds[(p / 16) * 4 + 2 * hh + is];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int32_t a = (raw.x >> (8 * m)) & 0xff, b = (raw.y >> (8 * m)) & 0xff, h = (raw.z >> (8 * m)) & 0xff;
+            const int32_t q1 = ((a & 0xf) | ((h & 3) << 4)) - 32;
+            const int32_t q2 = ((b & 0xf) | (((h >> 2) & 3) << 4)) - 32;
+            const int32_t q3 = ((a >> 4) | (((h >> 4) & 3) << 4)) - 32;
+            const int32_t q4 = ((b >> 4) | (((h >> 6) & 3) << 4)) - 32;
+            v[m] = f.x * (float)q1;
+            v[4 + m] = f.y * (float)q2;
+            v[8 + m] = f.z * (float)q3;
+            v[12 + m] = f.w * (float)q4;
+        }
+    }
+};
+
 // Plain gathers stream their output with non-temporal stores; the fused
 // gather + RMSNorm stores after its reduction barrier and measured faster
 // with regular stores.
@@ -189,7 +267,25 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
     const uint8_t *src = table + (bad ? 0 : (uint64_t)id * rb);
     const uint32_t parts = D::parts(dim);
     const size_t obase = (size_t)row * dim;
-    if constexpr (MAXC == 0) {
+    extern __shared__ float4 stage_lds[];  // staged decoders: parts / 4 scale slots
+    if constexpr (MAXC == 0 && D::STAGED) {
+        // The first part's quant bytes are requested before the scale slots
+        // are built, so their latency overlaps the staging and the barrier.
+        typename D::Raw raw0{};
+        if (threadIdx.x < parts) raw0 = D::load(src, threadIdx.x);
+        for (uint32_t t = threadIdx.x; t < parts / 4; t += kEmbBlock) stage_lds[t] = D::stage(src, t);
+        __syncthreads();
+        for (uint32_t p = threadIdx.x; p < parts; p += kEmbBlock) {
+            float v[D::OUT];
+            D::finish(p == threadIdx.x ? raw0 : D::load(src, p), p, stage_lds, v);
+            if (bad) {
+#pragma unroll
+                for (int k = 0; k < D::OUT; ++k) v[k] = 0.0f;
+            }
+            store_part<D, O, true>(h + obase, p, v);
+        }
+        return;
+    } else if constexpr (MAXC == 0) {
         for (uint32_t p = threadIdx.x; p < parts; p += kEmbBlock) {
             float v[D::OUT];
             D::decode(src, p, v);
@@ -203,11 +299,26 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
     } else {
         float v[MAXC][D::OUT];
         float ss = 0.0f;
+        if constexpr (D::STAGED) {
+            typename D::Raw raw[MAXC];
+#pragma unroll
+            for (int c = 0; c < MAXC; ++c) {
+                const uint32_t p = c * kEmbBlock + threadIdx.x;
+                if (p < parts) raw[c] = D::load(src, p);
+            }
+            for (uint32_t t = threadIdx.x; t < parts / 4; t += kEmbBlock) stage_lds[t] = D::stage(src, t);
+            __syncthreads();
+#pragma unroll
+            for (int c = 0; c < MAXC; ++c) {
+                const uint32_t p = c * kEmbBlock + threadIdx.x;
+                if (p < parts) D::finish(raw[c], p, stage_lds, v[c]);
+            }
+        }
 #pragma unroll
         for (int c = 0; c < MAXC; ++c) {
             const uint32_t p = c * kEmbBlock + threadIdx.x;
             if (p < parts) {
-                D::decode(src, p, v[c]);
+                if constexpr (!D::STAGED) D::decode(src, p, v[c]);
 #pragma unroll
                 for (int k = 0; k < D::OUT; ++k) {
                     if (bad) v[c][k] = 0.0f;
@@ -244,47 +355,6 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
     }
 }
 
-// Plain gather of TPW token rows per workgroup: the rows' parts form one
-// list of TPW * parts items; each thread decodes up to U of them (items t,
-// t + block, ...) into registers, every load in flight together, then
-// stores them.  Fewer, longer-lived workgroups than one row each, and the
-// dependent id loads of all TPW rows are issued at once.
-template <typename D, typename O, int U>
-__global__ __launch_bounds__(kEmbBlock) void gather_rows_kernel(
-    const uint8_t *__restrict__ table, uint64_t vocab, uint32_t dim, const uint32_t *__restrict__ ids,
-    uint32_t n_ids, uint32_t tpw, typename O::T *__restrict__ out, uint32_t *__restrict__ err) {
-    const uint32_t parts = D::parts(dim);
-    const uint64_t rb = D::row_bytes(dim);
-    const uint32_t tok0 = blockIdx.x * tpw;
-    const uint32_t ntok = n_ids - tok0 < tpw ? n_ids - tok0 : tpw;
-    const uint32_t items = ntok * parts;
-    for (uint32_t i0 = 0; i0 < items; i0 += U * kEmbBlock) {
-        float v[U][D::OUT];
-        uint32_t tk[U], pp[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t it = i0 + u * kEmbBlock + threadIdx.x;
-            tk[u] = it / parts;
-            pp[u] = it - tk[u] * parts;
-            if (it < items) {
-                const uint32_t id = ids[tok0 + tk[u]];
-                const bool bad = id >= vocab;
-                D::decode(table + (bad ? 0 : (uint64_t)id * rb), pp[u], v[u]);
-                if (bad) {
-                    if (err) atomicOr(err, 1u);
-#pragma unroll
-                    for (int k = 0; k < D::OUT; ++k) v[u][k] = 0.0f;
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t it = i0 + u * kEmbBlock + threadIdx.x;
-            if (it < items) store_part<D, O, true>(out + (size_t)(tok0 + tk[u]) * dim, pp[u], v[u]);
-        }
-    }
-}
-
 template <typename D, typename O>
 int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids,
                void *h, void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
@@ -292,23 +362,17 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
     const dim3 grid(n_ids), block(kEmbBlock);
     const uint8_t *tb = static_cast<const uint8_t *>(table);
     const uint32_t chunks = (D::parts(dim) + kEmbBlock - 1) / kEmbBlock;
+    const uint32_t lds = D::STAGED ? D::parts(dim) / 4 * sizeof(float4) : 0;
+    if (lds > 65536) return FELLM_ERR_SHAPE;  // dim > 262144
 #define FELLM_EMB(C, NORM)                                                                          \
     if (chunks <= C) {                                                                              \
-        FELLM_LAUNCH((embedding_kernel<D, O, C, NORM>), grid, block, 0, s, tb, vocab, dim, ids,  \
+        FELLM_LAUNCH((embedding_kernel<D, O, C, NORM>), grid, block, lds, s, tb, vocab, dim, ids, \
                            (TO *)h, (TO *)y, w, eps, err);                                          \
         return launch_status();                                                                     \
     }
     if (!w) {
-        constexpr bool dense = D::OUT == 8 && D::RUNS == 1;
-        constexpr uint32_t tpw = dense ? FELLM_EMB_TPW : FELLM_EMB_QTPW;
-        if (tpw > 0 && ids) {
-            const uint32_t groups = (n_ids + tpw - 1) / tpw;
-            FELLM_LAUNCH((gather_rows_kernel<D, O, FELLM_EMB_U>), dim3(groups), block, 0, s, tb, vocab, dim, ids,
-                         n_ids, tpw, (TO *)h, err);
-            return launch_status();
-        }
         if (FELLM_EMB_LOOP) {
-            FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, 0, s, tb, vocab, dim, ids, (TO *)h,
+            FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, lds, s, tb, vocab, dim, ids, (TO *)h,
                                nullptr, nullptr, 0.0f, err);
             return launch_status();
         }
@@ -316,7 +380,7 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
         FELLM_EMB(2, false)
         FELLM_EMB(4, false)
         FELLM_EMB(8, false)
-        FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, 0, s, tb, vocab, dim, ids, (TO *)h,
+        FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, lds, s, tb, vocab, dim, ids, (TO *)h,
                            nullptr, nullptr, 0.0f, err);
         return launch_status();
     }
@@ -335,9 +399,11 @@ int dispatch_table(const void *table, uint32_t table_dtype, uint64_t vocab, uint
     switch (table_dtype) {
         case FELLM_DTYPE_Q4K:
             if (dim % 256 || !aligned_to(table, 16)) return FELLM_ERR_SHAPE;
+            if (FELLM_EMB_STAGE) return launch_emb<Q4KStaged, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
             return launch_emb<Q4KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
         case FELLM_DTYPE_Q6K:
             if (dim % 256 || !aligned_to(table, 2)) return FELLM_ERR_SHAPE;
+            if (FELLM_EMB_STAGE) return launch_emb<Q6KStaged, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
             return launch_emb<Q6KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
         default:
             break;

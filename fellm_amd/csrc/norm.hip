@@ -16,14 +16,21 @@
 #ifndef FELLM_NORM_W_EARLY
 #define FELLM_NORM_W_EARLY 1
 #endif
-// Build knob: rows of at most 8 KB take one wavefront per row (1) instead of
-// one workgroup per row (0) when there are many rows.  Measured on MI355X
-// inside the op chain: 4096 x 4096 f16 add+RMSNorm 28.4 us (wavefront per
-// row) against 25.2 us (workgroup per row), and the RoPE launched after it
-// slowed from 15.6 to 19.5 us; 16384 x 2048 bf16 RMSNorm 26.4 against
-// 27.1-27.6 us.  Off.
-#ifndef FELLM_NORM_WAVE
-#define FELLM_NORM_WAVE 0
+// Build knob: with many rows, rows of at most FELLM_NORM_WAVE_BYTES bytes
+// take one wavefront per row instead of one workgroup per row (0: never).
+// Measured on MI355X inside the op chains: 16384 x 2048 bf16 RMSNorm
+// 26.2-26.3 us (wavefront per row) against 27.3-27.5 us; 4096 x 4096 f16
+// add+RMSNorm (8 KB rows) 28.4 us against 25.2 us, with the RoPE launched
+// after it slowed from 15.6 to 19.5 us.  So rows up to 4 KB only.
+#ifndef FELLM_NORM_WAVE_BYTES
+#define FELLM_NORM_WAVE_BYTES 4096
+#endif
+// Build knob: threads per row for rows of 2049..4096 (16-bit) elements at
+// >= 1024 rows (256: two 8-element chunks per thread; 512: one).  Measured
+// inside the op chain at 4096 x 4096 f16: 24.4-24.5 us (512) against
+// 25.2-25.9 us (256).
+#ifndef FELLM_NORM_PREFILL_BLOCK
+#define FELLM_NORM_PREFILL_BLOCK 512
 #endif
 
 namespace fellm {
@@ -253,13 +260,15 @@ int launch_typed(const void *x, const void *r, void *h, const float *w, void *y,
         }
         // Many rows of at most 8 KB: one wavefront per row.
         constexpr uint32_t WV = 16 / sizeof(typename A::T);  // elements per 16-byte chunk
-        if (FELLM_NORM_WAVE && group % WV == 0 && group * sizeof(typename A::T) <= 8192) {
+        if (group % WV == 0 && group * sizeof(typename A::T) <= FELLM_NORM_WAVE_BYTES) {
             const uint32_t nch = (group / WV + kWave - 1) / kWave;
             if (nch <= 1) return launch_wave<A, O, 1>(x, r, h, w, y, group, rows, eps, s);
             if (nch <= 2) return launch_wave<A, O, 2>(x, r, h, w, y, group, rows, eps, s);
             if (nch <= 4) return launch_wave<A, O, 4>(x, r, h, w, y, group, rows, eps, s);
             return launch_wave<A, O, 8>(x, r, h, w, y, group, rows, eps, s);
         }
+        if (FELLM_NORM_PREFILL_BLOCK == 512 && group > 256 * VEC && group <= 512 * VEC)
+            return launch_fast<A, O, 512, VEC, 1>(x, r, h, w, y, group, rows, eps, s);
         if (group <= 256 * VEC) return launch_fast<A, O, 256, VEC, 1>(x, r, h, w, y, group, rows, eps, s);
         if (group <= 256 * VEC * 2) return launch_fast<A, O, 256, VEC, 2>(x, r, h, w, y, group, rows, eps, s);
         if (group <= 256 * VEC * 4) return launch_fast<A, O, 256, VEC, 4>(x, r, h, w, y, group, rows, eps, s);

@@ -311,10 +311,13 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
 // rows per workgroup win (63.3 us against 69.1 us for one) by sharing the
 // launch and sin/cos set-up.  R * rope_dim/2 (sin, cos) pairs must fit the
 // LDS table.
+#ifndef FELLM_ROPE_MAX_R
+#define FELLM_ROPE_MAX_R 4
+#endif
 inline int rope_rows_per_block(uint32_t rows, uint32_t rope_dim) {
     const uint32_t half = rope_dim / 2;
-    if (rows >= 16384 && half <= kMaxHalf / 4) return 4;
-    if (rows >= 8192 && half <= kMaxHalf / 2) return 2;
+    if (FELLM_ROPE_MAX_R >= 4 && rows >= 16384 && half <= kMaxHalf / 4) return 4;
+    if (FELLM_ROPE_MAX_R >= 2 && rows >= 8192 && half <= kMaxHalf / 2) return 2;
     return 1;
 }
 

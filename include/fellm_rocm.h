@@ -364,14 +364,15 @@ void fellm_rocm_timing_disarm(void);
 
 /*
  * Streaming probe (measurement only; no counterpart in the reference):
- * out = a, or a ^ b when b != NULL, over `bytes` (a multiple of 16, 16-byte
- * aligned buffers), no arithmetic.  It moves the read and write bytes of an
- * op with nothing else, the ceiling the bench compares the op against.
- * variant bits 0-1: units of 16 bytes per thread (0, 1: one; 2: two; 3:
- * four), bit 2: non-temporal loads and stores.
+ * reads read_bytes from a (and as many from b when b != NULL) and writes
+ * write_bytes to out (a ^ b where both were read), no arithmetic; sizes are
+ * multiples of 16 and buffers 16-byte aligned.  It moves an op's read and
+ * write bytes with nothing else: the ceiling the bench compares the op
+ * against.  variant bits 0-1: 16-byte units per thread (0, 1: one; 2: two;
+ * 3: four), bit 2: non-temporal loads and stores.
  */
-int fellm_rocm_stream_probe(const void *a, const void *b, void *out, uint64_t bytes, uint32_t variant,
-                            void *stream);
+int fellm_rocm_stream_probe(const void *a, const void *b, uint64_t read_bytes, void *out, uint64_t write_bytes,
+                            uint32_t variant, void *stream);
 
 /*
  * Self-check of the device sinf/cosf restatement that builds RoPE's per-row
