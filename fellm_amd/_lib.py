@@ -58,7 +58,9 @@ _SIGNATURES = {
     "fellm_rocm_router_topk": (I32, [P, U32, U32, U32, U32, U32, F32, P, P, P]),
     "fellm_rocm_expf": (I32, [P, P, U64, P]),
     "fellm_rocm_sincosf": (I32, [P, P, P, U64, P]),
+    "fellm_rocm_mathf": (I32, [U32, P, P, U64, P]),
     "fellm_rocm_timing_arm": (I32, [P, P]),
+    "fellm_rocm_attention_f32kv": (I32, [P, P, U32, U32, U32, U32, P, P, U32, U32, P, P, U32, F32, P]),
     "fellm_rocm_stream_probe": (I32, [P, P, U64, P, U64, U32, P]),
     "fellm_rocm_timing_disarm": (None, []),
     "fellm_rocm_silu_fast_bound": (I32, [P, P]),

@@ -519,6 +519,174 @@ int dispatch_hd(uint32_t hd, uint32_t G, const void *q, void *out, uint32_t batc
     return FELLM_ERR_SHAPE;
 }
 
+// ---------------------------------------------------------------------------
+// Attention over f32 K/V rows held contiguously ([t, n_kv * head_dim]), the
+// non-paged arms of the reference's Attention launch:
+//  * decode (backend.rs:1371-1397; CUDA attention_heads, launchers.rs:
+//    3719-3760): one query row against keys [max(0, seq - window), seq) of
+//    one K/V pair;
+//  * canvas (backend.rs:1412-1535; CUDA attention_canvas_heads,
+//    launchers.rs:3270-3333): every query row against the prefix keys
+//    [prefix_start, past) of one pair and then all `rows` canvas keys of a
+//    second pair, with no causal mask.
+// One workgroup (four wavefronts) per (query row, KV head): the G query heads
+// of the KV head share every K/V byte.  Keys go in tiles of 64, tile i to
+// wavefront i % 4.  Scores: lane = key, the full q . k over the head
+// dimension from 16-byte K loads against q held in LDS.  Online softmax per
+// head (tile max and sum across the wavefront).  P.V: lane = dimension slot
+// (dims lane, lane + 64, ...), probabilities read back from LDS.  The four
+// wavefronts' (max, sum, accumulators) are merged in LDS at the end.
+constexpr int kF32kvWaves = 4;
+
+template <int VD, int GM>
+__global__ __launch_bounds__(kF32kvWaves * kWave) void attention_f32kv_kernel(
+    const float *__restrict__ q, float *__restrict__ out, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
+    const float *__restrict__ k1, const float *__restrict__ v1, uint32_t b1, uint32_t e1,
+    const float *__restrict__ k2, const float *__restrict__ v2, uint32_t n2, float scale) {
+    extern __shared__ float f32kv_lds[];
+    const uint32_t G = n_heads / n_kv;
+    const uint32_t row = blockIdx.x / n_kv, g = blockIdx.x % n_kv;
+    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const size_t kv_w = (size_t)n_kv * hd;  // elements per K/V row
+    float *q_lds = f32kv_lds;                        // [G][hd]
+    float *p_lds = f32kv_lds + GM * hd;              // [waves][GM][64]
+    const float *qrow = q + ((size_t)row * n_heads + (size_t)g * G) * hd;
+    for (uint32_t i = threadIdx.x; i < G * hd; i += kF32kvWaves * kWave) q_lds[i] = qrow[i];
+    __syncthreads();
+
+    const uint32_t n1 = e1 > b1 ? e1 - b1 : 0, n = n1 + n2;
+    float m[GM], l[GM], acc[GM][VD];
+#pragma unroll
+    for (int h = 0; h < GM; ++h) {
+        m[h] = -__builtin_inff();
+        l[h] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < VD; ++c) acc[h][c] = 0.0f;
+    }
+    float *pw = p_lds + (size_t)wave * GM * kWave;
+    for (uint32_t t0 = wave * kWave; t0 < n; t0 += kF32kvWaves * kWave) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // previous tile's p reads before new writes
+        __builtin_amdgcn_wave_barrier();
+        // scores: lane = key t0 + lane
+        const uint32_t j = t0 + lane;
+        const bool valid = j < n;
+        const float *kr = nullptr;
+        if (valid) kr = j < n1 ? k1 + (size_t)(b1 + j) * kv_w + (size_t)g * hd : k2 + (size_t)(j - n1) * kv_w + (size_t)g * hd;
+        float sc[GM];
+#pragma unroll
+        for (int h = 0; h < GM; ++h) sc[h] = 0.0f;
+        if (valid) {
+            for (uint32_t d = 0; d < hd; d += 4) {
+                const float4 kv4 = *reinterpret_cast<const float4 *>(kr + d);
+#pragma unroll
+                for (int h = 0; h < GM; ++h) {
+                    if (h < (int)G) {
+                        const float4 q4 = *reinterpret_cast<const float4 *>(q_lds + h * hd + d);
+                        sc[h] += q4.x * kv4.x + q4.y * kv4.y + q4.z * kv4.z + q4.w * kv4.w;
+                    }
+                }
+            }
+        }
+        float alpha[GM];
+#pragma unroll
+        for (int h = 0; h < GM; ++h) {
+            if (h >= (int)G) continue;
+            const float s = valid ? sc[h] * scale : -__builtin_inff();
+            const float m_new = fmaxf(m[h], wave_max(s));
+            alpha[h] = m[h] > -__builtin_inff() ? __expf(m[h] - m_new) : 0.0f;
+            const float p = valid ? __expf(s - m_new) : 0.0f;
+            l[h] = l[h] * alpha[h] + wave_sum(p);
+            m[h] = m_new;
+            pw[h * kWave + lane] = p;
+        }
+        // P.V: lane = dimension slot, reading the p values other lanes of
+        // this wavefront just wrote (waves run different tile counts, so no
+        // workgroup barrier here: a wavefront-scope fence orders the LDS
+        // writes before the reads).
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int h = 0; h < GM; ++h)
+            if (h < (int)G)
+#pragma unroll
+                for (int c = 0; c < VD; ++c) acc[h][c] *= alpha[h];
+        const uint32_t kn = n - t0 < (uint32_t)kWave ? n - t0 : (uint32_t)kWave;
+        for (uint32_t jj = 0; jj < kn; ++jj) {
+            const uint32_t jt = t0 + jj;
+            const float *vr = jt < n1 ? v1 + (size_t)(b1 + jt) * kv_w + (size_t)g * hd
+                                      : v2 + (size_t)(jt - n1) * kv_w + (size_t)g * hd;
+            float vv[VD];
+#pragma unroll
+            for (int c = 0; c < VD; ++c) {
+                const uint32_t d = lane + c * kWave;
+                vv[c] = d < hd ? vr[d] : 0.0f;
+            }
+#pragma unroll
+            for (int h = 0; h < GM; ++h) {
+                if (h < (int)G) {
+                    const float p = pw[h * kWave + jj];
+#pragma unroll
+                    for (int c = 0; c < VD; ++c) acc[h][c] += p * vv[c];
+                }
+            }
+        }
+    }
+    // Merge the wavefronts into wavefront 0, one at a time through LDS.
+    float *st = f32kv_lds;  // [GM][2 + hd]: m, l, acc
+    for (uint32_t w = 1; w < (uint32_t)kF32kvWaves; ++w) {
+        __syncthreads();
+        if (wave == w) {
+#pragma unroll
+            for (int h = 0; h < GM; ++h) {
+                if (h >= (int)G) continue;
+                float *sh = st + h * (2 + hd);
+                if (lane == 0) {
+                    sh[0] = m[h];
+                    sh[1] = l[h];
+                }
+#pragma unroll
+                for (int c = 0; c < VD; ++c) {
+                    const uint32_t d = lane + c * kWave;
+                    if (d < hd) sh[2 + d] = acc[h][c];
+                }
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int h = 0; h < GM; ++h) {
+                if (h >= (int)G) continue;
+                const float *sh = st + h * (2 + hd);
+                const float mo = sh[0], lo = sh[1];
+                const float mn = fmaxf(m[h], mo);
+                if (mn == -__builtin_inff()) continue;
+                const float a = m[h] > -__builtin_inff() ? __expf(m[h] - mn) : 0.0f;
+                const float b = mo > -__builtin_inff() ? __expf(mo - mn) : 0.0f;
+                l[h] = l[h] * a + lo * b;
+                m[h] = mn;
+#pragma unroll
+                for (int c = 0; c < VD; ++c) {
+                    const uint32_t d = lane + c * kWave;
+                    acc[h][c] = acc[h][c] * a + (d < hd ? sh[2 + d] : 0.0f) * b;
+                }
+            }
+        }
+    }
+    if (wave == 0) {
+        float *orow = out + ((size_t)row * n_heads + (size_t)g * G) * hd;
+#pragma unroll
+        for (int h = 0; h < GM; ++h) {
+            if (h >= (int)G) continue;
+            const float inv = l[h] > 0.0f ? 1.0f / l[h] : 0.0f;
+#pragma unroll
+            for (int c = 0; c < VD; ++c) {
+                const uint32_t d = lane + c * kWave;
+                if (d < hd) orow[(size_t)h * hd + d] = l[h] > 0.0f ? acc[h][c] * inv : 0.0f;
+            }
+        }
+    }
+}
+
 }  // namespace
 }  // namespace fellm
 
@@ -567,4 +735,41 @@ extern "C" int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void 
     FELLM_ATT_QO(FELLM_DTYPE_BF16, BF16, FELLM_DTYPE_F32, F32)
 #undef FELLM_ATT_QO
     return FELLM_ERR_DTYPE;
+}
+
+extern "C" int fellm_rocm_attention_f32kv(const float *q, float *out, uint32_t rows, uint32_t n_heads,
+                                          uint32_t n_kv_heads, uint32_t head_dim, const float *k1, const float *v1,
+                                          uint32_t begin1, uint32_t end1, const float *k2, const float *v2, uint32_t n2,
+                                          float scale, void *stream) {
+    using namespace fellm;
+    if (!q || !out) return FELLM_ERR_ARITY;
+    if (end1 > begin1 && (!k1 || !v1)) return FELLM_ERR_ARITY;
+    if (n2 && (!k2 || !v2)) return FELLM_ERR_ARITY;
+    if (!n_kv_heads || n_heads % n_kv_heads || head_dim == 0 || head_dim % 4 || head_dim > 256) return FELLM_ERR_SHAPE;
+    const uint32_t G = n_heads / n_kv_heads;
+    if (G > 16 || (uint64_t)G * head_dim > 2048) return FELLM_ERR_SHAPE;
+    for (const void *p : {(const void *)q, (const void *)k1, (const void *)v1, (const void *)k2, (const void *)v2})
+        if (p && !aligned_to(p, 16)) return FELLM_ERR_SHAPE;
+    if (rows == 0) return FELLM_OK;
+    if (!(scale > 0.0f)) scale = 1.0f / sqrtf((float)head_dim);
+    hipStream_t st = as_stream(stream);
+    const uint32_t vd = (head_dim + kWave - 1) / kWave;
+    auto go = [&]<int VD, int GM>() -> int {
+        const size_t a = (size_t)GM * head_dim + (size_t)kF32kvWaves * GM * kWave;
+        const size_t b = (size_t)GM * (2 + head_dim);
+        const size_t lds = (a > b ? a : b) * sizeof(float);
+        FELLM_LAUNCH((attention_f32kv_kernel<VD, GM>), dim3(rows * n_kv_heads), dim3(kF32kvWaves * kWave), lds, st,
+                     q, out, n_heads, n_kv_heads, head_dim, k1, v1, begin1, end1, k2, v2, n2, scale);
+        return launch_status();
+    };
+    auto go_vd = [&]<int GM>() -> int {
+        if (vd <= 1) return go.template operator()<1, GM>();
+        if (vd <= 2) return go.template operator()<2, GM>();
+        return go.template operator()<4, GM>();
+    };
+    if (G <= 1) return go_vd.template operator()<1>();
+    if (G <= 2) return go_vd.template operator()<2>();
+    if (G <= 4) return go_vd.template operator()<4>();
+    if (G <= 8) return go_vd.template operator()<8>();
+    return go_vd.template operator()<16>();
 }

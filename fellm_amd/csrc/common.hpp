@@ -403,6 +403,80 @@ __device__ __forceinline__ void sincosf_glibc(float y, float *sp, float *cp) {
     *cp = sincosf_poly(xs, x2, (n & 1) != 0, neg);
 }
 
+// ---------------------------------------------------------------------------
+// logf, bit-exact with glibc >= 2.28 on x86_64 (Rust's f32::ln on linux-gnu;
+// the router's sqrt-softplus gating, kernels/moe.rs:68-77, takes it).
+// Algorithm: Szabolcs Nagy's logf from ARM optimized-routines (MIT), as glibc
+// ships it: x = 2^k z with z in [0x1.66p-1, 0x1.66p0) (the bits minus 0x3f330000
+// pick k and one of 16 subintervals), log(x) = k ln2 + log(c) + log1p(z/c - 1)
+// with a cubic for log1p, all in double, one final rounding.  The 16 (1/c,
+// log c) pairs and the cubic's coefficients are the published ones; glibc's
+// x86_64 FMA variant contracts r = z/c - 1, k ln2 + log c and the Horner
+// steps into FMAs, as below.  Checked against the host's glibc on all 2^32
+// inputs.
+// ---------------------------------------------------------------------------
+__device__ __constant__ inline constexpr double kLogfTab[16][2] = {
+    {0x1.661ec79f8f3bep+0, -0x1.57bf7808caadep-2}, {0x1.571ed4aaf883dp+0, -0x1.2bef0a7c06ddbp-2},
+    {0x1.49539f0f010bp+0, -0x1.01eae7f513a67p-2},  {0x1.3c995b0b80385p+0, -0x1.b31d8a68224e9p-3},
+    {0x1.30d190c8864a5p+0, -0x1.6574f0ac07758p-3}, {0x1.25e227b0b8eap+0, -0x1.1aa2bc79c81p-3},
+    {0x1.1bb4a4a1a343fp+0, -0x1.a4e76ce8c0e5ep-4}, {0x1.12358f08ae5bap+0, -0x1.1973c5a611cccp-4},
+    {0x1.0953f419900a7p+0, -0x1.252f438e10c1ep-5}, {0x1p+0, 0x0p+0},
+    {0x1.e608cfd9a47acp-1, 0x1.aa5aa5df25984p-5},  {0x1.ca4b31f026aap-1, 0x1.c5e53aa362eb4p-4},
+    {0x1.b2036576afce6p-1, 0x1.526e57720db08p-3},  {0x1.9c2d163a1aa2dp-1, 0x1.bc2860d22477p-3},
+    {0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2},  {0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2}};
+
+__device__ __forceinline__ float logf_glibc(float x) {
+    uint32_t ix = __float_as_uint(x);
+    if (ix == 0x3f800000u) return 0.0f;
+    if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+        if (ix * 2 == 0) return -__builtin_inff();             // log(+-0) = -inf
+        if (ix == 0x7f800000u) return x;                       // log(inf) = inf
+        if ((ix & 0x80000000u) || ix * 2 >= 0xff000000u) return __builtin_nanf("");  // x < 0 or NaN
+        ix = __float_as_uint(x * 0x1p23f) - (23u << 23);       // subnormal: normalise
+    }
+    const uint32_t tmp = ix - 0x3f330000u;
+    const uint32_t i = (tmp >> (23 - 4)) % 16;
+    const int32_t k = (int32_t)tmp >> 23;
+    const uint32_t iz = ix - (tmp & 0xff800000u);
+    const double invc = kLogfTab[i][0], logc = kLogfTab[i][1];
+    const double z = (double)__uint_as_float(iz);
+    const double A0 = -0x1.00ea348b88334p-2, A1 = 0x1.5575b0be00b6ap-2, A2 = -0x1.ffffef20a4123p-2;
+    const double Ln2 = 0x1.62e42fefa39efp-1;
+    const double r = __fma_rn(z, invc, -1.0);
+    const double y0 = __fma_rn((double)k, Ln2, logc);
+    const double r2 = __dmul_rn(r, r);
+    double y = __fma_rn(A1, r, A2);
+    y = __fma_rn(A0, r2, y);
+    y = __fma_rn(y, r2, __dadd_rn(y0, r));
+    return (float)y;
+}
+
+// Correctly rounded f32 square root (IEEE sqrtf, what f32::sqrt gives).  The
+// hardware square root is an approximation; the seed is moved to the
+// neighbour on the other side of a rounding midpoint while one exists.  A
+// midpoint m of two adjacent floats has 25 significant bits, so m*m is exact
+// in double and the comparison with x decides the rounding exactly (x never
+// equals m*m: a 25-bit odd significand squared has bit 50 set).  Checked
+// against the host's sqrtf on every positive f32 from seeds up to 2 ulps off.
+__device__ __forceinline__ float sqrtf_rn(float x) {
+    if (!(x > 0.0f) || x == __builtin_inff()) return __builtin_sqrtf(x);  // +-0, negative, NaN, inf
+    float s = __builtin_sqrtf(x);
+    const double dx = (double)x;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const float up = __uint_as_float(__float_as_uint(s) + 1u), dn = __uint_as_float(__float_as_uint(s) - 1u);
+        const double hu = __dmul_rn(__dadd_rn((double)s, (double)up), 0.5);
+        const double hd = __dmul_rn(__dadd_rn((double)s, (double)dn), 0.5);
+        if (dx > __dmul_rn(hu, hu))
+            s = up;
+        else if (dx < __dmul_rn(hd, hd))
+            s = dn;
+        else
+            break;
+    }
+    return s;
+}
+
 // get_scale_min_k4 (dequant.rs:295-305): 6-bit scale and min j (0..7) of a
 // Q4_K/Q5_K block from its 12 scale bytes held as 3 little-endian dwords.
 __device__ __forceinline__ void k4_scale_min(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,

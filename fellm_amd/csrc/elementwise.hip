@@ -176,6 +176,13 @@ __global__ __launch_bounds__(kEwBlock) void sincosf_kernel(const float *__restri
     }
 }
 
+__global__ __launch_bounds__(kEwBlock) void mathf_kernel(uint32_t fn, const float *__restrict__ in,
+                                                         float *__restrict__ out, uint64_t n) {
+    const uint64_t stride = (uint64_t)gridDim.x * kEwBlock;
+    for (uint64_t i = (uint64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += stride)
+        out[i] = fn == 0 ? logf_glibc(in[i]) : sqrtf_rn(in[i]);
+}
+
 // Largest bit distance between silu_fast and silu over every f32 g of the
 // fast domain, one grid-stride sweep of all 2^32 patterns.
 __global__ __launch_bounds__(kEwBlock) void silu_fast_bound_kernel(uint32_t *__restrict__ max_dist) {
@@ -305,6 +312,15 @@ extern "C" int fellm_rocm_timing_arm(void *start_event, void *stop_event) {
 }
 
 extern "C" void fellm_rocm_timing_disarm(void) { fellm::g_launch_timing = fellm::LaunchTiming{}; }
+
+extern "C" int fellm_rocm_mathf(uint32_t fn, const float *in, float *out, uint64_t n, void *stream) {
+    using namespace fellm;
+    if (fn > 1) return FELLM_ERR_SHAPE;
+    if (n == 0) return FELLM_OK;
+    if (!in || !out) return FELLM_ERR_ARITY;
+    FELLM_LAUNCH(mathf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), fn, in, out, n);
+    return launch_status();
+}
 
 extern "C" int fellm_rocm_sincosf(const float *in, float *sin_out, float *cos_out, uint64_t n, void *stream) {
     using namespace fellm;

@@ -90,6 +90,9 @@ struct State {
     size_t pinned_bytes = 0;
     bool host_reads_pending = false;  // an H2D copy may still read caller memory
     int sync_outputs = -1;
+    // Output mirrors this launch marked stale, with their previous state, so
+    // that a launch failing before its kernel runs leaves them as they were.
+    std::vector<std::pair<Mirror *, bool>> touched_outputs;
 };
 
 State &state() {
@@ -192,6 +195,7 @@ void *ensure_output(State &st, const FellmTensorMut &t, bool inout = false) {
         ensure_capacity(m, t.byte_len);
     }
     if (inout && !m.device_valid) upload(st, m.dev, t.data, t.byte_len);
+    st.touched_outputs.emplace_back(&m, m.device_valid);
     m.device_valid = false;  // until the launch completes on the stream
     return m.dev;
 }
@@ -280,7 +284,22 @@ int guarded(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, 
         std::lock_guard<std::mutex> lock(st.mu);
         st.host_reads_pending = false;
         st.capturing = stream_capturing(st);
-        body(st);
+        st.touched_outputs.clear();
+        try {
+            body(st);
+        } catch (const LaunchError &e) {
+            // A rejected launch (argument, shape or dtype checks, which run
+            // before anything is enqueued) restores its outputs' mirror state:
+            // a mirror holding device-only data must not fall back to the
+            // caller's stale host bytes.  After a failed kernel launch the
+            // device copy may be partly written, so it stays stale.
+            if (e.code != FELLM_ERR_LAUNCH)
+                for (auto it = st.touched_outputs.rbegin(); it != st.touched_outputs.rend(); ++it)
+                    it->first->device_valid = it->second;
+            st.touched_outputs.clear();
+            throw;
+        }
+        st.touched_outputs.clear();
         if (st.host_reads_pending) {
             st.host_reads_pending = false;
             hip_check(hipStreamSynchronize(stream_locked(st)));
@@ -415,7 +434,12 @@ int launch_rope(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_
         const FellmOpAttrs &a = *attrs;
         const uint32_t dt = in[0].dtype;
         if (in[1].dtype != FELLM_DTYPE_F32 || out[0].dtype != dt) fail(FELLM_ERR_DTYPE);
-        if (a.custom_op_id == 1) fail(FELLM_ERR_DTYPE);  // pre-RoPE side channel: not provided
+        // custom_op_id 1 asks backend-cpu to copy the pre-rotation rows into
+        // the process's pre-RoPE key store (backend.rs:1152-1158).  Across the
+        // plugin C ABI there is no channel to that store (HostContext carries
+        // none; the CUDA plugin's call, launchers.rs:430-444, reaches its own
+        // never-installed copy of the store, c_abi.rs:40-44), so, like the
+        // CUDA plugin, the launch rotates and leaves the store alone.
         const size_t n = elems(in[0], dt);
         if (elems(out[0], dt) != n) fail(FELLM_ERR_SHAPE);
         const size_t nh = a.n_heads ? a.n_heads : 1, hd = a.head_dim ? a.head_dim : 1;
@@ -622,13 +646,91 @@ int launch_rope_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, ui
 // than one row) attends row r to row_lengths[r] keys, causal with
 // attention_window; a single sequence attends to past_len + 1 keys, causal
 // when attention_mode == 0.  K/V come from the device arena (f16, or bf16 when
-// cast_to is BF16, as rope_kv_write writes it).  Contiguous-KV and canvas
-// attention are not provided (-10).
+// cast_to is BF16, as rope_kv_write writes it).  block_size == 0 and the canvas
+// form go to launch_attention_f32kv.
+// A TensorRef for the first `bytes` of t (the rows an attention launch
+// reads), so that only those are mirrored, as the CUDA plugin's slices do.
+FellmTensorRef prefix_ref(const FellmTensorRef &t, size_t bytes) {
+    FellmTensorRef r = t;
+    r.byte_len = bytes;
+    return r;
+}
+
+// The non-paged Attention arms, f32 throughout (as both reference backends
+// read these K/V inputs as f32):
+//  * contiguous decode, block_size == 0 (backend.rs:1371-1397; CUDA
+//    launchers.rs:3719-3760): q is one row, keys 0..past_len of K/V
+//    inputs 1 and 2; a window keeps the last `window` keys when causal
+//    (attention_mode 0) and the first `window` otherwise, as the CPU
+//    backend's FA2-style loop does for one query row
+//    (attention_provider.rs:305-318);
+//  * canvas, attention_mode 1 with five inputs (backend.rs:1412-1535; CUDA
+//    launchers.rs:3270-3333): query_len rows, each attending the prefix keys
+//    [past_len - window, past_len) of inputs 1 and 2 and every canvas key of
+//    inputs 3 and 4.  A paged prefix (block_size > 0 with a paged context) is
+//    not served (-10).
+void launch_attention_f32kv(State &st, const FellmOpAttrs &a, const FellmTensorRef *in, uint32_t n_in,
+                            FellmTensorMut *out, bool canvas) {
+    if (n_in < 3) fail(FELLM_ERR_ARITY);
+    for (uint32_t i = 0; i < n_in && i < 5; ++i)
+        if (in[i].dtype != FELLM_DTYPE_F32) fail(FELLM_ERR_DTYPE);
+    if (out[0].dtype != FELLM_DTYPE_F32) fail(FELLM_ERR_DTYPE);
+    const size_t nh = a.n_heads ? a.n_heads : 1, nkv = a.n_kv_heads ? a.n_kv_heads : 1, hd = a.head_dim;
+    if (!hd) fail(FELLM_ERR_SHAPE);
+    const size_t kvw = nkv * hd, past = a.past_len, window = a.attention_window;
+    const size_t rows = canvas ? (a.query_len ? a.query_len : 1) : 1;
+    const size_t qn = elems(in[0], FELLM_DTYPE_F32);
+    if (qn != rows * nh * hd || elems(out[0], FELLM_DTYPE_F32) != qn) fail(FELLM_ERR_SHAPE);
+    size_t b1 = 0, e1 = 0, n_prefix_rows = 0, n2 = 0;
+    if (canvas) {
+        FellmPagedKvSnapshot snap;
+        if (a.block_size > 0 && snapshot(st, snap)) fail(FELLM_ERR_DTYPE);  // paged prefix
+        if (elems(in[3], FELLM_DTYPE_F32) < rows * kvw || elems(in[4], FELLM_DTYPE_F32) < rows * kvw)
+            fail(FELLM_ERR_SHAPE);
+        if (past && (elems(in[1], FELLM_DTYPE_F32) < past * kvw || elems(in[2], FELLM_DTYPE_F32) < past * kvw))
+            fail(FELLM_ERR_SHAPE);
+        b1 = window ? (past > window ? past - window : 0) : 0;
+        e1 = past;
+        n_prefix_rows = past;
+        n2 = rows;
+    } else {
+        const size_t seq = past + 1;
+        if (elems(in[1], FELLM_DTYPE_F32) < seq * kvw || elems(in[2], FELLM_DTYPE_F32) < seq * kvw)
+            fail(FELLM_ERR_SHAPE);
+        b1 = 0;
+        e1 = seq;
+        if (window) {
+            if (a.attention_mode == 0) b1 = seq > window ? seq - window : 0;
+            else e1 = window < seq ? window : seq;
+        }
+        n_prefix_rows = seq;
+    }
+    void *q = ensure_input(st, in[0]);
+    void *k1 = nullptr, *v1 = nullptr, *k2 = nullptr, *v2 = nullptr;
+    if (n_prefix_rows) {
+        k1 = ensure_input(st, prefix_ref(in[1], n_prefix_rows * kvw * 4));
+        v1 = ensure_input(st, prefix_ref(in[2], n_prefix_rows * kvw * 4));
+    }
+    if (n2) {
+        k2 = ensure_input(st, prefix_ref(in[3], n2 * kvw * 4));
+        v2 = ensure_input(st, prefix_ref(in[4], n2 * kvw * 4));
+    }
+    void *o = ensure_output(st, out[0]);
+    check(fellm_rocm_attention_f32kv((const float *)q, (float *)o, (uint32_t)rows, (uint32_t)nh, (uint32_t)nkv,
+                                     (uint32_t)hd, (const float *)k1, (const float *)v1, (uint32_t)b1, (uint32_t)e1,
+                                     (const float *)k2, (const float *)v2, (uint32_t)n2, a.scale, stream_ptr(st)));
+    finish_outputs(st, out, 1);
+}
+
 int launch_attention(const FellmOpAttrs *attrs, const FellmTensorRef *in, uint32_t n_in, FellmTensorMut *out,
                      uint32_t n_out, FellmStreamHandle) {
     return guarded(attrs, in, n_in, out, n_out, 1, 1, true, [&](State &st) {
         const FellmOpAttrs &a = *attrs;
-        if (a.block_size == 0 || (a.attention_mode == 1 && n_in >= 5)) fail(FELLM_ERR_DTYPE);
+        const bool canvas = a.attention_mode == 1 && n_in >= 5;
+        if (canvas || a.block_size == 0) {
+            launch_attention_f32kv(st, a, in, n_in, out, canvas);
+            return;
+        }
         FellmPagedKvSnapshot snap;
         if (!snapshot(st, snap)) fail(FELLM_ERR_PAGED_MISSING);
         const uint32_t dt = in[0].dtype, odt = out[0].dtype;
@@ -952,8 +1054,10 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
             {FELLM_OP_GATE_UP_SWIGLU, {Q5K, Q6K, F32}, F32, launch_gate_up_swiglu},
             {FELLM_OP_GATE_UP_SWIGLU, {Q6K, Q4K, F32}, F32, launch_gate_up_swiglu},
             {FELLM_OP_GATE_UP_SWIGLU, {Q6K, Q5K, F32}, F32, launch_gate_up_swiglu},
-            // Paged decode attention (launchers.rs:3243; lib.rs:537-546 registers [F32, F32, F32]).
+            // Attention (launchers.rs:3243): paged decode, contiguous decode and canvas; the CUDA
+            // plugin registers [F32, F32, F32] and the five-input canvas form (lib.rs:537-546, 575-582).
             {FELLM_OP_ATTENTION, {F32, F32, F32}, F32, launch_attention},
+            {FELLM_OP_ATTENTION, {F32, F32, F32, F32, F32}, F32, launch_attention},
             {FELLM_OP_ATTENTION, {F16, F16, F16}, F16, launch_attention},
             {FELLM_OP_ATTENTION, {BF16, BF16, BF16}, BF16, launch_attention},
             // Fused custom ops (OpKind::custom("rocm", ...)).

@@ -3,7 +3,8 @@
 // Reference: crates/backend-cpu/src/kernels/moe.rs
 //   gate_scores :79-111 (softmax: m = max(l); e_j = exp(l_j - m);
 //       denom += e_j in expert order; s_j = e_j / denom if denom > 0;
-//       sigmoid for gating 2: s_j = 1 / (1 + exp(-l_j)))
+//       sigmoid for gating 2: s_j = 1 / (1 + exp(-l_j));
+//       sqrt-softplus for gating 4 (:68-77): s_j = sqrt(max(softplus(l_j), 0)))
 //   select_routed_experts :142-186 (rank by s descending under f32
 //       total_cmp, ties -> lower expert id)
 //   finish_selected :113-140 (truncate to k; if norm_topk_prob divide by the
@@ -93,6 +94,15 @@ __global__ __launch_bounds__(kRouterBlock) void router_topk_grouped(
     if (gating == 2) {
 #pragma unroll
         for (int j = 0; j < EPL; ++j) s[j] = 1.0f / (1.0f + expf_glibc(-s[j], tab));
+    } else if (gating == 4) {
+        // sqrt_softplus (moe.rs:68-77): softplus = v (v > 20), exp(v) (v < -20),
+        // else ln(1 + exp(v)), all f32; then sqrt(max(softplus, 0)).
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const float v = s[j];
+            const float sp = v > 20.0f ? v : (v < -20.0f ? expf_glibc(v, tab) : logf_glibc(1.0f + expf_glibc(v, tab)));
+            s[j] = sqrtf_rn(fmaxf(sp, 0.0f));
+        }
     } else {
         float m = s[0];
 #pragma unroll
@@ -218,7 +228,6 @@ extern "C" int fellm_rocm_router_topk(const float *logits, uint32_t tokens, uint
                                       void *stream) {
     using namespace fellm;
     if (n_experts == 0 || n_experts > kMaxExperts) return FELLM_ERR_SHAPE;
-    if (gating_func == 4) return FELLM_ERR_DTYPE;  // sqrt-softplus gating not implemented
     const uint32_t k = n_expert_used < n_experts ? n_expert_used : n_experts;
     if (k == 0 || k > kMaxTopK) return FELLM_ERR_SHAPE;
     if (tokens == 0) return FELLM_OK;

@@ -427,6 +427,22 @@ def expf(x):
     return out
 
 
+def logf(x):
+    """Device glibc-exact logf (self-check of the restatement the router uses)."""
+    _dev(x)
+    out = torch.empty_like(x)
+    _lib.call("fellm_rocm_mathf", 0, _p(x), _p(out), x.numel(), _stream())
+    return out
+
+
+def sqrtf(x):
+    """Device correctly rounded sqrtf (self-check; the router's sqrt-softplus uses it)."""
+    _dev(x)
+    out = torch.empty_like(x)
+    _lib.call("fellm_rocm_mathf", 1, _p(x), _p(out), x.numel(), _stream())
+    return out
+
+
 def sincosf(x):
     """Device glibc-exact (sinf(x), cosf(x)) (self-check of the restatement RoPE uses)."""
     _dev(x)

@@ -140,8 +140,9 @@ int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q_heads, con
                              const FellmRocmPagedKv *kv, uint32_t *err_flag, void *stream);
 
 /*
- * MoE router: softmax (gating_func != 2) or sigmoid (gating_func == 2) over
- * each token's n_experts logits, top-k by score (ties -> lower expert id),
+ * MoE router: softmax (gating_func other than 2 and 4), sigmoid
+ * (gating_func == 2) or sqrt-softplus (gating_func == 4) over each token's
+ * n_experts logits, top-k by score (ties -> lower expert id),
  * optional renormalisation over the k selected, times routed_scaling_factor
  * (0 -> 1).   replaces: kernels/moe.rs:79-186 and :820-855.
  * logits f32 [tokens, n_experts] (n_experts <= 512), ids u32 [tokens, k],
@@ -211,6 +212,26 @@ int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void *out, uint3
                                uint32_t max_seq, float scale, uint32_t causal, uint32_t window,
                                const FellmRocmPagedKv *kv, float *workspace, uint64_t workspace_bytes,
                                void *stream);
+
+/*
+ * Attention over f32 K/V rows stored contiguously ([t, n_kv_heads * head_dim]):
+ * the non-paged arms of the Attention op.
+ *   replaces: crates/backend-cpu/src/backend.rs:1371-1397 (contiguous decode:
+ *   one query row, keys 0..past_len, optionally windowed) and :1412-1535
+ *   (launch_canvas_attention without a paged prefix); the CUDA plugin's
+ *   attention_heads / attention_canvas_heads (plugins/cuda_kernels/src/
+ *   launchers.rs:3719-3760, :3270-3333; oxide_kernels.rs:3878, :4089).
+ * q, out f32 [rows, n_heads, head_dim]; every query row attends, without a
+ * mask, the keys t in [begin1, end1) of (k1, v1) and then t in [0, n2) of
+ * (k2, v2): out = softmax(q . k * scale) . v, scale <= 0 meaning
+ * 1/sqrt(head_dim); query head h uses KV head h / (n_heads / n_kv_heads).
+ * No keys gives a zero row.  head_dim % 4 == 0, head_dim <= 256,
+ * (n_heads / n_kv_heads) * head_dim <= 2048, 16-byte aligned buffers.
+ * Accumulation and the softmax run in f32 with the device exp.
+ */
+int fellm_rocm_attention_f32kv(const float *q, float *out, uint32_t rows, uint32_t n_heads, uint32_t n_kv_heads,
+                               uint32_t head_dim, const float *k1, const float *v1, uint32_t begin1, uint32_t end1,
+                               const float *k2, const float *v2, uint32_t n2, float scale, void *stream);
 
 /*
  * Cast: dst = src converted elementwise, n_elems elements.
@@ -380,6 +401,14 @@ int fellm_rocm_stream_probe(const void *a, const void *b, uint64_t read_bytes, v
  * Diagnostic only (no counterpart in the reference).
  */
 int fellm_rocm_sincosf(const float *in, float *sin_out, float *cos_out, uint64_t n, void *stream);
+
+/*
+ * Self-check of the device logf restatement (fn 0) and correctly rounded
+ * sqrtf (fn 1) used by the router's sqrt-softplus gating: out[i] =
+ * logf(in[i]) or sqrtf(in[i]).  Diagnostic only (no counterpart in the
+ * reference).
+ */
+int fellm_rocm_mathf(uint32_t fn, const float *in, float *out, uint64_t n, void *stream);
 
 /*
  * Verification hook for fellm_rocm_silu_gate's 16-bit output path (no

@@ -59,6 +59,8 @@ def lib(path: Path | None = None) -> C.CDLL:
             "oracle_f32_to_bf16": (None, [P, P, S, C.c_int]),
             "oracle_expf": (None, [P, P, S]),
             "oracle_sincosf": (None, [P, P, P, S]),
+            "oracle_logf": (None, [P, P, S]),
+            "oracle_attention_f32kv": (None, [P, P, S, S, S, S, P, P, S, S, P, P, S, F]),
             "oracle_get_scale_min_k4": (None, [S, P, P, P]),
             "oracle_row_bytes": (S, [U32, S]),
             "oracle_dequantize_row": (C.c_int, [U32, P, P, S]),
@@ -152,6 +154,13 @@ def expf(x: np.ndarray) -> np.ndarray:
     a = _c(x, np.float32)
     out = np.empty_like(a)
     lib().oracle_expf(_p(a), _p(out), a.size)
+    return out
+
+
+def logf(x: np.ndarray) -> np.ndarray:
+    a = _c(x, np.float32)
+    out = np.empty_like(a)
+    lib().oracle_logf(_p(a), _p(out), a.size)
     return out
 
 
@@ -386,3 +395,20 @@ def moe_weighted_reduce(y0: np.ndarray | None, expert_out: np.ndarray, weights: 
     for s in range(k):
         y = (y + (ww[:, s:s + 1] * eo[:, s]).astype(np.float32)).astype(np.float32)
     return y
+
+
+def attention_f32kv(q: np.ndarray, n_heads: int, n_kv: int, head_dim: int, k1, v1, b1: int, e1: int,
+                    k2=None, v2=None, n2: int = 0, scale: float = 0.0) -> np.ndarray:
+    """Non-paged attention (backend.rs:1371-1397, :1412-1535): q [rows, n_heads * head_dim]."""
+    q = _c(q, np.float32)
+    rows = q.size // (n_heads * head_dim)
+    out = np.zeros_like(q)
+    if scale <= 0:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+    ka = _c(k1, np.float32) if k1 is not None else np.zeros(1, np.float32)
+    va = _c(v1, np.float32) if v1 is not None else np.zeros(1, np.float32)
+    kb = _c(k2, np.float32) if k2 is not None else np.zeros(1, np.float32)
+    vb = _c(v2, np.float32) if v2 is not None else np.zeros(1, np.float32)
+    lib().oracle_attention_f32kv(_p(q), _p(out), rows, n_heads, n_kv, head_dim, _p(ka), _p(va), b1, e1, _p(kb),
+                                 _p(vb), n2, scale)
+    return out

@@ -134,6 +134,11 @@ void oracle_expf(const float *in, float *out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = expf(in[i]);
 }
 
+/* f32::ln: glibc logf. */
+void oracle_logf(const float *in, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = logf(in[i]);
+}
+
 /* f32::sin_cos as rope.rs:46-58 calls it: glibc sinf and cosf. */
 void oracle_sincosf(const float *in, float *s, float *c, size_t n) {
     for (size_t i = 0; i < n; ++i) {
@@ -434,11 +439,16 @@ static int rank_cmp(const void *pa, const void *pb) {
     return a->e < b->e ? -1 : (a->e > b->e ? 1 : 0);
 }
 
+/* moe.rs:68-77 */
+static float sqrt_softplus(float v) {
+    const float sp = v > 20.0f ? v : (v < -20.0f ? expf(v) : logf(1.0f + expf(v)));
+    return sqrtf(fmaxf(sp, 0.0f)); /* f32::max returns the non-NaN operand */
+}
+
 /* moe.rs:79-186: gate_scores -> sort -> finish_selected, per token. */
 int oracle_router(const float *logits, size_t tokens, size_t n_experts, size_t n_expert_used, uint32_t gating,
                   uint32_t norm_topk_prob, float routed_scaling_factor, uint32_t *ids, float *weights) {
     if (n_experts == 0) return -2;
-    if (gating == 4) return -10;
     Scored *sc = (Scored *)malloc(n_experts * sizeof(Scored));
     if (!sc) return -3;
     const size_t k = n_expert_used < n_experts ? n_expert_used : n_experts;
@@ -446,6 +456,8 @@ int oracle_router(const float *logits, size_t tokens, size_t n_experts, size_t n
         const float *l = logits + t * n_experts;
         if (gating == 2) {
             for (size_t e = 0; e < n_experts; ++e) sc[e] = (Scored){e, 1.0f / (1.0f + expf(-l[e]))};
+        } else if (gating == 4) {
+            for (size_t e = 0; e < n_experts; ++e) sc[e] = (Scored){e, sqrt_softplus(l[e])};
         } else {
             float m = -INFINITY;
             for (size_t e = 0; e < n_experts; ++e) m = fmaxf(m, l[e]); /* f32::max ignores NaN */
@@ -473,6 +485,44 @@ int oracle_router(const float *logits, size_t tokens, size_t n_experts, size_t n
     }
     free(sc);
     return 0;
+}
+
+/* ---- f32 K/V attention (non-paged Attention arms) ------------------------
+ * backend.rs:1412-1535 (launch_canvas_attention, no paged prefix): per query
+ * row and head, scores over keys [b1, e1) of (k1, v1) then [0, n2) of
+ * (k2, v2): score = sum_d q*k in dimension order, times scale; max; denom =
+ * sum exp(s - max) in key order; out = sum (exp(s - max) / denom) * v in key
+ * order.  Contiguous decode (backend.rs:1371-1397) is the one-row case over
+ * [max(0, seq - window), seq) of one pair. */
+void oracle_attention_f32kv(const float *q, float *out, size_t rows, size_t n_heads, size_t n_kv, size_t hd,
+                            const float *k1, const float *v1, size_t b1, size_t e1, const float *k2, const float *v2,
+                            size_t n2, float scale) {
+    const size_t kvw = n_kv * hd, group = n_heads / (n_kv ? n_kv : 1);
+    const size_t n1 = e1 > b1 ? e1 - b1 : 0, n = n1 + n2;
+    float *sc = (float *)malloc((n ? n : 1) * sizeof(float));
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t h = 0; h < n_heads; ++h) {
+            const size_t kh = h / (group ? group : 1);
+            const float *qh = q + (r * n_heads + h) * hd;
+            float *oh = out + (r * n_heads + h) * hd;
+            for (size_t j = 0; j < n; ++j) {
+                const float *kr = j < n1 ? k1 + (b1 + j) * kvw + kh * hd : k2 + (j - n1) * kvw + kh * hd;
+                float s = 0.0f;
+                for (size_t d = 0; d < hd; ++d) s += qh[d] * kr[d];
+                sc[j] = s * scale;
+            }
+            float mx = -INFINITY, den = 0.0f;
+            for (size_t j = 0; j < n; ++j) mx = fmaxf(mx, sc[j]);
+            for (size_t j = 0; j < n; ++j) den += expf(sc[j] - mx);
+            for (size_t d = 0; d < hd; ++d) oh[d] = 0.0f;
+            if (den > 0.0f)
+                for (size_t j = 0; j < n; ++j) {
+                    const float w = expf(sc[j] - mx) / den;
+                    const float *vr = j < n1 ? v1 + (b1 + j) * kvw + kh * hd : v2 + (j - n1) * kvw + kh * hd;
+                    for (size_t d = 0; d < hd; ++d) oh[d] += w * vr[d];
+                }
+        }
+    free(sc);
 }
 
 /* ---- next: quantized gate/up GEMV with the SwiGLU epilogue ---------------

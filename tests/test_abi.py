@@ -168,10 +168,10 @@ def test_launch_error_paths_before_gpu(host):
     tref = abi.tensor_ref(table.ctypes.data, table.nbytes, abi.DType.F32, [4, 8])
     iref = abi.tensor_ref(ids.ctypes.data, ids.nbytes, abi.DType.U32, [2])
     assert _launch(host, *emb, attrs, [tref, iref], [tm(out)]) == abi.ERR_SHAPE
-    # RoPE with the pre-RoPE side channel requested -> unsupported
-    attrs_r = abi.OpAttrs(n_heads=1, head_dim=10, rope_dim=10, custom_op_id=1)
+    # RoPE: x.len() not a multiple of n_heads * head_dim -> -2
+    attrs_r = abi.OpAttrs(n_heads=1, head_dim=4, rope_dim=4)
     rope = (abi.OpKind.ROPE, [abi.DType.F32, abi.DType.F32], abi.DType.F32)
-    assert _launch(host, *rope, attrs_r, [tr(x), tr(_f32(5))], [tm(y)]) == abi.ERR_DTYPE
+    assert _launch(host, *rope, attrs_r, [tr(x), tr(_f32(5))], [tm(y)]) == abi.ERR_SHAPE
     # fused RoPE + KV write without a paged context -> -20
     q, k = _f32(8), _f32(8)
     rkv = (abi.OP_ROPE_KV_WRITE, [abi.DType.F32] * 4, abi.DType.F32)
@@ -207,8 +207,8 @@ def test_device_api_validates_before_launch():
     assert lib.fellm_rocm_add_rmsnorm(None, None, None, 1, None, 16, None, 1, 32, 1e-5, None) == abi.ERR_ARITY
     assert lib.fellm_rocm_router_topk(C.c_void_p(16), 1, 600, 8, 1, 1, 0.0, C.c_void_p(16), C.c_void_p(16),
                                       None) == abi.ERR_SHAPE
-    assert lib.fellm_rocm_router_topk(C.c_void_p(16), 1, 8, 2, 4, 1, 0.0, C.c_void_p(16), C.c_void_p(16),
-                                      None) == abi.ERR_DTYPE
+    assert lib.fellm_rocm_router_topk(C.c_void_p(16), 1, 0, 2, 4, 1, 0.0, C.c_void_p(16), C.c_void_p(16),
+                                      None) == abi.ERR_SHAPE
     assert lib.fellm_rocm_embedding(C.c_void_p(16), 99, 10, 16, C.c_void_p(16), 1, C.c_void_p(16), 0, None,
                                     None) == abi.ERR_DTYPE
     assert lib.fellm_rocm_rope(C.c_void_p(16), C.c_void_p(16), 1, None, None, 0, 0, 1, 8, 10, 0, C.c_void_p(16),

@@ -131,3 +131,61 @@ def test_paged_attention_empty_rows_and_zero_batch(ops, dev):
     ref = oracle.paged_attention(q, n_heads, n_kv, hd, np.array(lengths), float(np.float32(1 / np.sqrt(hd))), arena,
                                  table, n_logical, 1, 0, 16, bb)
     check(got, ref, v16, "f32", "empty rows")
+
+
+# ---- non-paged attention: f32 K/V rows (contiguous decode, canvas) -----------------
+def _f32kv(ops, q, n_heads, n_kv, hd, k1, v1, b1, e1, k2=None, v2=None, n2=0, scale=0.0):
+    from fellm_amd import _lib
+
+    dev = torch.device("cuda:0")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev) if a is not None else None
+    qd, k1d, v1d, k2d, v2d = t(q), t(k1), t(v1), t(k2), t(v2)
+    out = torch.full_like(qd, float("nan"))
+    p = lambda x: x.data_ptr() if x is not None else None
+    rc = _lib.lib().fellm_rocm_attention_f32kv(p(qd), p(out), q.shape[0], n_heads, n_kv, hd, p(k1d), p(v1d), b1, e1,
+                                               p(k2d), p(v2d), n2, scale, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, rc
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,seq,b1", [(32, 8, 128, 4096, 0), (8, 2, 64, 37, 0), (32, 8, 128, 300, 44),
+                                                    (16, 1, 128, 129, 0), (4, 4, 80, 5, 0), (8, 1, 256, 1000, 10),
+                                                    (2, 2, 96, 64, 0), (12, 4, 64, 1, 0)])
+def test_attention_f32kv_decode(ops, n_heads, n_kv, hd, seq, b1):
+    rng = np.random.default_rng(seq * 7 + hd)
+    q = rng.normal(size=(1, n_heads * hd)).astype(np.float32)
+    k = rng.normal(size=(seq, n_kv * hd)).astype(np.float32)
+    v = rng.normal(size=(seq, n_kv * hd)).astype(np.float32)
+    got = _f32kv(ops, q, n_heads, n_kv, hd, k, v, b1, seq)
+    ref = oracle.attention_f32kv(q, n_heads, n_kv, hd, k, v, b1, seq)
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(v).max() + np.abs(ref).max() * 2.0 ** -23
+
+
+@pytest.mark.parametrize("rows,past", [(4, 100), (1, 0), (17, 3), (32, 513)])
+def test_attention_f32kv_canvas(ops, rows, past):
+    rng = np.random.default_rng(rows * 100 + past)
+    nh, nkv, hd = 16, 4, 128
+    q = rng.normal(size=(rows, nh * hd)).astype(np.float32)
+    pk = rng.normal(size=(max(past, 1), nkv * hd)).astype(np.float32)
+    pv = rng.normal(size=(max(past, 1), nkv * hd)).astype(np.float32)
+    ck = rng.normal(size=(rows, nkv * hd)).astype(np.float32)
+    cv = rng.normal(size=(rows, nkv * hd)).astype(np.float32)
+    got = _f32kv(ops, q, nh, nkv, hd, pk, pv, 0, past, ck, cv, rows, 0.07)
+    ref = oracle.attention_f32kv(q, nh, nkv, hd, pk, pv, 0, past, ck, cv, rows, 0.07)
+    assert np.abs(got - ref).max() <= 2e-5 * max(np.abs(pv).max(), np.abs(cv).max()) + np.abs(ref).max() * 2.0 ** -23
+
+
+def test_attention_f32kv_empty_and_errors(ops):
+    from fellm_amd import _lib
+
+    rng = np.random.default_rng(5)
+    q = rng.normal(size=(2, 4 * 64)).astype(np.float32)
+    k = rng.normal(size=(8, 2 * 64)).astype(np.float32)
+    assert not _f32kv(ops, q, 4, 2, 64, k, k, 3, 3).any()  # no keys: zero rows
+    lib = _lib.lib()
+    x = torch.zeros(4096, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.fellm_rocm_attention_f32kv(x.data_ptr(), x.data_ptr(), 1, 4, 3, 64, x.data_ptr(), x.data_ptr(), 0, 1,
+                                          None, None, 0, 0.0, s) == -2  # heads not a multiple of KV heads
+    assert lib.fellm_rocm_attention_f32kv(x.data_ptr(), x.data_ptr(), 1, 32, 1, 128, x.data_ptr(), x.data_ptr(), 0,
+                                          1, None, None, 0, 0.0, s) == -2  # 32 heads per KV head

@@ -5,6 +5,10 @@
 * the device sinf/cosf restatement (RoPE's per-row sin/cos table) against
   the host's glibc sinf and cosf (f32::sin_cos, kernels/rope.rs:46-58), all
   2^32 inputs;
+* the device logf restatement (sqrt-softplus router gating) against the
+  host's glibc logf, all 2^32 inputs;
+* the device correctly rounded sqrtf against numpy's IEEE float32 sqrt, all
+  2^32 inputs;
 * SwiGLU's silu(g) = g / (1 + exp(-g)) (kernels/swiglu.rs:5-7) through the
   product kernel with up = 1, against the oracle, all 2^32 values of g.
   silu depends on g alone, so this proves the kernel's exp + division path
@@ -40,6 +44,15 @@ def _host_expf(start: int) -> np.ndarray:
 def _host_sincosf(start: int) -> np.ndarray:
     s, c = oracle.sincosf(_bits(start))
     return np.concatenate([s, c])
+
+
+def _host_logf(start: int) -> np.ndarray:
+    return oracle.logf(_bits(start))
+
+
+def _host_sqrtf(start: int) -> np.ndarray:
+    with np.errstate(invalid="ignore"):
+        return np.sqrt(_bits(start))
 
 
 def _host_silu(start: int) -> np.ndarray:
@@ -97,3 +110,21 @@ def test_sincosf_all_inputs(dev):
         return torch.cat([s, c]).cpu().numpy()
 
     _sweep(dev_fn, _host_sincosf, "sincosf")
+
+
+def test_logf_all_inputs(dev):
+    from fellm_amd import ops
+
+    def dev_fn(start):
+        return ops.logf(torch.from_numpy(_bits(start)).to(dev)).cpu().numpy()
+
+    _sweep(dev_fn, _host_logf, "logf")
+
+
+def test_sqrtf_all_inputs(dev):
+    from fellm_amd import ops
+
+    def dev_fn(start):
+        return ops.sqrtf(torch.from_numpy(_bits(start)).to(dev)).cpu().numpy()
+
+    _sweep(dev_fn, _host_sqrtf, "sqrtf")

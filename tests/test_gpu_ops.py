@@ -45,6 +45,20 @@ def test_device_expf_matches_glibc(ops, dev):
     assert_exact(got[~nan], ref[~nan], "expf")
 
 
+def test_device_logf_matches_glibc(ops, dev):
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 2**32, size=1 << 22, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0.0, -0.0, 1.0, -1.0, 1e-45, 1e-38, 1.17549435e-38, 3.4e38, np.inf, -np.inf, np.nan, 2.0,
+                        0.5, 1.0000001, 0.99999994], np.float32)
+    dense = np.linspace(0.5, 4.0, 1 << 20, dtype=np.float32)
+    x = np.concatenate([bits.view(np.float32), special, dense])
+    got = from_dev(ops.logf(torch.from_numpy(x).to(dev)))
+    ref = oracle.logf(x)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_exact(got[~nan], ref[~nan], "logf")
+
+
 def test_device_sincosf_matches_glibc(ops, dev):
     """RoPE's sin/cos table entries: every reduction path (|x| < 2^-12, < pi/4,
     < 120, Payne-Hanek) and the RoPE angle range, bit for bit."""
@@ -400,7 +414,8 @@ def test_kv_write_out_of_range_flags(ops, dev):
 
 # ---- Router --------------------------------------------------------------------
 @pytest.mark.parametrize("n_exp,k", [(128, 8), (64, 6), (256, 8), (512, 32), (60, 1), (128, 128)])
-@pytest.mark.parametrize("gating,norm,rsf", [(1, True, 0.0), (2, False, 2.5), (1, False, 1.0)])
+@pytest.mark.parametrize("gating,norm,rsf", [(1, True, 0.0), (2, False, 2.5), (1, False, 1.0), (4, True, 0.0),
+                                             (4, False, 2.5)])
 def test_router_topk(ops, dev, n_exp, k, gating, norm, rsf):
     rng = np.random.default_rng(n_exp * 100 + k)
     tokens = 1023

@@ -184,6 +184,42 @@ def test_rope_uses_paged_row_positions(host):
     assert_exact(materialize(host, y, D.F32), oracle.rope(x, nh, hd, hd, 0, inv, None, position0=40), "plugin rope pos0")
 
 
+def test_rope_pre_rope_write_request_rotates(host):
+    """custom_op_id 1 (backend.rs:1152-1158) asks for the pre-rotation rows to
+    be captured; the plugin has no channel to the host's store (neither has the
+    CUDA plugin), so the launch must still rotate exactly as without it."""
+    rng = np.random.default_rng(13)
+    nh, hd = 4, 64
+    x = rng.normal(size=(5, nh * hd)).astype(np.float32)
+    inv = oracle.rope_inv_freqs(500000.0, hd)
+    y = np.zeros_like(x)
+    run(host, abi.OpKind.ROPE, [D.F32, D.F32], D.F32,
+        abi.OpAttrs(n_heads=nh, head_dim=hd, rope_dim=hd, position=7, custom_op_id=1, layer_ord=2),
+        [tref(x, D.F32), tref(inv, D.F32)], [tmut(y, D.F32)])
+    assert_exact(materialize(host, y, D.F32), oracle.rope(x, nh, hd, hd, 0, inv, None, position0=7), "pre-rope")
+
+
+def test_rejected_launch_keeps_output_mirror(host):
+    """An output that is valid only on the device stays valid when a later
+    launch writing it is rejected before its kernel runs."""
+    from fellm_amd.plugin_host import PluginError
+
+    rng = np.random.default_rng(14)
+    g = rng.normal(size=512).astype(np.float32)
+    u = rng.normal(size=512).astype(np.float32)
+    y = np.zeros(512, np.float32)
+    run(host, abi.OpKind.SILU_GATE, [D.F32, D.F32], D.F32, abi.OpAttrs(), [tref(g, D.F32), tref(u, D.F32)],
+        [tmut(y, D.F32)])
+    inv = oracle.rope_inv_freqs(10000.0, 128)  # enough frequencies for rope_dim 128
+    h = host.lookup(abi.OpKind.ROPE, [D.F32, D.F32], D.F32)
+    with pytest.raises(PluginError) as e:  # rope_dim > head_dim: rejected by the kernel's shape check
+        host.launch(h, abi.OpAttrs(n_heads=8, head_dim=64, rope_dim=128), [tref(g, D.F32), tref(inv, D.F32)],
+                    [tmut(y, D.F32)])
+    assert e.value.code == -2
+    assert np.all(y == 0)
+    assert_exact(materialize(host, y, D.F32), oracle.silu_gate(g, u), "device copy kept")
+
+
 def test_kv_write_paged(host):
     rng = np.random.default_rng(4)
     batch, nkv, hd, bs, n_blocks = 9, 2, 64, 16, 32
@@ -383,6 +419,52 @@ def test_attention_paged_batch(host):
     for r in range(len(lengths)):
         tol = 2e-5 * np.abs(v16[r]).max() + np.abs(ref[r]) * 2.0 ** -23
         assert np.all(np.abs(got[r] - ref[r]) <= tol), (r, np.abs(got[r] - ref[r]).max())
+
+
+@pytest.mark.parametrize("window,mode", [(0, 0), (16, 0), (16, 1)])
+def test_attention_contiguous_decode(host, window, mode):
+    """Attention [F32, F32, F32] with block_size 0: one query row against keys
+    0..past_len of host K/V (backend.rs:1371-1397); a window keeps the last
+    `window` keys when causal, the first ones otherwise (attention_provider.rs:
+    305-318 for one query row)."""
+    rng = np.random.default_rng(31 + window + mode)
+    nh, nkv, hd, past = 32, 8, 128, 200
+    q = rng.normal(size=nh * hd).astype(np.float32)
+    k = rng.normal(size=(256, nkv * hd)).astype(np.float32)  # capacity 256 rows, past + 1 used
+    v = rng.normal(size=(256, nkv * hd)).astype(np.float32)
+    out = np.zeros_like(q)
+    run(host, abi.OpKind.ATTENTION, [D.F32, D.F32, D.F32], D.F32,
+        abi.OpAttrs(n_heads=nh, n_kv_heads=nkv, head_dim=hd, past_len=past, block_size=0, attention_window=window,
+                    attention_mode=mode),
+        [tref(q, D.F32), tref(k, D.F32), tref(v, D.F32)], [tmut(out, D.F32)])
+    seq = past + 1
+    b, e = 0, seq
+    if window:
+        b, e = (seq - window, seq) if mode == 0 else (0, window)
+    ref = oracle.attention_f32kv(q[None], nh, nkv, hd, k, v, b, e)[0]
+    got = materialize(host, out, D.F32)
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(v).max() + np.abs(ref).max() * 2.0 ** -23
+
+
+def test_attention_canvas(host):
+    """Attention [F32 x 5] in canvas mode (attention_mode 1): query_len rows,
+    each attending the prefix keys [past - window, past) of inputs 1, 2 and
+    every canvas key of inputs 3, 4 (backend.rs:1412-1535)."""
+    rng = np.random.default_rng(41)
+    nh, nkv, hd, rows, past, window = 8, 2, 64, 12, 50, 20
+    q = rng.normal(size=(rows, nh * hd)).astype(np.float32)
+    pk = rng.normal(size=(past, nkv * hd)).astype(np.float32)
+    pv = rng.normal(size=(past, nkv * hd)).astype(np.float32)
+    ck = rng.normal(size=(rows, nkv * hd)).astype(np.float32)
+    cv = rng.normal(size=(rows, nkv * hd)).astype(np.float32)
+    out = np.zeros_like(q)
+    attrs = abi.OpAttrs(n_heads=nh, n_kv_heads=nkv, head_dim=hd, past_len=past, attention_mode=1, query_len=rows,
+                        attention_window=window)
+    run(host, abi.OpKind.ATTENTION, [D.F32] * 5, D.F32, attrs,
+        [tref(q, D.F32), tref(pk, D.F32), tref(pv, D.F32), tref(ck, D.F32), tref(cv, D.F32)], [tmut(out, D.F32)])
+    ref = oracle.attention_f32kv(q, nh, nkv, hd, pk, pv, past - window, past, ck, cv, rows)
+    got = materialize(host, out, D.F32)
+    assert np.abs(got - ref).max() <= 2e-5 * max(np.abs(pv).max(), np.abs(cv).max()) + np.abs(ref).max() * 2.0 ** -23
 
 
 def test_cast_converts_on_device(host):

@@ -384,6 +384,10 @@ def _brute_router(logits, k, gating, norm, rsf):
         l = logits[i]
         if gating == 2:
             s = (np.float32(1) / (np.float32(1) + oracle.expf(-l))).astype(np.float32)
+        elif gating == 4:  # moe.rs:68-77
+            sp = np.where(l > 20, l, np.where(l < -20, oracle.expf(l),
+                                               oracle.logf((np.float32(1) + oracle.expf(l)).astype(np.float32))))
+            s = np.sqrt(np.maximum(sp.astype(np.float32), np.float32(0))).astype(np.float32)
         else:
             m = np.float32(max(l))
             ex = oracle.expf((l - m).astype(np.float32))
@@ -404,7 +408,8 @@ def _brute_router(logits, k, gating, norm, rsf):
     return ids, w
 
 
-@pytest.mark.parametrize("gating,norm,rsf", [(1, True, 0.0), (2, False, 2.5), (1, False, 1.0)])
+@pytest.mark.parametrize("gating,norm,rsf", [(1, True, 0.0), (2, False, 2.5), (1, False, 1.0), (4, True, 2.5),
+                                             (4, False, 0.0)])
 def test_router_brute_force(gating, norm, rsf):
     rng = np.random.default_rng(7)
     logits = rng.normal(size=(40, 16)).astype(np.float32)
@@ -417,6 +422,36 @@ def test_router_brute_force(gating, norm, rsf):
     assert ids[0].tolist() == [0, 1, 2, 3]
     if norm and gating == 1:
         assert np.allclose(w.sum(axis=1), 1.0, atol=1e-6)
+
+
+def test_router_sqrt_softplus_closed_forms():
+    """gating 4 (moe.rs:68-77): sqrt(v) above 20, sqrt(exp(v)) below -20,
+    sqrt(ln 2) at 0, and a float64 recomputation in between."""
+    l = np.array([[25.0, -25.0, 0.0, 3.0, -3.0, 20.0, -20.0, np.nan]], np.float32)
+    ids, w = oracle.router(l, 8, 4, False, 0.0)
+    s = dict(zip(ids[0].tolist(), w[0].tolist()))
+    assert s[0] == np.float32(np.sqrt(np.float32(25.0)))
+    assert s[1] == np.float32(np.sqrt(oracle.expf(np.array([-25.0], np.float32))[0]))
+    assert abs(s[2] - np.sqrt(np.log(2.0))) < 1e-7
+    for e, v in ((3, 3.0), (4, -3.0), (5, 20.0), (6, -20.0)):
+        # the f32 sum 1 + exp(v) is rounded before the log, as in the reference
+        one_plus = float(np.float32(1) + oracle.expf(np.array([v], np.float32))[0])
+        want = np.sqrt(np.log(one_plus))
+        assert abs(s[e] - want) <= 3e-7 * want
+    assert s[7] == 0.0  # NaN: max(NaN, 0) is 0, as f32::max
+    assert ids[0][0] == 0
+
+
+def test_oracle_logf_is_libm():
+    import ctypes
+    import ctypes.util
+
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.logf.restype = ctypes.c_float
+    libm.logf.argtypes = [ctypes.c_float]
+    x = np.concatenate([np.geomspace(1e-40, 1e38, 997), [1.0, 0.0, 2.0]]).astype(np.float32)
+    got = oracle.logf(x)
+    assert all(got[i] == np.float32(libm.logf(float(x[i]))) for i in range(x.size))
 
 
 def test_router_k_clamped_and_sigmoid_monotone():

@@ -155,3 +155,58 @@ def test_reference_decode_inputs():
     v = [vf.reshape(kv_len, n_kv * hd)]
     got, ref, v16 = run(q.reshape(1, -1), k, v, n_heads, n_kv, hd, float(np.float32(1.0 / np.sqrt(8.0))))
     assert np.abs(got - ref).max() < 1e-6
+
+
+# ---- non-paged attention (contiguous decode, canvas) ------------------------------
+def _f64_attention(q, n_heads, n_kv, hd, keys, vals, scale):
+    """float64 softmax attention of every query row over the key list."""
+    rows = q.shape[0]
+    out = np.zeros((rows, n_heads * hd))
+    g = n_heads // n_kv
+    for r in range(rows):
+        for h in range(n_heads):
+            kh = h // g
+            qh = q[r, h * hd:(h + 1) * hd].astype(np.float64)
+            if len(keys) == 0:
+                continue
+            K = keys[:, kh * hd:(kh + 1) * hd].astype(np.float64)
+            V = vals[:, kh * hd:(kh + 1) * hd].astype(np.float64)
+            s = K @ qh * scale
+            p = np.exp(s - s.max())
+            out[r, h * hd:(h + 1) * hd] = (p / p.sum()) @ V
+    return out
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,seq", [(8, 2, 64, 37), (32, 8, 128, 300), (4, 4, 80, 5), (16, 1, 128, 1)])
+def test_attention_f32kv_matches_f64(n_heads, n_kv, hd, seq):
+    rng = np.random.default_rng(seq + hd)
+    q = rng.normal(size=(1, n_heads * hd)).astype(np.float32)
+    k = rng.normal(size=(seq, n_kv * hd)).astype(np.float32)
+    v = rng.normal(size=(seq, n_kv * hd)).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    got = oracle.attention_f32kv(q, n_heads, n_kv, hd, k, v, 0, seq)
+    ref = _f64_attention(q, n_heads, n_kv, hd, k, v, scale)
+    assert np.abs(got - ref).max() <= 2e-6 * max(1.0, np.abs(v).max())
+
+
+def test_attention_f32kv_closed_forms_and_segments():
+    rng = np.random.default_rng(21)
+    nh, nkv, hd = 4, 2, 64
+    q = rng.normal(size=(3, nh * hd)).astype(np.float32)
+    k = rng.normal(size=(20, nkv * hd)).astype(np.float32)
+    v = rng.normal(size=(20, nkv * hd)).astype(np.float32)
+    # one key: the output is that key's V row, exactly
+    one = oracle.attention_f32kv(q[:1], nh, nkv, hd, k, v, 7, 8)
+    for h in range(nh):
+        assert np.array_equal(one[0, h * hd:(h + 1) * hd], v[7, (h // 2) * hd:(h // 2 + 1) * hd])
+    # q = 0: uniform weights, the mean of V
+    z = oracle.attention_f32kv(np.zeros((1, nh * hd), np.float32), nh, nkv, hd, k, v, 0, 20)
+    assert np.allclose(z[0, :hd], v[:, :hd].mean(axis=0), atol=1e-6)
+    # no keys: zero rows
+    assert not oracle.attention_f32kv(q, nh, nkv, hd, k, v, 5, 5).any()
+    # two segments == one concatenated segment (canvas = prefix keys then canvas keys)
+    two = oracle.attention_f32kv(q, nh, nkv, hd, k[:12], v[:12], 4, 12, k[12:], v[12:], 8)
+    cat = oracle.attention_f32kv(q, nh, nkv, hd, k[4:], v[4:], 0, 16)
+    assert np.array_equal(two, cat)
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    assert np.abs(two - _f64_attention(q, nh, nkv, hd, k[4:], v[4:], scale)).max() < 2e-6 * np.abs(v).max()
