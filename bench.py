@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     ap.add_argument("--suite", action="store_true", help="per-op table for every config")
+    ap.add_argument("--reps", type=int, default=0, help="per-op timing reps (default max(steps, 50))")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the same-run copy-ceiling probes")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 512 MiB device copy (PMC byte-counter calibration)")
     return ap.parse_args()
@@ -903,11 +905,12 @@ def main():
             if args.only and name not in args.only.split(","):
                 continue
             chain, sets, _ = make(torch, ops, dev, args.sets)
-            _, per_op = run_chain(torch, chain, sets, args.steps, args.warmup)
+            _, per_op = run_chain(torch, chain, sets, args.steps, args.warmup, args.reps or None)
             result[name] = op_report(per_op)
             del sets
             torch.cuda.empty_cache()
-            for op_name, c in measure_ceilings(torch, chain, max(args.steps, 50)).items():
+            ceilings = {} if args.no_ceiling else measure_ceilings(torch, chain, args.reps or max(args.steps, 50))
+            for op_name, c in ceilings.items():
                 result[name][op_name].update(c)
                 result[name][op_name]["frac_of_probe"] = round(result[name][op_name]["GBps"] / c["probe_GBps"], 4)
             del chain
@@ -918,11 +921,11 @@ def main():
         return
 
     chain, sets, T = c2_ops(torch, ops, dev, args.sets)
-    elapsed, per_op = run_chain(torch, chain, sets, args.steps, args.warmup)
+    elapsed, per_op = run_chain(torch, chain, sets, args.steps, args.warmup, args.reps or None)
     rep = op_report(per_op)
     del sets
     torch.cuda.empty_cache()
-    ceilings = measure_ceilings(torch, chain, max(args.steps, 50))
+    ceilings = {} if args.no_ceiling else measure_ceilings(torch, chain, args.reps or max(args.steps, 50))
     for name, c in ceilings.items():
         rep[name].update(c)
         rep[name]["frac_of_probe"] = round(rep[name]["GBps"] / c["probe_GBps"], 4)
