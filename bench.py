@@ -189,6 +189,11 @@ def c4_ops(torch, ops, dev, n_sets, seed=4):
                                                                    y_out=s["y"]), (2, B * H * 2, 2 * B * H * 2)),
         Op("swiglu", B * I * 2 * 3, lambda s: ops.silu_gate(s["gate"], s["up"], out=s["act"]), (2, B * I * 2, B * I * 2)),
     ]
+    # The same three ops in one launch (fellm_rocm_decode_step).
+    chain.append(Op("decode_step_fused", sum(op.nbytes for op in chain),
+                    lambda s: ops.decode_step(s["q"], s["k"], s["v"], inv, s["pos"], s["cache"], s["x"], s["r"], w, 1e-5,
+                                              s["gate"], s["up"], head_dim=hd, q_out=s["qo"], h_out=s["h"],
+                                              y_out=s["y"], act_out=s["act"])))
     return chain, sets, B
 
 
@@ -430,7 +435,10 @@ def decode_graph_report(torch, ops, dev, steps, warmup):
     out = {}
     chain, sets, _ = c4_ops(torch, ops, dev, 1)
     st = sets[0]
-    out["c4_decode_step_b256"] = time_eager_vs_graph(torch, lambda: [op.fn(st) for op in chain], steps, warmup)
+    sep = [op for op in chain if op.name != "decode_step_fused"]
+    fused = [op for op in chain if op.name == "decode_step_fused"][0]
+    out["c4_decode_step_b256"] = time_eager_vs_graph(torch, lambda: [op.fn(st) for op in sep], steps, warmup)
+    out["c4_decode_step_b256_one_launch"] = time_eager_vs_graph(torch, lambda: fused.fn(st), steps, warmup)
     del chain, sets, st
     torch.cuda.empty_cache()
 

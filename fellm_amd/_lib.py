@@ -42,6 +42,20 @@ class FellmRocmPagedKv(C.Structure):
     ]
 
 
+class FellmRocmDecodeStep(C.Structure):
+    """Mirror of FellmRocmDecodeStep (include/fellm_rocm.h)."""
+
+    _fields_ = [
+        ("act_dtype", U32),
+        ("q", P), ("q_out", P), ("n_q_heads", U32), ("k", P), ("k_out", P), ("v", P), ("n_kv_heads", U32),
+        ("batch", U32), ("head_dim", U32), ("rope_dim", U32), ("pairing", U32), ("inv_freqs", P),
+        ("rope_positions", P), ("kv_positions", P), ("kv", C.POINTER(FellmRocmPagedKv)), ("err_flag", P),
+        ("x", P), ("residual", P), ("h_out", P), ("norm_weight", P), ("group", U32), ("y", P), ("norm_elems", U64),
+        ("eps", F32),
+        ("gate", P), ("up", P), ("act_out", P), ("swiglu_elems", U64),
+    ]
+
+
 _SIGNATURES = {
     "fellm_rocm_version": (C.c_char_p, []),
     "fellm_rocm_add_rmsnorm": (I32, [P, P, P, U32, P, U32, P, U32, U64, F32, P]),
@@ -61,6 +75,7 @@ _SIGNATURES = {
     "fellm_rocm_mathf": (I32, [U32, P, P, U64, P]),
     "fellm_rocm_timing_arm": (I32, [P, P]),
     "fellm_rocm_attention_f32kv": (I32, [P, P, U32, U32, U32, U32, P, P, U32, U32, P, P, U32, F32, P]),
+    "fellm_rocm_decode_step": (I32, [C.POINTER(FellmRocmDecodeStep), P]),
     "fellm_rocm_stream_probe": (I32, [P, P, U64, P, U64, U32, P]),
     "fellm_rocm_timing_disarm": (None, []),
     "fellm_rocm_silu_fast_bound": (I32, [P, P]),

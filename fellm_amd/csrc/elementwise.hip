@@ -17,32 +17,10 @@
 // the exact one is bounded over every input decides the rounded output
 // whenever the interval it implies holds a single 16-bit value
 // (silu_mul_fast, common.hpp); the rest take the exact path.
-#include "common.hpp"
+#include "swiglu_body.hpp"
 
 namespace fellm {
 namespace {
-
-constexpr int kEwBlock = 256;
-
-// Build knob: 16-bit outputs take the interval fast path of silu_mul_fast (1).
-#ifndef FELLM_SWIGLU_FAST
-#define FELLM_SWIGLU_FAST 1
-#endif
-
-// Non-temporal store of VEC already-rounded output elements.
-template <typename O, int VEC>
-__device__ __forceinline__ void store_raw_nt(typename O::T *p, const typename O::T (&v)[VEC]) {
-    using P = Pack<typename O::T, VEC>;
-    constexpr int W = sizeof(P) / 4;
-    P pk;
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) pk.v[i] = v[i];
-    uint32_t w[W];
-    memcpy(w, &pk, sizeof(P));
-    uint32_t *dst = reinterpret_cast<uint32_t *>(p);
-#pragma unroll
-    for (int i = 0; i < W; ++i) __builtin_nontemporal_store(w[i], dst + i);
-}
 
 inline uint32_t ew_grid(uint64_t units) {
     uint64_t g = (units + kEwBlock - 1) / kEwBlock;
@@ -54,49 +32,9 @@ inline uint32_t ew_grid(uint64_t units) {
 template <typename I, typename O, int VEC, int UNROLL>
 __global__ __launch_bounds__(kEwBlock) void silu_gate_kernel(const typename I::T *__restrict__ g,
                                                              const typename I::T *__restrict__ u,
-                                                             typename O::T *__restrict__ out,
-                                                             uint64_t n) {
+                                                             typename O::T *__restrict__ out, uint64_t n) {
     __shared__ uint64_t tab_lds[32];
-    const uint64_t *tab = stage_expf_table(tab_lds);
-    const uint64_t nvec = n / VEC;
-    const uint64_t stride = (uint64_t)gridDim.x * kEwBlock * UNROLL;
-    for (uint64_t base = (uint64_t)blockIdx.x * kEwBlock * UNROLL + threadIdx.x; base < nvec; base += stride) {
-        float gv[UNROLL][VEC], uv[UNROLL][VEC];
-#pragma unroll
-        for (int j = 0; j < UNROLL; ++j) {
-            const uint64_t i = base + (uint64_t)j * kEwBlock;
-            if (i < nvec) {
-                load_f32_nt<I, VEC>(g + i * VEC, gv[j]);
-                load_f32_nt<I, VEC>(u + i * VEC, uv[j]);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < UNROLL; ++j) {
-            const uint64_t i = base + (uint64_t)j * kEwBlock;
-            if (i < nvec) {
-                if constexpr (FELLM_SWIGLU_FAST && sizeof(typename O::T) == 2 && VEC % 2 == 0) {
-                    // The exact silu runs only for the elements (and only in
-                    // the wavefronts) whose rounding the interval leaves open.
-                    typename O::T o[VEC];
-#pragma unroll
-                    for (int k = 0; k < VEC; ++k)
-                        if (__builtin_expect(!silu_mul_fast<O>(gv[j][k], uv[j][k], o[k]), 0))
-                            o[k] = O::store(silu(gv[j][k], tab) * uv[j][k]);
-                    store_raw_nt<O, VEC>(out + i * VEC, o);
-                } else {
-                    float o[VEC];
-#pragma unroll
-                    for (int k = 0; k < VEC; ++k) o[k] = silu(gv[j][k], tab) * uv[j][k];
-                    store_f32_nt<O, VEC>(out + i * VEC, o);
-                }
-            }
-        }
-    }
-    // Tail (n % VEC elements), handled by the first threads of block 0.
-    if (blockIdx.x == 0) {
-        const uint64_t t = nvec * VEC + threadIdx.x;
-        if (t < n) out[t] = O::store(silu(I::load(g[t]), tab) * I::load(u[t]));
-    }
+    silu_gate_blocks<I, O, VEC, UNROLL>(g, u, out, n, blockIdx.x, gridDim.x, tab_lds);
 }
 
 template <typename I, typename O, int VEC>

@@ -11,11 +11,8 @@
 // read exactly once and h and y written exactly once: 4 row-passes of HBM
 // traffic with the residual fused (the unfused graph needs 6).
 // The sum of squares is one wavefront shuffle reduction plus one LDS exchange.
-#include "common.hpp"
+#include "norm_body.hpp"
 
-#ifndef FELLM_NORM_W_EARLY
-#define FELLM_NORM_W_EARLY 1
-#endif
 // Build knob: with many rows, rows of at most FELLM_NORM_WAVE_BYTES bytes
 // take one wavefront per row instead of one workgroup per row (0: never).
 // Measured on MI355X inside the op chains: 16384 x 2048 bf16 RMSNorm
@@ -35,84 +32,14 @@
 
 namespace fellm {
 
-// x and residual are read once with non-temporal loads, and h and y are
-// written with non-temporal stores.  For the many-row (prefill) layout
-// regular stores make this kernel alone faster (26.7 vs 28.4 us at
-// 4096 x 4096 f16) but leave 67 MB of dirty lines that the next kernel pays
-// to write back; judged on a whole chain the non-temporal stores win
-// (embedding -> add+RMSNorm -> RoPE -> SwiGLU at T 4096: 123.0 -> 116.4 us).
-template <typename A, int N>
-__device__ __forceinline__ void norm_load(const typename A::T *p, float (&v)[N]) {
-    load_f32_nt<A, N>(p, v);
-}
-template <typename A, int N, bool NT>
-__device__ __forceinline__ void norm_store(typename A::T *p, const float (&v)[N]) {
-    if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
-}
 namespace {
 
 template <typename A, typename O, int BLOCK, int VEC, int NCHUNK, bool ADD, bool STORE_H>
-__global__ __launch_bounds__(BLOCK) void add_rmsnorm_kernel(
-    // h may alias x or r (in-place residual update): no __restrict__ on them.
-    const typename A::T *x, const typename A::T *r, typename A::T *h, const float *__restrict__ w,
-    typename O::T *y, uint32_t group, float eps) {
+__global__ __launch_bounds__(BLOCK) void add_rmsnorm_kernel(const typename A::T *x, const typename A::T *r,
+                                                            typename A::T *h, const float *__restrict__ w,
+                                                            typename O::T *y, uint32_t group, float eps) {
     __shared__ float red[BLOCK / kWave];
-    const size_t row = blockIdx.x;
-    const typename A::T *xr = x + row * group;
-    float v[NCHUNK][VEC];
-    float ss = 0.0f;
-    // Every chunk's x and r are requested before the first h store: h may
-    // alias x or r, so the compiler cannot move a later chunk's loads above
-    // an earlier chunk's store by itself, which would expose one memory
-    // latency per chunk.
-    float rv[ADD ? NCHUNK : 1][VEC];
-#pragma unroll
-    for (int c = 0; c < NCHUNK; ++c) {
-        const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
-        if (base < group) {
-            norm_load<A, VEC>(xr + base, v[c]);
-            if constexpr (ADD) norm_load<A, VEC>(r + row * group + base, rv[c]);
-        }
-    }
-#pragma unroll
-    for (int c = 0; c < NCHUNK; ++c) {
-        const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
-        if (base < group) {
-            if constexpr (ADD) {
-#pragma unroll
-                for (int i = 0; i < VEC; ++i) {
-                    // h is stored in the activation dtype and normalised as stored.
-                    v[c][i] = A::load(A::store(v[c][i] + rv[c][i]));
-                }
-                if constexpr (STORE_H) norm_store<A, VEC, true>(h + row * group + base, v[c]);
-            }
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) ss += v[c][i] * v[c][i];
-        }
-    }
-    // The weights do not depend on the reduction: with FELLM_NORM_W_EARLY they
-    // are requested before the barrier, so their (cache) latency overlaps it.
-    float wv[NCHUNK][VEC];
-    if constexpr (FELLM_NORM_W_EARLY) {
-#pragma unroll
-        for (int c = 0; c < NCHUNK; ++c) {
-            const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
-            if (base < group) load_f32<F32, VEC>(w + base, wv[c]);
-        }
-    }
-    ss = block_sum<BLOCK>(ss, red);
-    const float scale = 1.0f / sqrtf(ss / (float)group + eps);
-#pragma unroll
-    for (int c = 0; c < NCHUNK; ++c) {
-        const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
-        if (base < group) {
-            float o[VEC];
-            if constexpr (!FELLM_NORM_W_EARLY) load_f32<F32, VEC>(w + base, wv[c]);
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) o[i] = (v[c][i] * scale) * wv[c][i];
-            norm_store<O, VEC, true>(y + row * group + base, o);
-        }
-    }
+    add_rmsnorm_row<A, O, BLOCK, VEC, NCHUNK, ADD, STORE_H>(x, r, h, w, y, group, eps, blockIdx.x, red);
 }
 
 // One wavefront per row, four rows per workgroup, for rows of at most 8 KB

@@ -21,6 +21,8 @@
 #include <initializer_list>
 
 #include "common.hpp"
+#include "norm_body.hpp"
+#include "swiglu_body.hpp"
 
 // Build knob: non-temporal activation loads (bit 0) and stores (bit 1).
 #ifndef FELLM_ROPE_NT
@@ -204,20 +206,21 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
 // Each workgroup handles R consecutive rows: all threads first fill the
 // R x rope_dim/2 (sin, cos) table (one barrier), then stream every item of
 // the R rows.
+// The work of workgroup `bid` of a RoPE launch (every thread calls it;
+// contains a barrier).  cs_all / kbase_all: the LDS tables below.
 template <typename A, typename C, int PV, int MODE, int R>
-__global__ __launch_bounds__(kRopeBlock) void rope_kernel(
+__device__ __forceinline__ void rope_block(
     // x1/out1 and x2/out2 may alias (in-place rotation): no __restrict__.
     const typename A::T *x1, typename A::T *out1, uint32_t nh1,
     const typename A::T *x2, typename A::T *out2, uint32_t nh2,
     const typename A::T *__restrict__ x3, uint32_t rows, uint32_t head_dim, uint32_t rope_dim, uint32_t pairing,
     const float *__restrict__ inv_freqs, const uint32_t *__restrict__ rope_pos, uint32_t pos0,
-    const uint32_t *__restrict__ kv_pos, KvDev kv, uint32_t *__restrict__ err, uint32_t hsplit) {
-    __shared__ float2 cs_all[R][kMaxHalf / R];
-    __shared__ uint64_t kbase_all[R];
+    const uint32_t *__restrict__ kv_pos, const KvDev &kv, uint32_t *__restrict__ err, uint32_t hsplit, uint32_t bid,
+    float2 (*cs_all)[kMaxHalf / R], uint64_t *kbase_all) {
     // hsplit workgroups share a row group, each taking a contiguous range of
     // its (q, k, v) heads.
-    const uint32_t part = blockIdx.x % hsplit;
-    const uint32_t row0 = blockIdx.x / hsplit * R;
+    const uint32_t part = bid % hsplit;
+    const uint32_t row0 = bid / hsplit * R;
     const uint32_t half = rope_dim / 2;
     for (uint32_t t = threadIdx.x; t < R * half; t += kRopeBlock) {
         const uint32_t rr = t / half, i = t % half;
@@ -303,6 +306,18 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
                                         pairing, n_rot, cs_all[rr], e, kbase_all[rr], kv, v_off);
         }
     }
+}
+
+template <typename A, typename C, int PV, int MODE, int R>
+__global__ __launch_bounds__(kRopeBlock) void rope_kernel(
+    const typename A::T *x1, typename A::T *out1, uint32_t nh1, const typename A::T *x2, typename A::T *out2,
+    uint32_t nh2, const typename A::T *__restrict__ x3, uint32_t rows, uint32_t head_dim, uint32_t rope_dim,
+    uint32_t pairing, const float *__restrict__ inv_freqs, const uint32_t *__restrict__ rope_pos, uint32_t pos0,
+    const uint32_t *__restrict__ kv_pos, KvDev kv, uint32_t *__restrict__ err, uint32_t hsplit) {
+    __shared__ float2 cs_all[R][kMaxHalf / R];
+    __shared__ uint64_t kbase_all[R];
+    rope_block<A, C, PV, MODE, R>(x1, out1, nh1, x2, out2, nh2, x3, rows, head_dim, rope_dim, pairing, inv_freqs,
+                                  rope_pos, pos0, kv_pos, kv, err, hsplit, blockIdx.x, cs_all, kbase_all);
 }
 
 // Rows per workgroup.  Measured on MI355X (q+k, 32/8 heads, hd 128): at
@@ -508,6 +523,187 @@ extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q
                 return launch_status();
             };
             return vec ? go.template operator()<4>() : go.template operator()<1>();
+        });
+    });
+}
+
+// ---------------------------------------------------------------------------
+// One decode step's three memory-bound ops in one launch.  At decode batch
+// sizes each op moves 10-44 MB, a few microseconds of traffic, and as
+// separate kernels each pays its own fill and drain.  Here the grid is the
+// concatenation of the three launches' grids, workgroup ranges in order:
+//   [0, nb_rope)                RoPE(q), RoPE(k) + paged K/V append,
+//   [nb_rope, + rows)           residual add + RMSNorm, one row each,
+//   [.., + nb_silu)             SwiGLU,
+// each range running the same device code as its standalone kernel
+// (rope_block, add_rmsnorm_row, silu_gate_blocks), so the results are the
+// standalone launches' bit for bit, except y, whose sum of squares is
+// reduced over 256 threads here (the few-row standalone launch uses 1024).  The ops are independent (disjoint
+// outputs), as in the reference's decode graph before attention
+// (crates/fellm-model/src/graph.rs:2136-2246).
+// ---------------------------------------------------------------------------
+#ifndef FELLM_STEP_ORDER
+#define FELLM_STEP_ORDER 0
+#endif
+
+namespace fellm {
+namespace {
+
+template <typename A>
+struct StepArgs {
+    using T = typename A::T;
+    // RoPE + K/V append
+    const T *q;
+    T *q_out;
+    const T *k;
+    T *k_out;
+    const T *v;
+    uint32_t nq, nkv, batch, head_dim, rope_dim, pairing, hsplit;
+    const float *inv_freqs;
+    const uint32_t *rope_pos, *kv_pos;
+    KvDev kv;
+    uint32_t *err;
+    // add + RMSNorm
+    const T *x, *r;
+    T *h, *y;
+    const float *w;
+    uint32_t group;
+    float eps;
+    // SwiGLU
+    const T *gate, *up;
+    T *act;
+    uint64_t n_silu;
+    // workgroup ranges
+    uint32_t nb_rope, nb_norm, nb_silu;
+};
+
+template <typename A, typename C, int NCHUNK>
+__global__ __launch_bounds__(kRopeBlock) void decode_step_kernel(StepArgs<A> p) {
+    static_assert(kRopeBlock == 256 && kEwBlock == 256, "the three roles share one workgroup size");
+    __shared__ float2 cs_all[1][kMaxHalf];
+    __shared__ uint64_t kbase_all[1];
+    __shared__ float red[256 / kWave];
+    __shared__ uint64_t tab_lds[32];
+    // Role order along the grid (build knob FELLM_STEP_ORDER): 0 RoPE, norm,
+    // SwiGLU; 1 norm, RoPE, SwiGLU; 2 SwiGLU, RoPE, norm.
+    constexpr int kOrder[3][3] = {{0, 1, 2}, {1, 0, 2}, {2, 0, 1}};
+    const uint32_t nb[3] = {p.nb_rope, p.nb_norm, p.nb_silu};
+    uint32_t b = blockIdx.x;
+    int role = kOrder[FELLM_STEP_ORDER][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = kOrder[FELLM_STEP_ORDER][i];
+        if (b < nb[r]) {
+            role = r;
+            break;
+        }
+        b -= nb[r];
+    }
+    if (role == 0) {
+        rope_block<A, C, 4, 1, 1>(p.q, p.q_out, p.nq, p.k, p.k_out, p.nkv, p.v, p.batch, p.head_dim, p.rope_dim,
+                                  p.pairing, p.inv_freqs, p.rope_pos, 0u, p.kv_pos, p.kv, p.err, p.hsplit, b, cs_all,
+                                  kbase_all);
+    } else if (role == 1) {
+        add_rmsnorm_row<A, A, 256, 8, NCHUNK, true, true>(p.x, p.r, p.h, p.w, p.y, p.group, p.eps, b, red);
+    } else {
+        silu_gate_blocks<A, A, 8, 2>(p.gate, p.up, p.act, p.n_silu, b, p.nb_silu, tab_lds);
+    }
+}
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" int fellm_rocm_decode_step(const FellmRocmDecodeStep *d, void *stream) {
+    using namespace fellm;
+    if (!d) return FELLM_ERR_ARITY;
+    const uint32_t dt = d->act_dtype;
+    const size_t es = act_bytes(dt);
+    if (!es) return FELLM_ERR_DTYPE;
+    // The fused layout: 16-byte vectors everywhere, a residual and an h
+    // output, rows of 2049..16384 elements (256 threads, 2-8 chunks of 8), a
+    // SwiGLU length that is a whole number of 8-element vectors.
+    const bool norm_fits = d->residual && d->h_out && d->group && d->group % 8 == 0 && d->group > 2048 &&
+                           d->group <= 16384 && d->norm_elems % d->group == 0 && d->norm_elems / d->group <= 0x7fffffffull;
+    bool fuse = norm_fits && d->swiglu_elems % 8 == 0 && d->batch > 0 && d->kv &&
+                rope_vec_ok(d->head_dim, d->rope_dim, d->pairing, es, {d->q, d->q_out, d->k, d->k_out, d->v}) &&
+                aligned_to(d->kv->arena, 16) && d->kv->block_bytes % 16 == 0;
+    for (const void *p : {d->x, d->residual, (const void *)d->h_out, (const void *)d->y, d->gate, d->up,
+                          (const void *)d->act_out})
+        fuse = fuse && p && aligned_to(p, 16);
+    fuse = fuse && aligned_to(d->norm_weight, 32);
+    KvDev kv{};
+    if (fuse) {
+        if (!d->q || !d->q_out || !d->k || !d->v || !d->kv_positions || (d->rope_dim && !d->inv_freqs))
+            return FELLM_ERR_ARITY;
+        if (d->n_q_heads == 0 || d->n_kv_heads == 0) return FELLM_ERR_SHAPE;
+        if (int rc = check_rope_shape(d->head_dim, d->rope_dim, d->pairing)) return rc;
+        if (!make_kv(d->kv, kv) || kv.stride != d->n_kv_heads * d->head_dim) return FELLM_ERR_SHAPE;
+        if (!d->norm_weight || !d->y) return FELLM_ERR_ARITY;
+        if (d->swiglu_elems && (!d->gate || !d->up || !d->act_out)) return FELLM_ERR_ARITY;
+        if (d->kv->kv_dtype != FELLM_DTYPE_F16 && d->kv->kv_dtype != FELLM_DTYPE_BF16) return FELLM_ERR_DTYPE;
+    }
+    hipStream_t s = as_stream(stream);
+    if (!fuse) {  // the same three ops, launched separately
+        if (d->batch) {
+            if (int rc = fellm_rocm_rope_kv_write(d->q, d->q_out, d->n_q_heads, d->k, d->k_out, d->v, d->n_kv_heads, dt,
+                                                  d->batch, d->head_dim, d->rope_dim, d->pairing, d->inv_freqs,
+                                                  d->rope_positions, d->kv_positions, d->kv, d->err_flag, stream))
+                return rc;
+        }
+        if (d->norm_elems) {
+            if (int rc = fellm_rocm_add_rmsnorm(d->x, d->residual, d->h_out, dt, d->norm_weight, d->group, d->y, dt,
+                                                d->norm_elems, d->eps, stream))
+                return rc;
+        }
+        if (d->swiglu_elems) return fellm_rocm_silu_gate(d->gate, d->up, dt, d->act_out, dt, d->swiglu_elems, stream);
+        return FELLM_OK;
+    }
+    const uint32_t nchunk = (d->group / 8 + 255) / 256;  // 2..8
+    return dispatch_act(dt, [&]<typename A>() -> int {
+        return dispatch_cache(d->kv->kv_dtype, [&]<typename C>() -> int {
+            using T = typename A::T;
+            StepArgs<A> p{};
+            p.q = (const T *)d->q;
+            p.q_out = (T *)d->q_out;
+            p.k = (const T *)d->k;
+            p.k_out = (T *)d->k_out;
+            p.v = (const T *)d->v;
+            p.nq = d->n_q_heads;
+            p.nkv = d->n_kv_heads;
+            p.batch = d->batch;
+            p.head_dim = d->head_dim;
+            p.rope_dim = d->rope_dim;
+            p.pairing = d->pairing;
+            p.hsplit = rope_head_split(d->batch, d->n_q_heads + 2 * d->n_kv_heads);
+            p.inv_freqs = d->inv_freqs;
+            p.rope_pos = d->rope_positions;
+            p.kv_pos = d->kv_positions;
+            p.kv = kv;
+            p.err = d->err_flag;
+            p.x = (const T *)d->x;
+            p.r = (const T *)d->residual;
+            p.h = (T *)d->h_out;
+            p.y = (T *)d->y;
+            p.w = d->norm_weight;
+            p.group = d->group;
+            p.eps = d->eps;
+            p.gate = (const T *)d->gate;
+            p.up = (const T *)d->up;
+            p.act = (T *)d->act_out;
+            p.n_silu = d->swiglu_elems;
+            p.nb_rope = d->batch * p.hsplit;
+            p.nb_norm = (uint32_t)(d->norm_elems / d->group);
+            const uint64_t units = d->swiglu_elems / 8;
+            p.nb_silu = (uint32_t)((units + kEwBlock * 2 - 1) / (kEwBlock * 2));
+            const uint64_t grid = (uint64_t)p.nb_rope + p.nb_norm + p.nb_silu;
+            if (grid > 0x7fffffffull) return FELLM_ERR_SHAPE;
+            auto go = [&]<int NC>() -> int {
+                FELLM_LAUNCH((decode_step_kernel<A, C, NC>), dim3((uint32_t)grid), dim3(kRopeBlock), 0, s, p);
+                return launch_status();
+            };
+            if (nchunk <= 2) return go.template operator()<2>();
+            if (nchunk <= 4) return go.template operator()<4>();
+            return go.template operator()<8>();
         });
     });
 }

@@ -215,6 +215,31 @@ def rope_kv_write(q, k, v, inv_freqs, kv_positions, cache: PagedKvCache, *, head
     return q_out
 
 
+def decode_step(q, k, v, inv_freqs, kv_positions, cache: PagedKvCache, x, residual, norm_weight, eps: float,
+                gate, up, *, head_dim: int, rope_dim: int | None = None, pairing: int = 0, rope_positions=None,
+                layer: int = 0, q_out=None, k_out=None, h_out=None, y_out=None, act_out=None, err_flag=None):
+    """One launch for a decode step's RoPE(q, k) + paged K/V append, residual
+    add + RMSNorm and SwiGLU (fellm_rocm_decode_step).  Returns (q_out, h, y, act)."""
+    _dev(q, k, v, inv_freqs, kv_positions, rope_positions, x, residual, norm_weight, gate, up)
+    rope_dim = head_dim if rope_dim is None else rope_dim
+    batch = q.shape[0]
+    q_out = q_out if q_out is not None else torch.empty_like(q)
+    h_out = h_out if h_out is not None else torch.empty_like(x)
+    y_out = y_out if y_out is not None else torch.empty_like(x)
+    act_out = act_out if act_out is not None else torch.empty_like(gate)
+    kv = cache.c_struct(layer)
+    st = _lib.FellmRocmDecodeStep(
+        act_dtype=_code(q), q=_p(q), q_out=_p(q_out), n_q_heads=q.numel() // (batch * head_dim), k=_p(k),
+        k_out=_p(k_out), v=_p(v), n_kv_heads=k.numel() // (batch * head_dim), batch=batch, head_dim=head_dim,
+        rope_dim=rope_dim, pairing=pairing, inv_freqs=_p(inv_freqs), rope_positions=_p(rope_positions),
+        kv_positions=_p(kv_positions), kv=C.pointer(kv), err_flag=_p(err_flag),
+        x=_p(x), residual=_p(residual), h_out=_p(h_out), norm_weight=_p(norm_weight), group=norm_weight.numel(),
+        y=_p(y_out), norm_elems=x.numel(), eps=eps, gate=_p(gate), up=_p(up), act_out=_p(act_out),
+        swiglu_elems=gate.numel())
+    _lib.call("fellm_rocm_decode_step", C.byref(st), _stream())
+    return q_out, h_out, y_out, act_out
+
+
 def paged_attention(q, row_lengths, cache: PagedKvCache, *, n_heads: int, n_kv_heads: int, head_dim: int,
                     max_seq: int, layer: int = 0, scale: float = 0.0, causal: bool = True, window: int = 0,
                     out=None, out_dtype=None, workspace=None):

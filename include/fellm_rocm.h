@@ -140,6 +140,59 @@ int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q_heads, con
                              const FellmRocmPagedKv *kv, uint32_t *err_flag, void *stream);
 
 /*
+ * One decode step's memory-bound ops in a single launch: RoPE(q), RoPE(k) and
+ * the paged K/V append (fellm_rocm_rope_kv_write's arguments), residual add +
+ * RMSNorm with y in act_dtype (fellm_rocm_add_rmsnorm's), and SwiGLU
+ * (fellm_rocm_silu_gate's), all in act_dtype.
+ *   replaces: the decode graph's separate launches of these ops
+ *   (crates/fellm-model/src/graph.rs:2136-2246, :420-451, :1456-1510).
+ * Rotated q and k, the K/V slots, h and the SwiGLU output are bit for bit
+ * those of the three separate calls; y is within RMSNorm's tolerance of
+ * theirs (the fused row reduces its sum of squares over 256 threads, the
+ * standalone few-row launch over 1024).  The three ops must write disjoint
+ * outputs.  Shapes outside the fused layout (unaligned
+ * buffers, no residual or h, rows of <= 2048 or > 16384 elements) run as the
+ * three separate launches; a zero batch / norm_elems / swiglu_elems skips
+ * that op there.
+ */
+typedef struct FellmRocmDecodeStep {
+    uint32_t act_dtype;
+    /* RoPE + paged K/V append */
+    const void *q;
+    void *q_out;
+    uint32_t n_q_heads;
+    const void *k;
+    void *k_out; /* may be NULL */
+    const void *v;
+    uint32_t n_kv_heads;
+    uint32_t batch;
+    uint32_t head_dim;
+    uint32_t rope_dim;
+    uint32_t pairing;
+    const float *inv_freqs;
+    const uint32_t *rope_positions; /* NULL: kv_positions */
+    const uint32_t *kv_positions;
+    const FellmRocmPagedKv *kv;
+    uint32_t *err_flag;
+    /* residual add + RMSNorm */
+    const void *x;
+    const void *residual;
+    void *h_out;
+    const float *norm_weight;
+    uint32_t group;
+    void *y;
+    uint64_t norm_elems;
+    float eps;
+    /* SwiGLU */
+    const void *gate;
+    const void *up;
+    void *act_out;
+    uint64_t swiglu_elems;
+} FellmRocmDecodeStep;
+
+int fellm_rocm_decode_step(const FellmRocmDecodeStep *step, void *stream);
+
+/*
  * MoE router: softmax (gating_func other than 2 and 4), sigmoid
  * (gating_func == 2) or sqrt-softplus (gating_func == 4) over each token's
  * n_experts logits, top-k by score (ties -> lower expert id),
