@@ -75,6 +75,7 @@ def lib(path: Path | None = None) -> C.CDLL:
             "oracle_quantize_q8k": (None, [P, S, P, P, P]),
             "oracle_kquant45_ints": (None, [U32, P, P, P, P]),
             "oracle_kquant_row_dot": (F, [U32, P, S, P, P, P]),
+            "oracle_kquant_row_dot_avx2": (F, [U32, P, S, P, P, P]),
             "oracle_matvec_kquant": (C.c_int, [U32, P, S, S, P, P]),
             "oracle_gate_up_swiglu": (C.c_int, [U32, P, U32, P, S, S, P, P]),
             "oracle_moe_dispatch": (C.c_int, [P, S, S, S, P, P, P, P]),
@@ -306,6 +307,13 @@ def kquant_row_dot(dtype: int, row: np.ndarray, cols: int, qs, bsums, d) -> floa
     r = _c(row, np.uint8)
     q, s, dd = _c(qs, np.int8), _c(bsums, np.int16), _c(d, np.float32)
     return float(np.float32(lib().oracle_kquant_row_dot(dtype, _p(r), cols, _p(q), _p(s), _p(dd))))
+
+
+def kquant_row_dot_avx2(dtype: int, row: np.ndarray, cols: int, qs, bsums, d) -> float:
+    """The x86 AVX2/FMA row dot's f32 combine (Q4_K, Q5_K) on a Q8_K vector."""
+    r = _c(row, np.uint8)
+    q, s, dd = _c(qs, np.int8), _c(bsums, np.int16), _c(d, np.float32)
+    return float(np.float32(lib().oracle_kquant_row_dot_avx2(dtype, _p(r), cols, _p(q), _p(s), _p(dd))))
 
 
 def matvec_kquant(dtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:

@@ -668,6 +668,61 @@ float oracle_kquant_row_dot(uint32_t dtype, const uint8_t *row, size_t cols, con
     return acc;
 }
 
+/* The x86 AVX2 + FMA row dot's f32 combine for Q4_K / Q5_K
+ * (vec_dot_q4k.rs:381-451 vec_dot_q4_k_q8_k_row_avx2; vec_dot_q5k.rs:229-312),
+ * which an AVX2/FMA host (and, with the same lane layout, the AVX-512 path at
+ * vec_dot_q4k.rs:690-774) runs instead of the portable scalar order above.
+ * Per block i: d = y.d * d, dmin = -y.d * dmin (f32); eight int32 lanes
+ * sumi[k] = sum over the four 64-element chunks j of
+ *   sc[2j] * sum_{b=4k..4k+3} lo_j[b] q8[64j + b] + sc[2j+1] * sum_{b} hi_j[b] q8[64j + 32 + b]
+ * (maddubs pairs bytes, madd pairs those with the broadcast scale); four
+ * int32 lanes prod[m] = mn[2m] (bs[4m] + bs[4m+1]) + mn[2m+1] (bs[4m+2] + bs[4m+3]);
+ * acc[k] = fma(d, sumi[k], acc[k]), acc_m[m] = fma(dmin, prod[m], acc_m[m]).
+ * End: hsum_float_8(acc) = ((a0+a4) + (a2+a6)) + ((a1+a5) + (a3+a7)),
+ * acc_m folded as (m0 + m2) + (m1 + m3), result hsum + acc_m.
+ * Used only to measure how far the device GEMV (which follows the portable
+ * order bit for bit) lies from what such a host computes. */
+float oracle_kquant_row_dot_avx2(uint32_t dtype, const uint8_t *row, size_t cols, const int8_t *qs,
+                                 const int16_t *bsums, const float *xd) {
+    const size_t bb = kquant_block_bytes(dtype);
+    float acc[8] = {0}, acc_m[4] = {0};
+    for (size_t i = 0; i < cols / QK_K; ++i) {
+        const uint8_t *blk = row + i * bb;
+        const int8_t *q = qs + i * QK_K;
+        const int16_t *bs = bsums + i * 16;
+        const float d = xd[i] * f16_to_f32(le16(blk));
+        const float dmin = -xd[i] * f16_to_f32(le16(blk + 2));
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) get_scale_min_k4((size_t)j, blk + 4, &sc[j], &mn[j]);
+        for (int m = 0; m < 4; ++m) {
+            const int32_t prod = (int32_t)mn[2 * m] * (int32_t)(int16_t)(bs[4 * m] + bs[4 * m + 1]) +
+                                 (int32_t)mn[2 * m + 1] * (int32_t)(int16_t)(bs[4 * m + 2] + bs[4 * m + 3]);
+            acc_m[m] = fmaf(dmin, (float)prod, acc_m[m]);
+        }
+        const uint8_t *qb = blk + (dtype == 13 ? 48 : 16), *qh = blk + 16;
+        int32_t sumi[8] = {0};
+        for (int j = 0; j < 4; ++j)
+            for (int k = 0; k < 8; ++k) {
+                int32_t pl = 0, ph = 0;
+                for (int b = 4 * k; b < 4 * k + 4; ++b) {
+                    int lo = qb[32 * j + b] & 0x0F, hi = qb[32 * j + b] >> 4;
+                    if (dtype == 13) {
+                        lo += ((qh[b] >> (2 * j)) & 1) << 4;
+                        hi += ((qh[b] >> (2 * j + 1)) & 1) << 4;
+                    }
+                    pl += lo * q[64 * j + b];
+                    ph += hi * q[64 * j + 32 + b];
+                }
+                sumi[k] += (int32_t)sc[2 * j] * pl + (int32_t)sc[2 * j + 1] * ph;
+            }
+        for (int k = 0; k < 8; ++k) acc[k] = fmaf(d, (float)sumi[k], acc[k]);
+    }
+    const float s0 = acc[0] + acc[4], s1 = acc[1] + acc[5], s2 = acc[2] + acc[6], s3 = acc[3] + acc[7];
+    const float h = (s0 + s2) + (s1 + s3);
+    const float m = (acc_m[0] + acc_m[2]) + (acc_m[1] + acc_m[3]);
+    return h + m;
+}
+
 static int matvec_kquant_q(uint32_t dtype, const uint8_t *w, size_t rows, size_t cols, const int8_t *qs,
                            const int16_t *bs, const float *d, float *y) {
     const size_t bb = kquant_block_bytes(dtype);

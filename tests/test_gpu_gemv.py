@@ -169,3 +169,34 @@ def test_gate_up_swiglu_q8k_matches(ops, dev, gt, ut):
     got = ops.gate_up_swiglu_q8k(to_dev(g, dev), to_dev(u, dev), xq, qtype=NAMES[gt], up_qtype=NAMES[ut])
     assert_exact(got.cpu().numpy(), oracle.gate_up_swiglu(gt, g, ut, u, rows, cols, x),
                  f"gate_up_q8k {NAMES[gt]}/{NAMES[ut]}")
+
+
+@pytest.mark.parametrize("dtype", [12, 13])
+def test_gemv_distance_from_avx2_order(ops, dev, dtype):
+    """The device GEMV is bit-exact with the CPU's portable order; an x86 host
+    with AVX2 + FMA (or AVX-512) combines the same integers in another f32
+    order (vec_dot_q4k.rs:381-451, vec_dot_q5k.rs:229-312).  This measures the
+    device result's distance from that order at the Llama-3-8B gate shape
+    (14336 x 4096) and bounds it by 4e-6 of each row's magnitude; the printed
+    ulp distances are the figures quoted for it."""
+    rng = np.random.default_rng(8 + dtype)
+    rows, cols = 14336, 4096
+    w = weights(rng, dtype, rows, cols)
+    x = rng.normal(size=cols).astype(np.float32)
+    got = ops.matvec_kquant(to_dev(w, dev), to_dev(x, dev), qtype=NAMES[dtype]).cpu().numpy()
+    qs, bs, d = oracle.quantize_q8k(x)
+    avx = np.array([oracle.kquant_row_dot_avx2(dtype, w[r], cols, qs, bs, d) for r in range(rows)], np.float32)
+    port = oracle.matvec_kquant(dtype, w, rows, cols, x)
+    assert_exact(got, port, "device vs portable order")
+    gi, ai = got.view(np.int32).astype(np.int64), avx.view(np.int32).astype(np.int64)
+    gi = np.where(gi < 0, -(gi & 0x7FFFFFFF), gi)
+    ai = np.where(ai < 0, -(ai & 0x7FFFFFFF), ai)
+    ulps = np.abs(gi - ai)
+    xq = (qs.astype(np.float64).reshape(-1, 256) * d[:, None].astype(np.float64)).ravel()
+    mags = np.array([float(np.dot(np.abs(oracle.dequantize_row(dtype, w[r], cols).astype(np.float64)), np.abs(xq)))
+                     for r in range(0, rows, 97)])
+    dev_rel = np.abs(got[::97].astype(np.float64) - avx[::97].astype(np.float64)) / mags
+    print(f"\n{NAMES[dtype]} {rows}x{cols}: device vs AVX2-order: equal {int((ulps == 0).sum())}/{rows}, "
+          f"ulp distance max {int(ulps.max())} median {float(np.median(ulps))} p99 {float(np.percentile(ulps, 99))}; "
+          f"max |diff| / row magnitude {dev_rel.max():.2e}")
+    assert dev_rel.max() <= 4e-6

@@ -177,6 +177,8 @@ def test_k45_row_dot_exact_integers(dtype, d, dmin):
     exact = int(np.dot(w.astype(np.int64), x.astype(np.int64)))
     assert abs(exact) < 2**24
     assert oracle.kquant_row_dot(dtype, row, cols, qs, bs, dq) == float(exact)
+    # the x86 AVX2/FMA combine partitions the same integers differently: exact too
+    assert oracle.kquant_row_dot_avx2(dtype, row, cols, qs, bs, dq) == float(exact)
 
 
 def test_q6k_row_dot_exact_integers():
@@ -232,6 +234,30 @@ def test_row_dot_close_to_exact(dtype):
         ref = float(np.dot(wr, xq))
         mag = float(np.dot(np.abs(wr), np.abs(xq)))
         assert abs(float(y[r]) - ref) <= 2e-5 * mag, (r, y[r], ref, mag)
+
+
+@pytest.mark.parametrize("dtype", [Q4K, Q5K])
+def test_avx2_combine_close_to_exact(dtype):
+    """The AVX2/FMA-order restatement (vec_dot_q4k.rs:381-451,
+    vec_dot_q5k.rs:229-312) stays within the same bound of the float64 dot,
+    and differs from the portable order by at most a few ulps of the row's
+    magnitude (the two orders are what an AVX2 host and the device compute)."""
+    rng = np.random.default_rng(31 + dtype)
+    cols, rows = 4096, 64
+    w = synth.KQUANT_TABLES[dtype](rng, rows, cols)
+    x = rng.normal(size=cols).astype(np.float32)
+    qs, bs, d = oracle.quantize_q8k(x)
+    xq = (qs.astype(np.float64).reshape(-1, 256) * d[:, None].astype(np.float64)).ravel()
+    diffs = 0
+    for r in range(rows):
+        a = oracle.kquant_row_dot_avx2(dtype, w[r], cols, qs, bs, d)
+        p = oracle.kquant_row_dot(dtype, w[r], cols, qs, bs, d)
+        wr = oracle.dequantize_row(dtype, w[r], cols).astype(np.float64)
+        ref, mag = float(np.dot(wr, xq)), float(np.dot(np.abs(wr), np.abs(xq)))
+        assert abs(a - ref) <= 2e-5 * mag
+        assert abs(a - p) <= 4e-6 * mag
+        diffs += a != p
+    assert diffs > 0  # the orders do differ in the last bits
 
 
 def test_gate_up_swiglu_composes():
