@@ -37,9 +37,14 @@
 #define FELLM_EMB_BLOCK 256
 #endif
 // Build knob: Q4_K / Q6_K scale factors staged in LDS once per row (1) or
-// decoded from the block header by every part (0).
+// decoded from the block header by every part (0); 2 also takes Q4_K in
+// parts of 8 consecutive outputs, every part of a thread decoded before its
+// stores.  Measured at configs[2] (Q4_K / Q6_K gather, interleaved on one
+// box): staged 15.2-15.4 / 19.0-19.3 us; 8-output Q4_K parts 14.8-15.0 us
+// (decoding all parts first; 16.0 us part by part); 8-output Q6_K parts
+// 22.2-22.8 us, so Q6_K keeps its 16-output parts.
 #ifndef FELLM_EMB_STAGE
-#define FELLM_EMB_STAGE 1
+#define FELLM_EMB_STAGE 2
 #endif
 // Build knob: plain gathers decode and store part by part (1) or decode all
 // parts into registers first (0).
@@ -230,6 +235,39 @@ struct Q6KStaged {
     }
 };
 
+// Staged decoders with parts of 8 consecutive outputs (one 16-byte store
+// of a 16-bit output per part, so a wavefront writes 1 KB of a row
+// contiguously); same scale slots and arithmetic as Q4KStaged / Q6KStaged.
+// Q4_K: outputs o = 8p' .. 8p'+7 of block p / 32 (p' = p % 32): chunk
+// c = o / 64, offset j = o % 64, low nibbles of qs[32c + j ..] when j < 32,
+// else high nibbles of qs[32c + j - 32 ..] (dequant.rs:268-289).
+struct Q4KStaged8 {
+    static constexpr bool STAGED = true;
+    static constexpr bool ALL_PARTS_IN_REGS = true;  // plain gathers decode every part before storing
+    static constexpr int OUT = 8, RUNS = 1, RUNLEN = 8;
+    using Raw = uint2;
+    __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)(dim / 256) * 144; }
+    __host__ __device__ static uint32_t parts(uint32_t dim) { return dim / 8; }
+    __device__ static uint32_t run_off(uint32_t p, int) { return p * 8; }
+    __device__ static Raw load(const uint8_t *row, uint32_t p) {
+        const uint32_t o = 8 * (p % 32);
+        return *reinterpret_cast<const uint2 *>(row + (size_t)(p / 32) * 144 + 16 + 32 * (o / 64) + (o % 32));
+    }
+    __device__ static float4 stage(const uint8_t *row, uint32_t slot) { return Q4KStaged::stage(row, slot); }
+    __device__ static void finish(Raw qs, uint32_t p, const float4 *lds, float (&v)[OUT]) {
+        const uint32_t o = 8 * (p % 32);
+        const float4 f = lds[(p / 32) * 4 + o / 64];
+        const bool hi = (o % 64) >= 32;
+        const float dq = hi ? f.z : f.x, mq = hi ? f.w : f.y;
+        const uint32_t sh = hi ? 4 : 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t b = ((k < 4 ? qs.x : qs.y) >> (8 * (k % 4) + sh)) & 0x0fu;
+            v[k] = dq * (float)b - mq;
+        }
+    }
+};
+
 // Plain gathers stream their output with non-temporal stores; the fused
 // gather + RMSNorm stores after its reduction barrier and measured faster
 // with regular stores.
@@ -267,13 +305,13 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
     const uint8_t *src = table + (bad ? 0 : (uint64_t)id * rb);
     const uint32_t parts = D::parts(dim);
     const size_t obase = (size_t)row * dim;
-    extern __shared__ float4 stage_lds[];  // staged decoders: parts / 4 scale slots
+    extern __shared__ float4 stage_lds[];  // staged decoders: 4 scale slots per 256-element block
     if constexpr (MAXC == 0 && D::STAGED) {
         // The first part's quant bytes are requested before the scale slots
         // are built, so their latency overlaps the staging and the barrier.
         typename D::Raw raw0{};
         if (threadIdx.x < parts) raw0 = D::load(src, threadIdx.x);
-        for (uint32_t t = threadIdx.x; t < parts / 4; t += kEmbBlock) stage_lds[t] = D::stage(src, t);
+        for (uint32_t t = threadIdx.x; t < dim / 64; t += kEmbBlock) stage_lds[t] = D::stage(src, t);
         __syncthreads();
         for (uint32_t p = threadIdx.x; p < parts; p += kEmbBlock) {
             float v[D::OUT];
@@ -306,7 +344,7 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
                 const uint32_t p = c * kEmbBlock + threadIdx.x;
                 if (p < parts) raw[c] = D::load(src, p);
             }
-            for (uint32_t t = threadIdx.x; t < parts / 4; t += kEmbBlock) stage_lds[t] = D::stage(src, t);
+            for (uint32_t t = threadIdx.x; t < dim / 64; t += kEmbBlock) stage_lds[t] = D::stage(src, t);
             __syncthreads();
 #pragma unroll
             for (int c = 0; c < MAXC; ++c) {
@@ -362,7 +400,7 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
     const dim3 grid(n_ids), block(kEmbBlock);
     const uint8_t *tb = static_cast<const uint8_t *>(table);
     const uint32_t chunks = (D::parts(dim) + kEmbBlock - 1) / kEmbBlock;
-    const uint32_t lds = D::STAGED ? D::parts(dim) / 4 * sizeof(float4) : 0;
+    const uint32_t lds = D::STAGED ? dim / 64 * sizeof(float4) : 0;
     if (lds > 65536) return FELLM_ERR_SHAPE;  // dim > 262144
 #define FELLM_EMB(C, NORM)                                                                          \
     if (chunks <= C) {                                                                              \
@@ -371,7 +409,8 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
         return launch_status();                                                                     \
     }
     if (!w) {
-        if (FELLM_EMB_LOOP) {
+        constexpr bool regs = requires { D::ALL_PARTS_IN_REGS; };
+        if (FELLM_EMB_LOOP && !regs) {
             FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, lds, s, tb, vocab, dim, ids, (TO *)h,
                                nullptr, nullptr, 0.0f, err);
             return launch_status();
@@ -399,6 +438,7 @@ int dispatch_table(const void *table, uint32_t table_dtype, uint64_t vocab, uint
     switch (table_dtype) {
         case FELLM_DTYPE_Q4K:
             if (dim % 256 || !aligned_to(table, 16)) return FELLM_ERR_SHAPE;
+            if (FELLM_EMB_STAGE == 2) return launch_emb<Q4KStaged8, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
             if (FELLM_EMB_STAGE) return launch_emb<Q4KStaged, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
             return launch_emb<Q4KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
         case FELLM_DTYPE_Q6K:

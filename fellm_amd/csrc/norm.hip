@@ -11,6 +11,8 @@
 // read exactly once and h and y written exactly once: 4 row-passes of HBM
 // traffic with the residual fused (the unfused graph needs 6).
 // The sum of squares is one wavefront shuffle reduction plus one LDS exchange.
+#include <algorithm>
+
 #include "norm_body.hpp"
 
 // Build knob: with many rows, rows of at most FELLM_NORM_WAVE_BYTES bytes
@@ -19,6 +21,14 @@
 // 26.2-26.3 us (wavefront per row) against 27.3-27.5 us; 4096 x 4096 f16
 // add+RMSNorm (8 KB rows) 28.4 us against 25.2 us, with the RoPE launched
 // after it slowed from 15.6 to 19.5 us.  So rows up to 4 KB only.
+// Build knob: many-row add + RMSNorm with h, rows of 2049..4096 16-bit
+// elements, as a persistent pipelined grid of FELLM_NORM_PIPE workgroups per
+// CU (0: one workgroup per row).  Measured inside the op chain at 4096 x 4096
+// f16: 3 per CU 23.6-24.0 us, 2 per CU 24.1-24.5, 4 per CU 24.4, one
+// workgroup per row 24.1-25.0.
+#ifndef FELLM_NORM_PIPE
+#define FELLM_NORM_PIPE 3
+#endif
 #ifndef FELLM_NORM_WAVE_BYTES
 #define FELLM_NORM_WAVE_BYTES 4096
 #endif
@@ -40,6 +50,88 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_kernel(const typename A::T 
                                                             typename O::T *y, uint32_t group, float eps) {
     __shared__ float red[BLOCK / kWave];
     add_rmsnorm_row<A, O, BLOCK, VEC, NCHUNK, ADD, STORE_H>(x, r, h, w, y, group, eps, blockIdx.x, red);
+}
+
+// Persistent, software-pipelined add + RMSNorm for many rows: a grid of
+// about `waves_per_cu` workgroups per CU loops over rows bid, bid + grid, ...
+// and requests row i+1's x and r before it reduces and stores row i, so the
+// loads of the next row overlap the barrier and the stores of this one.  The
+// weights are read once per workgroup.  Same arithmetic as add_rmsnorm_row.
+template <typename A, typename O, int BLOCK, int VEC, int NCHUNK>
+__global__ __launch_bounds__(BLOCK) void add_rmsnorm_pipe_kernel(const typename A::T *x, const typename A::T *r,
+                                                                 typename A::T *h, const float *__restrict__ w,
+                                                                 typename O::T *y, uint32_t group, uint32_t rows,
+                                                                 float eps) {
+    __shared__ float red[2][BLOCK / kWave];
+    float wv[NCHUNK][VEC];
+#pragma unroll
+    for (int c = 0; c < NCHUNK; ++c) {
+        const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
+        if (base < group) load_f32<F32, VEC>(w + base, wv[c]);
+    }
+    float xv[NCHUNK][VEC], rv[NCHUNK][VEC];
+    auto load_row = [&](uint32_t row, float (&xo)[NCHUNK][VEC], float (&ro)[NCHUNK][VEC]) {
+#pragma unroll
+        for (int c = 0; c < NCHUNK; ++c) {
+            const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
+            if (base < group) {
+                norm_load<A, VEC>(x + (size_t)row * group + base, xo[c]);
+                norm_load<A, VEC>(r + (size_t)row * group + base, ro[c]);
+            }
+        }
+    };
+    uint32_t row = blockIdx.x;
+    if (row < rows) load_row(row, xv, rv);
+    int parity = 0;
+    for (; row < rows; row += gridDim.x) {
+        float hv[NCHUNK][VEC];
+#pragma unroll
+        for (int c = 0; c < NCHUNK; ++c)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) hv[c][i] = A::load(A::store(xv[c][i] + rv[c][i]));
+        const uint32_t next = row + gridDim.x;
+        if (next < rows) load_row(next, xv, rv);  // in flight during this row's reduction and stores
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCHUNK; ++c) {
+            const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
+            if (base < group) {
+                norm_store<A, VEC, true>(h + (size_t)row * group + base, hv[c]);
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) ss += hv[c][i] * hv[c][i];
+            }
+        }
+        // Alternate the LDS slots so one barrier per row suffices.
+        ss = wave_sum(ss);
+        if (threadIdx.x % kWave == 0) red[parity][threadIdx.x / kWave] = ss;
+        __syncthreads();
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < BLOCK / kWave; ++i) t += red[parity][i];
+        parity ^= 1;
+        const float scale = 1.0f / sqrtf(t / (float)group + eps);
+#pragma unroll
+        for (int c = 0; c < NCHUNK; ++c) {
+            const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
+            if (base < group) {
+                float o[VEC];
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) o[i] = (hv[c][i] * scale) * wv[c][i];
+                norm_store<O, VEC, true>(y + (size_t)row * group + base, o);
+            }
+        }
+    }
+}
+
+inline int cu_count() {
+    static int n = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        return v;
+    }();
+    return n;
 }
 
 // One wavefront per row, four rows per workgroup, for rows of at most 8 KB
@@ -193,6 +285,14 @@ int launch_typed(const void *x, const void *r, void *h, const float *w, void *y,
             if (nch <= 2) return launch_wave<A, O, 2>(x, r, h, w, y, group, rows, eps, s);
             if (nch <= 4) return launch_wave<A, O, 4>(x, r, h, w, y, group, rows, eps, s);
             return launch_wave<A, O, 8>(x, r, h, w, y, group, rows, eps, s);
+        }
+        if (FELLM_NORM_PIPE && r && h && group > 256 * VEC && group <= 512 * VEC) {
+            using TA = typename A::T;
+            using TO = typename O::T;
+            const uint32_t grid = (uint32_t)std::min<uint64_t>(rows, (uint64_t)cu_count() * FELLM_NORM_PIPE);
+            FELLM_LAUNCH((add_rmsnorm_pipe_kernel<A, O, 512, VEC, 1>), dim3(grid), dim3(512), 0, s, (const TA *)x,
+                         (const TA *)r, (TA *)h, w, (TO *)y, group, (uint32_t)rows, eps);
+            return launch_status();
         }
         if (FELLM_NORM_PREFILL_BLOCK == 512 && group > 256 * VEC && group <= 512 * VEC)
             return launch_fast<A, O, 512, VEC, 1>(x, r, h, w, y, group, rows, eps, s);
