@@ -104,6 +104,35 @@ __device__ __forceinline__ void rope_load(const typename A::T *x1, const typenam
                                           const typename A::T *x3, uint32_t nh1, uint32_t nh2, size_t w1, size_t w2,
                                           uint32_t row, uint32_t hd, uint32_t it, uint32_t head_dim, uint32_t rope_dim,
                                           uint32_t pairing, uint32_t n_rot, float (&e)[2 * PV]) {
+    if constexpr (sizeof(typename A::T) * 2 * PV > 16) {
+        // Items wider than one 16-byte access (f32) take two loads whatever
+        // the layout: the branches pick the two addresses and the loads
+        // follow unconditionally, so e is written at fixed indices only
+        // (writes of e merged across branches would move it to scratch).
+        const typename A::T *p0, *p1;
+        if (hd < nh1 + nh2) {
+            const bool first = hd < nh1;
+            const typename A::T *src = first ? x1 : x2;
+            const size_t base = first ? (size_t)row * w1 + (size_t)hd * head_dim
+                                      : (size_t)row * w2 + (size_t)(hd - nh1) * head_dim;
+            uint32_t lo, hi;
+            item_offsets(it, n_rot, head_dim, rope_dim, pairing, PV, lo, hi);
+            p0 = src + base + lo;
+            p1 = src + base + hi;
+        } else {  // V head: plain 2*PV-element run
+            p0 = x3 + (size_t)row * w2 + (size_t)(hd - nh1 - nh2) * head_dim + it * 2 * PV;
+            p1 = p0 + PV;
+        }
+        float a[PV], b[PV];
+        act_load<A, PV>(p0, a);
+        act_load<A, PV>(p1, b);
+#pragma unroll
+        for (int k = 0; k < PV; ++k) {
+            e[k] = a[k];
+            e[PV + k] = b[k];
+        }
+        return;
+    }
     const typename A::T *src;
     size_t base;
     if (hd < nh1) {
@@ -542,6 +571,15 @@ extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q
 // outputs), as in the reference's decode graph before attention
 // (crates/fellm-model/src/graph.rs:2136-2246).
 // ---------------------------------------------------------------------------
+// Minimum waves per SIMD requested for the fused decode step when a norm
+// row takes at most 4 chunks per thread: the norm role's registers would
+// otherwise set the occupancy of all three roles (82 VGPRs, 5 waves; 6 waves
+// fit without spilling and measured 17.6 vs 18.5 us at 256 x H 8192 bf16).
+// 8 chunks (rows above 8192 elements) keep the compiler's choice: limiting
+// them spills.
+#ifndef FELLM_STEP_WAVES
+#define FELLM_STEP_WAVES 6
+#endif
 #ifndef FELLM_STEP_ORDER
 #define FELLM_STEP_ORDER 0
 #endif
@@ -578,7 +616,9 @@ struct StepArgs {
 };
 
 template <typename A, typename C, int NCHUNK>
-__global__ __launch_bounds__(kRopeBlock) void decode_step_kernel(StepArgs<A> p) {
+__global__ __launch_bounds__(kRopeBlock)
+__attribute__((amdgpu_waves_per_eu(NCHUNK <= 4 && FELLM_STEP_WAVES ? FELLM_STEP_WAVES : 1)))
+void decode_step_kernel(StepArgs<A> p) {
     static_assert(kRopeBlock == 256 && kEwBlock == 256, "the three roles share one workgroup size");
     __shared__ float2 cs_all[1][kMaxHalf];
     __shared__ uint64_t kbase_all[1];
