@@ -366,14 +366,17 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
         if (grp == 0) {
 #pragma unroll
             for (int h = 0; h < GM; ++h) {
-                if ((uint32_t)h >= G) break;
-                const float lh = lds_h[h];
-                const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
-                typename O::T *o = out + ((size_t)b * n_heads + (size_t)g * G + h) * HD + col * DP;
-                float r[DP];
+                // A guard rather than a break: a loop with a second exit is
+                // not fully unrolled at GM 16, and acc then lives in scratch.
+                if ((uint32_t)h < G) {
+                    const float lh = lds_h[h];
+                    const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+                    typename O::T *o = out + ((size_t)b * n_heads + (size_t)g * G + h) * HD + col * DP;
+                    float r[DP];
 #pragma unroll
-                for (int d = 0; d < DP; ++d) r[d] = lh > 0.0f ? acc[h][d] * inv : 0.0f;
-                store_f32<O, DP>(o, r);
+                    for (int d = 0; d < DP; ++d) r[d] = lh > 0.0f ? acc[h][d] * inv : 0.0f;
+                    store_f32<O, DP>(o, r);
+                }
             }
         }
     } else {
@@ -382,9 +385,10 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
         if (grp == 0) {
 #pragma unroll
             for (int h = 0; h < GM; ++h) {
-                if ((uint32_t)h >= G) break;
+                if ((uint32_t)h < G) {
 #pragma unroll
-                for (int d = 0; d < DP; ++d) rec[h * (HD + 2) + col * DP + d] = acc[h][d];
+                    for (int d = 0; d < DP; ++d) rec[h * (HD + 2) + col * DP + d] = acc[h][d];
+                }
             }
             if (col < G) {
                 rec[col * (HD + 2) + HD] = m;

@@ -66,7 +66,8 @@ def check(got, ref, v16, out_kind, what):
         assert not bad.any(), f"{what} row {r}: max err {err.max()} (tol {tol[bad][:3]}) got {got[r][bad][:3]} ref {ref[r][bad][:3]}"
 
 
-SHAPES = [(32, 8, 128), (64, 8, 128), (32, 4, 128), (8, 1, 64), (4, 4, 128), (16, 1, 256), (32, 2, 256)]
+SHAPES = [(32, 8, 128), (64, 8, 128), (32, 4, 128), (8, 1, 64), (4, 4, 128), (16, 1, 256), (32, 2, 256),
+          (16, 1, 64), (64, 4, 128), (48, 4, 128)]  # the last three: 12-16 query heads per K/V head
 
 
 @pytest.mark.parametrize("n_heads,n_kv,hd", SHAPES)
