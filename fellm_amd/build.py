@@ -34,6 +34,8 @@ COMMON_FLAGS = [
     f"-I{CSRC}",
     "-Wall",
     "-Wno-unused-function",
+    # A requested unroll that fails leaves register arrays in scratch memory.
+    "-Werror=pass-failed",
 ]
 DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 

@@ -67,6 +67,19 @@ struct BF16Trunc {
     __device__ __forceinline__ static T store(float v) { return (T)(__float_as_uint(v) >> 16); }
 };
 
+// Compute units of the current device (the first call's device; every
+// device this library runs on is the same part), for persistent grids.
+inline int cu_count() {
+    static int n = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        return v;
+    }();
+    return n;
+}
+
 // Host-side dispatch helper: call f.template operator()<Type>() for a dtype code.
 template <typename Fn>
 inline int dispatch_act(uint32_t dtype, Fn &&f) {

@@ -51,6 +51,14 @@
 #ifndef FELLM_EMB_LOOP
 #define FELLM_EMB_LOOP 1
 #endif
+// Build knob: workgroups per compute unit of the persistent, pipelined plain
+// gather (0: one workgroup per row).  Measured at configs[1] (4096 f16 rows of
+// 4096, interleaved on one box): one workgroup per row 13.2-13.4 us; 2 per CU
+// 16.6-16.7 us; 4 per CU 13.4-13.5 us; 8 per CU (the occupancy limit of
+// 256-thread workgroups) 12.3-12.4 us.
+#ifndef FELLM_EMB_PIPE
+#define FELLM_EMB_PIPE 8
+#endif
 
 
 namespace fellm {
@@ -64,6 +72,7 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
 template <typename A, int VEC>
 struct DenseDec {
     static constexpr bool STAGED = false;
+    static constexpr bool DENSE = true;  // gathers may take the persistent kernel
     static constexpr int OUT = VEC, RUNS = 1, RUNLEN = VEC;
     __host__ __device__ static uint64_t row_bytes(uint32_t dim) { return (uint64_t)dim * sizeof(typename A::T); }
     __host__ __device__ static uint32_t parts(uint32_t dim) { return dim / VEC; }
@@ -393,6 +402,81 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
     }
 }
 
+// Plain (unquantized) gather, persistent: workgroup b copies rows b, b + G,
+// b + 2G, ... (G = the grid).  The id of the row after next is requested a
+// row ahead, and the next row's data are loaded before the current row is
+// stored, so neither the id's latency nor the data's is paid per row.  A
+// thread moves C parts of VEC elements per row.
+template <typename D, int C>
+__device__ __forceinline__ void emb_pipe_load(const uint8_t *table, uint64_t vocab, uint64_t rb, uint32_t parts,
+                                              uint32_t id, float (&v)[C][D::OUT]) {
+    const uint8_t *src = table + (id < vocab ? (uint64_t)id * rb : 0);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const uint32_t p = c * kEmbBlock + threadIdx.x;
+        if (p < parts) D::decode(src, p, v[c]);
+    }
+}
+
+template <typename D, typename O, int C>
+__device__ __forceinline__ void emb_pipe_store(typename O::T *hrow, uint32_t parts, bool bad, float (&v)[C][D::OUT]) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const uint32_t p = c * kEmbBlock + threadIdx.x;
+        if (p < parts) {
+            if (bad) {
+#pragma unroll
+                for (int k = 0; k < D::OUT; ++k) v[c][k] = 0.0f;
+            }
+            store_part<D, O, true>(hrow, p, v[c]);
+        }
+    }
+}
+
+// Plain (unquantized) gather, persistent: workgroup b copies rows b, b + G,
+// b + 2G, ... (G = the grid).  The id of the row after next is requested a
+// row ahead, and the next row's data are loaded before the current row is
+// stored, so neither the id's latency nor the data's is paid per row.  A
+// thread moves C parts of VEC elements per row; two register sets alternate.
+template <typename D, typename O, int C>
+__global__ __launch_bounds__(kEmbBlock) void embedding_pipe_kernel(
+    const uint8_t *__restrict__ table, uint64_t vocab, uint32_t dim, const uint32_t *__restrict__ ids,
+    uint32_t n_ids, typename O::T *__restrict__ h, uint32_t *__restrict__ err) {
+    static_assert(D::DENSE, "plain tables only");
+    const uint64_t rb = D::row_bytes(dim);
+    const uint32_t parts = D::parts(dim);
+    const uint32_t G = gridDim.x;
+    uint32_t row = blockIdx.x;
+    if (row >= n_ids) return;
+    uint32_t id_a = ids[row];
+    uint32_t id_b = row + G < n_ids ? ids[row + G] : 0u;
+    float va[C][D::OUT], vb[C][D::OUT];
+    emb_pipe_load<D, C>(table, vocab, rb, parts, id_a, va);
+    uint32_t bad_rows = 0;
+    for (;;) {
+        // va holds row (id_a); id_b is row + G's id.
+        uint32_t next = row + G;
+        if (next < n_ids) emb_pipe_load<D, C>(table, vocab, rb, parts, id_b, vb);
+        uint32_t id_c = next + G < n_ids ? ids[next + G] : 0u;
+        bad_rows |= id_a >= vocab;
+        emb_pipe_store<D, O, C>(h + (size_t)row * dim, parts, id_a >= vocab, va);
+        if (next >= n_ids) break;
+        row = next;
+        // vb holds row (id_b); id_c is row + G's id.
+        next = row + G;
+        if (next < n_ids) emb_pipe_load<D, C>(table, vocab, rb, parts, id_c, va);
+        id_a = next + G < n_ids ? ids[next + G] : 0u;
+        bad_rows |= id_b >= vocab;
+        emb_pipe_store<D, O, C>(h + (size_t)row * dim, parts, id_b >= vocab, vb);
+        if (next >= n_ids) break;
+        row = next;
+        const uint32_t t = id_a;  // va now holds row (id_c); id_a is row + G's id
+        id_a = id_c;
+        id_b = t;
+    }
+    if (bad_rows && threadIdx.x == 0 && err) atomicOr(err, 1u);
+}
+
 template <typename D, typename O>
 int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids,
                void *h, void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
@@ -409,6 +493,23 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
         return launch_status();                                                                     \
     }
     if (!w) {
+        if constexpr (requires { D::DENSE; } && FELLM_EMB_PIPE > 0) {
+            // Many rows: persistent workgroups (more rows than one pass of
+            // the grid, so the pipeline has rows to overlap).
+            const uint32_t pgrid = (uint32_t)cu_count() * FELLM_EMB_PIPE;
+            if (ids && chunks <= 4 && n_ids >= 2 * pgrid) {
+#define FELLM_EMB_P(C)                                                                                        \
+    if (chunks <= C) {                                                                                        \
+        FELLM_LAUNCH((embedding_pipe_kernel<D, O, C>), dim3(pgrid), block, 0, s, tb, vocab, dim, ids, n_ids, \
+                     (TO *)h, err);                                                                           \
+        return launch_status();                                                                               \
+    }
+                FELLM_EMB_P(1)
+                FELLM_EMB_P(2)
+                FELLM_EMB_P(4)
+#undef FELLM_EMB_P
+            }
+        }
         constexpr bool regs = requires { D::ALL_PARTS_IN_REGS; };
         if (FELLM_EMB_LOOP && !regs) {
             FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, lds, s, tb, vocab, dim, ids, (TO *)h,

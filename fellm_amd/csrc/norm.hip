@@ -123,17 +123,6 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_pipe_kernel(const typename 
     }
 }
 
-inline int cu_count() {
-    static int n = [] {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-            v = 256;
-        return v;
-    }();
-    return n;
-}
-
 // One wavefront per row, four rows per workgroup, for rows of at most 8 KB
 // (NCH 16-byte chunks per lane, chunk c of the row at lanes' c * 1 KB).  Every
 // lane requests all of its x and r chunks before any arithmetic; the sum of

@@ -259,6 +259,31 @@ def test_embedding_rmsnorm_fused(ops, dev, src):
     assert_close(from_dev(y), y_ref, out_kind, what="fused y")
 
 
+@pytest.mark.parametrize("table_kind,out_kind,dim", [("f16", "f16", 4096), ("f32", "f32", 4096), ("bf16", "f32", 2048),
+                                                      ("f16", "bf16", 100), ("f32", "f16", 1024)])
+@pytest.mark.parametrize("n_rows", [4099, 6144, 2051])
+def test_embedding_dense_many_rows(ops, dev, table_kind, out_kind, dim, n_rows):
+    """Thousands of rows take the persistent gather (each workgroup walks
+    rows b, b + grid, ...): rows counts that end on either half of its two
+    register sets, and out-of-range ids spread through the batch."""
+    rng = np.random.default_rng(n_rows + dim)
+    vocab = 3000
+    t = _dense_table(rng, vocab, dim, table_kind)
+    ids = rng.integers(0, vocab, size=n_rows, dtype=np.uint32)
+    bad = rng.choice(n_rows, size=5, replace=False)
+    ids[bad] = vocab + np.arange(5, dtype=np.uint32) * 1000
+    code = {"f32": 0, "f16": 1, "bf16": 30}[table_kind]
+    ok = ids < vocab
+    ref = np.zeros((n_rows, dim), np.float32)
+    ref[ok] = oracle.embedding(t.view(np.uint8), code, vocab, dim, ids[ok])
+    ref = oracle.narrow(ref, out_kind)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    got = ops.embedding(to_dev(t, table_kind, dev), torch.from_numpy(ids.view(np.int32)).to(dev),
+                        out_dtype=KINDS[out_kind], err_flag=flag)
+    assert int(flag.item()) == 1
+    assert_exact(from_dev(got), ref, f"embedding {n_rows} rows {table_kind}->{out_kind} dim {dim}")
+
+
 def test_embedding_bad_id_sets_flag(ops, dev):
     rng = np.random.default_rng(0)
     t = _dense_table(rng, 10, 64, "f32")
