@@ -362,12 +362,16 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    // The epilogue loops over head slots are unrolled (with a guard rather
+    // than a break: a loop with a second exit is not fully unrolled at GM 16,
+    // and acc then lives in scratch), except where acc (GM x HD / 16 floats
+    // per lane) cannot stay in registers anyway: at 16 x 256 unrolling only
+    // multiplies the compile time.
+    constexpr int kEpiUnroll = GM * DP > 128 ? 1 : GM;
     if (splits == 1) {
         if (grp == 0) {
-#pragma unroll
+#pragma unroll kEpiUnroll
             for (int h = 0; h < GM; ++h) {
-                // A guard rather than a break: a loop with a second exit is
-                // not fully unrolled at GM 16, and acc then lives in scratch.
                 if ((uint32_t)h < G) {
                     const float lh = lds_h[h];
                     const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
@@ -383,7 +387,7 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
         // partial record per (b, g, s, head slot): HD sums, then m, l
         float *rec = part + ((size_t)bg * splits + s) * GM * (HD + 2);
         if (grp == 0) {
-#pragma unroll
+#pragma unroll kEpiUnroll
             for (int h = 0; h < GM; ++h) {
                 if ((uint32_t)h < G) {
 #pragma unroll

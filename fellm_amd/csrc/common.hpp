@@ -80,6 +80,19 @@ inline int cu_count() {
     return n;
 }
 
+// Grid of a persistent kernel whose rows are assigned statically (workgroup b
+// takes rows b, b + grid, ...): every workgroup must be resident from the
+// start, or the late ones would run their rows after the others finish.  At
+// most `cap` workgroups per compute unit, fewer when the kernel's registers
+// or LDS (`lds` bytes, the largest the caller uses) allow fewer.  Cached per
+// kernel: call it from one instantiation per kernel.
+template <typename K>
+inline uint32_t resident_grid(K kernel, int block, size_t lds, int cap) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, lds) != hipSuccess || n <= 0) n = 1;
+    return (uint32_t)cu_count() * (uint32_t)(n < cap ? n : cap);
+}
+
 // Host-side dispatch helper: call f.template operator()<Type>() for a dtype code.
 template <typename Fn>
 inline int dispatch_act(uint32_t dtype, Fn &&f) {

@@ -494,19 +494,21 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
     }
     if (!w) {
         if constexpr (requires { D::DENSE; } && FELLM_EMB_PIPE > 0) {
-            // Many rows: persistent workgroups (more rows than one pass of
-            // the grid, so the pipeline has rows to overlap).
-            const uint32_t pgrid = (uint32_t)cu_count() * FELLM_EMB_PIPE;
-            if (ids && chunks <= 4 && n_ids >= 2 * pgrid) {
-#define FELLM_EMB_P(C)                                                                                        \
-    if (chunks <= C) {                                                                                        \
-        FELLM_LAUNCH((embedding_pipe_kernel<D, O, C>), dim3(pgrid), block, 0, s, tb, vocab, dim, ids, n_ids, \
-                     (TO *)h, err);                                                                           \
-        return launch_status();                                                                               \
-    }
+            // Many rows (at least two per workgroup, so the pipeline has rows
+            // to overlap): persistent workgroups, all resident.
+            if (ids && chunks <= 4) {
+#define FELLM_EMB_P(C)                                                                                         \
+    if (chunks <= C) {                                                                                         \
+        static const uint32_t pgrid = resident_grid(embedding_pipe_kernel<D, O, C>, kEmbBlock, 0, FELLM_EMB_PIPE); \
+        if (n_ids >= 2 * pgrid) {                                                                              \
+            FELLM_LAUNCH((embedding_pipe_kernel<D, O, C>), dim3(pgrid), block, 0, s, tb, vocab, dim, ids, n_ids, \
+                         (TO *)h, err);                                                                        \
+            return launch_status();                                                                            \
+        }                                                                                                      \
+    } else
                 FELLM_EMB_P(1)
                 FELLM_EMB_P(2)
-                FELLM_EMB_P(4)
+                FELLM_EMB_P(4) {}
 #undef FELLM_EMB_P
             }
         }

@@ -483,6 +483,38 @@ def test_rope_many_rows(ops, dev, kind, rows):
     assert_exact(from_dev(g1), r1, f"split-half {rows} rows")
 
 
+@pytest.mark.parametrize("kind,nq,nk,hd,rd,pairing,inplace,rows", [
+    ("f16", 32, 8, 128, 128, 0, False, 4099),
+    ("bf16", 48, 16, 128, 64, 2, False, 6000),  # partial rotary
+    ("f32", 8, 0, 64, 32, 1, True, 5000),       # in place, q only
+    ("f16", 16, 4, 64, 64, 1, False, 4500),
+    ("bf16", 24, 8, 256, 256, 0, True, 4097),   # head_dim 256, in place
+    ("f16", 64, 16, 128, 128, 0, False, 4500),
+])
+def test_rope_many_rows_shapes(ops, dev, kind, nq, nk, hd, rd, pairing, inplace, rows):
+    """Thousands of rows at other shapes: 1 to 5 (head) slots per thread per
+    row, partial rotary, every pairing, in-place rotation, q alone, head_dim
+    64 and 256; random positions; bit-exact against the oracle."""
+    rng = np.random.default_rng(rows + hd + nq)
+    inv = oracle.rope_inv_freqs(500000.0, rd)
+    pos = rng.integers(0, 1 << 17, size=rows, dtype=np.uint32)
+    q = random_stored(rng, (rows, nq * hd), kind)
+    qr = oracle.narrow(oracle.rope(oracle.widen(q, kind), nq, hd, rd, pairing, inv, pos), kind)
+    posd = torch.from_numpy(pos.view(np.int32)).to(dev)
+    invd = torch.from_numpy(inv).to(dev)
+    qd = to_dev(q, kind, dev)
+    if nk:
+        k = random_stored(rng, (rows, nk * hd), kind)
+        kr = oracle.narrow(oracle.rope(oracle.widen(k, kind), nk, hd, rd, pairing, inv, pos), kind)
+        kd = to_dev(k, kind, dev)
+        qo, ko = ops.rope(qd, invd, head_dim=hd, rope_dim=rd, pairing=pairing, positions=posd, x2=kd,
+                          inplace=inplace)
+        assert_exact(from_dev(ko), kr, f"k {rows} rows")
+    else:
+        qo = ops.rope(qd, invd, head_dim=hd, rope_dim=rd, pairing=pairing, positions=posd, inplace=inplace)
+    assert_exact(from_dev(qo), qr, f"q {rows} rows")
+
+
 @pytest.mark.parametrize("kind", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("rows,group", [(1024, 2048), (1031, 1000), (1024, 8192), (1029, 16384), (1024, 12288)])
 def test_add_rmsnorm_many_rows(ops, dev, kind, rows, group):
