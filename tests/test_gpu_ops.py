@@ -284,6 +284,33 @@ def test_embedding_dense_many_rows(ops, dev, table_kind, out_kind, dim, n_rows):
     assert_exact(from_dev(got), ref, f"embedding {n_rows} rows {table_kind}->{out_kind} dim {dim}")
 
 
+@pytest.mark.parametrize("qtype", ["q4k", "q6k"])
+@pytest.mark.parametrize("out_kind,dim,n_rows", [("f16", 3584, 8195), ("bf16", 4096, 4099), ("f32", 256, 6000),
+                                                 ("f16", 16384, 4097)])
+def test_embedding_quant_many_rows(ops, dev, qtype, out_kind, dim, n_rows):
+    """Thousands of K-quant rows (one workgroup per row, 1-2 parts per thread
+    or the looping layout at dim 16384); Zipf ids with out-of-range ids spread
+    through the batch; bit-exact against the oracle."""
+    from fellm_amd import synth
+
+    rng = np.random.default_rng(n_rows + dim + len(qtype))
+    vocab = 700
+    table = synth.q4k_table(rng, vocab, dim) if qtype == "q4k" else synth.q6k_table(rng, vocab, dim)
+    ids = synth.zipf_ids(rng, n_rows, vocab)
+    bad = rng.choice(n_rows, size=4, replace=False)
+    ids[bad] = vocab + np.arange(4, dtype=np.uint32)
+    code = 12 if qtype == "q4k" else 14
+    ok = ids < vocab
+    ref = np.zeros((n_rows, dim), np.float32)
+    ref[ok] = oracle.embedding(table, code, vocab, dim, ids[ok])
+    ref = oracle.narrow(ref, out_kind)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    got = ops.embedding(torch.from_numpy(table).to(dev), torch.from_numpy(ids.view(np.int32)).to(dev), dim=dim,
+                        qtype=qtype, out_dtype=KINDS[out_kind], err_flag=flag)
+    assert int(flag.item()) == 1
+    assert_exact(from_dev(got), ref, f"embedding {qtype} {n_rows} rows dim={dim} -> {out_kind}")
+
+
 def test_embedding_bad_id_sets_flag(ops, dev):
     rng = np.random.default_rng(0)
     t = _dense_table(rng, 10, 64, "f32")
