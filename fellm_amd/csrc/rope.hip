@@ -28,6 +28,15 @@
 #ifndef FELLM_ROPE_NT
 #define FELLM_ROPE_NT 2
 #endif
+// Build knob: MODE 0 slot walk with per-thread constants hoisted (1) or the
+// generic walk shared with MODE 1 (0), for one row per workgroup.  Measured
+// interleaved on one box: configs[1] q+k 15.0-15.4 against 15.5-16.3 us, f32
+// and split-half pairings 4-8% faster.  With four rows per workgroup the
+// hoisted walk needs 67 VGPRs for bf16 (7 waves against 8) and measured 61.4
+// against 59.5-60.2 us at configs[4], so row groups keep the generic walk.
+#ifndef FELLM_ROPE_FAST
+#define FELLM_ROPE_FAST 1
+#endif
 // Build knob: (row, head) slots each thread loads before rotating/storing.
 #ifndef FELLM_ROPE_UNROLL
 #define FELLM_ROPE_UNROLL 3
@@ -229,6 +238,106 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
     }
 }
 
+// MODE 0 with a fixed item position per thread: the slot walk with every
+// per-thread constant hoisted out of it.  KIND is the thread's item kind
+// (uniform over its slots): 0 pass-through (unrotated span), 1 adjacent
+// pairs (e[2k], e[2k+1]) in one contiguous run, 2 split-half pairs
+// (e[k], e[PV+k]) in two runs `hi - lo` apart.  With one row per workgroup
+// (the only caller) the thread's PV (sin, cos) pairs are read from LDS once.
+constexpr int kRopePass = 0, kRopeAdjacent = 1, kRopeSplit = 2;
+
+template <typename A, int PV, int R, int KIND>
+__device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typename A::T *out1, uint32_t nh1,
+                                                const typename A::T *x2, typename A::T *out2, size_t w1, size_t w2,
+                                                uint32_t row0, uint32_t total_slots, uint32_t h0, uint32_t heads,
+                                                uint32_t head_dim, uint32_t lo, uint32_t hi, uint32_t i0,
+                                                uint32_t step, float2 (*cs_all)[kMaxHalf / R]) {
+    using T = typename A::T;
+    constexpr int U = FELLM_ROPE_UNROLL;
+    float2 sc1[KIND == kRopePass || R > 1 ? 1 : PV];
+    if constexpr (KIND != kRopePass && R == 1) {
+#pragma unroll
+        for (int k = 0; k < PV; ++k) sc1[k] = cs_all[0][i0 + k];
+    }
+    uint32_t slot = threadIdx.x / (kRopeBlock / step);
+    uint32_t rr = slot / heads, hd = slot % heads;
+    for (; slot < total_slots; slot += step * U) {
+        float e[U][2 * PV];
+        uint32_t srr[U];
+        size_t off[U];
+        bool first[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t h = h0 + hd;
+            first[u] = h < nh1;
+            srr[u] = rr;
+            off[u] = first[u] ? (size_t)(row0 + rr) * w1 + (size_t)h * head_dim
+                              : (size_t)(row0 + rr) * w2 + (size_t)(h - nh1) * head_dim;
+            if (slot + u * step < total_slots) {
+                const T *src = (first[u] ? x1 : x2) + off[u];
+                if constexpr (KIND == kRopeSplit) {
+                    float a[PV], b[PV];
+                    act_load<A, PV>(src + lo, a);
+                    act_load<A, PV>(src + hi, b);
+#pragma unroll
+                    for (int k = 0; k < PV; ++k) {
+                        e[u][k] = a[k];
+                        e[u][PV + k] = b[k];
+                    }
+                } else if constexpr (sizeof(T) * 2 * PV > 16) {
+                    float a[PV], b[PV];
+                    act_load<A, PV>(src + lo, a);
+                    act_load<A, PV>(src + lo + PV, b);
+#pragma unroll
+                    for (int k = 0; k < PV; ++k) {
+                        e[u][k] = a[k];
+                        e[u][PV + k] = b[k];
+                    }
+                } else {
+                    act_load<A, 2 * PV>(src + lo, e[u]);
+                }
+            }
+            hd += step;
+            while (hd >= heads) {
+                hd -= heads;
+                ++rr;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (slot + u * step >= total_slots) continue;
+            const T *src = (first[u] ? x1 : x2) + off[u];
+            T *dst = (first[u] ? out1 : out2);
+            if (!dst) continue;
+            dst += off[u];
+            if constexpr (KIND == kRopePass) {
+                if (dst == src) continue;  // in place: the span is already there
+            } else {
+#pragma unroll
+                for (int k = 0; k < PV; ++k) {
+                    const float2 sc = R == 1 ? sc1[k] : cs_all[srr[u]][i0 + k];  // (sin, cos)
+                    const int ia = KIND == kRopeSplit ? k : 2 * k, ib = KIND == kRopeSplit ? PV + k : 2 * k + 1;
+                    const float a = e[u][ia], b = e[u][ib];
+                    e[u][ia] = a * sc.y - b * sc.x;
+                    e[u][ib] = a * sc.x + b * sc.y;
+                }
+            }
+            if constexpr (KIND == kRopeSplit) {
+                float a[PV], b[PV];
+#pragma unroll
+                for (int k = 0; k < PV; ++k) {
+                    a[k] = e[u][k];
+                    b[k] = e[u][PV + k];
+                }
+                act_store<A, PV>(dst + lo, a);
+                act_store<A, PV>(dst + hi, b);
+            } else {
+                act_store<A, 2 * PV>(dst + lo, e[u]);
+            }
+        }
+    }
+}
+
 // MODE 0: rotate x1 -> out1 and x2 -> out2.
 // MODE 1: additionally write rotated x2 (K) and x3 (V) into the paged cache
 //         (cache element type C).
@@ -296,6 +405,24 @@ __device__ __forceinline__ void rope_block(
     // enumerate items one by one with divisions.
     const bool fixed_item = items_head <= kRopeBlock && kRopeBlock % items_head == 0;
     const uint32_t total_slots = nrows * heads;
+    if constexpr (MODE == 0 && FELLM_ROPE_FAST && R == 1) {
+        if (fixed_item) {
+            const uint32_t it = threadIdx.x % items_head;
+            uint32_t lo, hi;
+            item_offsets(it, n_rot, head_dim, rope_dim, pairing, PV, lo, hi);
+            const uint32_t step = kRopeBlock / items_head;
+            if (it >= n_rot)
+                rope_fast_slots<A, PV, R, kRopePass>(x1, out1, nh1, x2, out2, w1, w2, row0, total_slots, h0, heads,
+                                                     head_dim, lo, hi, 0, step, cs_all);
+            else if (hi == lo + PV)
+                rope_fast_slots<A, PV, R, kRopeAdjacent>(x1, out1, nh1, x2, out2, w1, w2, row0, total_slots, h0,
+                                                         heads, head_dim, lo, hi, it * PV, step, cs_all);
+            else
+                rope_fast_slots<A, PV, R, kRopeSplit>(x1, out1, nh1, x2, out2, w1, w2, row0, total_slots, h0, heads,
+                                                      head_dim, lo, hi, it * PV, step, cs_all);
+            return;
+        }
+    }
     if (fixed_item) {
         const uint32_t it = threadIdx.x % items_head;
         const uint32_t step = kRopeBlock / items_head;
