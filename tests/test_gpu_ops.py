@@ -542,6 +542,30 @@ def test_rope_many_rows_shapes(ops, dev, kind, nq, nk, hd, rd, pairing, inplace,
     assert_exact(from_dev(qo), qr, f"q {rows} rows")
 
 
+@pytest.mark.parametrize("kind,group,residual,inplace", [("bf16", 2048, False, False), ("f16", 1024, True, False),
+                                                          ("bf16", 512, True, True), ("f32", 1024, True, False)])
+@pytest.mark.parametrize("rows", [16384, 20011])
+def test_add_rmsnorm_wavefront_rows(ops, dev, kind, group, residual, inplace, rows):
+    """Tens of thousands of rows of at most 4 KB (one wavefront per row):
+    plain RMSNorm and the residual form, h written in place over x; bit-exact
+    h, y within the RMSNorm tolerance."""
+    rng = np.random.default_rng(rows + group)
+    x = random_stored(rng, (rows, group), kind)
+    w = rng.normal(1.0, 0.1, size=group).astype(np.float32)
+    xw = oracle.widen(x, kind)
+    if residual:
+        r = random_stored(rng, (rows, group), kind, sigma=4.0)
+        h_ref, y_ref = oracle.add_rmsnorm(x, r, w, 1e-5, kind)
+        xd = to_dev(x, kind, dev)
+        h_out = xd if inplace else None
+        h, y = ops.add_rmsnorm(xd, to_dev(r, kind, dev), torch.from_numpy(w).to(dev), 1e-5, h_out=h_out)
+        assert_exact(from_dev(h), h_ref, f"h {rows}x{group}")
+    else:
+        y_ref = oracle.narrow(oracle.rmsnorm(xw, w, 1e-5), kind)
+        y = ops.rmsnorm(to_dev(x, kind, dev), torch.from_numpy(w).to(dev), 1e-5)
+    assert_close(from_dev(y), y_ref, kind, what=f"y {rows}x{group}")
+
+
 @pytest.mark.parametrize("kind", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("rows,group", [(1024, 2048), (1031, 1000), (1024, 8192), (1029, 16384), (1024, 12288)])
 def test_add_rmsnorm_many_rows(ops, dev, kind, rows, group):
