@@ -51,6 +51,18 @@
 #ifndef FELLM_EMB_LOOP
 #define FELLM_EMB_LOOP 1
 #endif
+// Build knob: workgroup size of the plain Q4_K gather (parts of 8 outputs,
+// all of a thread's parts decoded before its stores).  Measured at
+// configs[2] (8192 Zipf rows of 3584, interleaved on one box): 128 threads
+// 13.3-13.4 us against 15.0-15.1 us for 256, 13.5-13.9 us for 64 and
+// 17.4-17.6 us for 512.  The fused gather + RMSNorm measured slower with 128
+// threads (23.2-23.5 against 21.8-22.0 us) and keeps FELLM_EMB_BLOCK.  Q6_K
+// stays on the part-by-part loop: on this all-parts layout it measured
+// 19.0-19.3 us with 256 threads (level with the loop's 19.4), 21.0-21.1 with
+// 128 and 22.1-22.7 with 64.
+#ifndef FELLM_EMB_Q4K_BLOCK
+#define FELLM_EMB_Q4K_BLOCK 128
+#endif
 // Build knob: workgroups per compute unit of the persistent, pipelined plain
 // gather (0: one workgroup per row).  Measured at configs[1] (4096 f16 rows of
 // 4096, interleaved on one box): one workgroup per row 13.2-13.4 us; 2 per CU
@@ -300,12 +312,12 @@ constexpr int kEmbBlock = FELLM_EMB_BLOCK;
 // into registers before storing anything, so all of its loads are in flight
 // together.  MAXC == 0 selects a looping variant for rows longer than
 // 8 * kEmbBlock parts (no fused norm).
-template <typename D, typename O, int MAXC, bool NORM>
-__global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
+template <typename D, typename O, int MAXC, bool NORM, int BLOCK = kEmbBlock>
+__global__ __launch_bounds__(BLOCK) void embedding_kernel(
     const uint8_t *__restrict__ table, uint64_t vocab, uint32_t dim, const uint32_t *__restrict__ ids,
     typename O::T *__restrict__ h, typename O::T *__restrict__ y, const float *__restrict__ w, float eps,
     uint32_t *__restrict__ err) {
-    __shared__ float red[kEmbBlock / kWave];
+    __shared__ float red[BLOCK / kWave];
     const uint32_t row = blockIdx.x;
     const uint32_t id = ids ? ids[row] : row;  // no ids: row r of the table (Cast's dequantization)
     const bool bad = id >= vocab;
@@ -320,9 +332,9 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
         // are built, so their latency overlaps the staging and the barrier.
         typename D::Raw raw0{};
         if (threadIdx.x < parts) raw0 = D::load(src, threadIdx.x);
-        for (uint32_t t = threadIdx.x; t < dim / 64; t += kEmbBlock) stage_lds[t] = D::stage(src, t);
+        for (uint32_t t = threadIdx.x; t < dim / 64; t += BLOCK) stage_lds[t] = D::stage(src, t);
         __syncthreads();
-        for (uint32_t p = threadIdx.x; p < parts; p += kEmbBlock) {
+        for (uint32_t p = threadIdx.x; p < parts; p += BLOCK) {
             float v[D::OUT];
             D::finish(p == threadIdx.x ? raw0 : D::load(src, p), p, stage_lds, v);
             if (bad) {
@@ -333,7 +345,7 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
         }
         return;
     } else if constexpr (MAXC == 0) {
-        for (uint32_t p = threadIdx.x; p < parts; p += kEmbBlock) {
+        for (uint32_t p = threadIdx.x; p < parts; p += BLOCK) {
             float v[D::OUT];
             D::decode(src, p, v);
             if (bad) {
@@ -350,20 +362,20 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
             typename D::Raw raw[MAXC];
 #pragma unroll
             for (int c = 0; c < MAXC; ++c) {
-                const uint32_t p = c * kEmbBlock + threadIdx.x;
+                const uint32_t p = c * BLOCK + threadIdx.x;
                 if (p < parts) raw[c] = D::load(src, p);
             }
-            for (uint32_t t = threadIdx.x; t < dim / 64; t += kEmbBlock) stage_lds[t] = D::stage(src, t);
+            for (uint32_t t = threadIdx.x; t < dim / 64; t += BLOCK) stage_lds[t] = D::stage(src, t);
             __syncthreads();
 #pragma unroll
             for (int c = 0; c < MAXC; ++c) {
-                const uint32_t p = c * kEmbBlock + threadIdx.x;
+                const uint32_t p = c * BLOCK + threadIdx.x;
                 if (p < parts) D::finish(raw[c], p, stage_lds, v[c]);
             }
         }
 #pragma unroll
         for (int c = 0; c < MAXC; ++c) {
-            const uint32_t p = c * kEmbBlock + threadIdx.x;
+            const uint32_t p = c * BLOCK + threadIdx.x;
             if (p < parts) {
                 if constexpr (!D::STAGED) D::decode(src, p, v[c]);
 #pragma unroll
@@ -376,15 +388,15 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_kernel(
         if constexpr (!NORM) {
 #pragma unroll
             for (int c = 0; c < MAXC; ++c) {
-                const uint32_t p = c * kEmbBlock + threadIdx.x;
+                const uint32_t p = c * BLOCK + threadIdx.x;
                 if (p < parts) store_part<D, O, true>(h + obase, p, v[c]);
             }
         } else {
-            ss = block_sum<kEmbBlock>(ss, red);
+            ss = block_sum<BLOCK>(ss, red);
             const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
 #pragma unroll
             for (int c = 0; c < MAXC; ++c) {
-                const uint32_t p = c * kEmbBlock + threadIdx.x;
+                const uint32_t p = c * BLOCK + threadIdx.x;
                 if (p < parts) {
                     if (h) store_part<D, O, FELLM_EMB_NORM_NT>(h + obase, p, v[c]);
                     float o[D::OUT];
@@ -513,6 +525,21 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
             }
         }
         constexpr bool regs = requires { D::ALL_PARTS_IN_REGS; };
+        if constexpr (regs && FELLM_EMB_Q4K_BLOCK != kEmbBlock) {
+            constexpr int B = FELLM_EMB_Q4K_BLOCK;
+            const uint32_t ch = (D::parts(dim) + B - 1) / B;
+#define FELLM_EMB_B(C)                                                                                         \
+    if (ch <= C) {                                                                                             \
+        FELLM_LAUNCH((embedding_kernel<D, O, C, false, B>), grid, dim3(B), lds, s, tb, vocab, dim, ids, (TO *)h, \
+                     nullptr, nullptr, 0.0f, err);                                                             \
+        return launch_status();                                                                                \
+    }
+            FELLM_EMB_B(1)
+            FELLM_EMB_B(2)
+            FELLM_EMB_B(4)
+            FELLM_EMB_B(8)
+#undef FELLM_EMB_B
+        }
         if (FELLM_EMB_LOOP && !regs) {
             FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, lds, s, tb, vocab, dim, ids, (TO *)h,
                                nullptr, nullptr, 0.0f, err);
