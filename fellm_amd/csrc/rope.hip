@@ -46,6 +46,17 @@ namespace fellm {
 namespace {
 
 constexpr int kRopeBlock = 256;
+// Build knobs: workgroup size of the prefill RoPE launch with one row per
+// workgroup (BLOCK1) and with row groups (BLOCKN).  Measured interleaved on
+// one box: configs[1] (one row) 128 threads 14.6-14.7 us, level with 256
+// (14.4-15.5), 512 18.9-19.4; configs[4] (four rows) 256 59.1-59.6 us, 128
+// 64.1-64.4, 512 61.9-62.4.
+#ifndef FELLM_ROPE_BLOCK1
+#define FELLM_ROPE_BLOCK1 256
+#endif
+#ifndef FELLM_ROPE_BLOCKN
+#define FELLM_ROPE_BLOCKN 256
+#endif
 constexpr uint32_t kMaxHalf = 512;  // rope_dim <= 1024
 
 struct KvDev {
@@ -246,7 +257,7 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
 // (the only caller) the thread's PV (sin, cos) pairs are read from LDS once.
 constexpr int kRopePass = 0, kRopeAdjacent = 1, kRopeSplit = 2;
 
-template <typename A, int PV, int R, int KIND>
+template <typename A, int PV, int R, int KIND, int BLOCK>
 __device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typename A::T *out1, uint32_t nh1,
                                                 const typename A::T *x2, typename A::T *out2, size_t w1, size_t w2,
                                                 uint32_t row0, uint32_t total_slots, uint32_t h0, uint32_t heads,
@@ -259,7 +270,7 @@ __device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typenam
 #pragma unroll
         for (int k = 0; k < PV; ++k) sc1[k] = cs_all[0][i0 + k];
     }
-    uint32_t slot = threadIdx.x / (kRopeBlock / step);
+    uint32_t slot = threadIdx.x / (BLOCK / step);
     uint32_t rr = slot / heads, hd = slot % heads;
     for (; slot < total_slots; slot += step * U) {
         float e[U][2 * PV];
@@ -346,7 +357,7 @@ __device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typenam
 // the R rows.
 // The work of workgroup `bid` of a RoPE launch (every thread calls it;
 // contains a barrier).  cs_all / kbase_all: the LDS tables below.
-template <typename A, typename C, int PV, int MODE, int R>
+template <typename A, typename C, int PV, int MODE, int R, int BLOCK = kRopeBlock>
 __device__ __forceinline__ void rope_block(
     // x1/out1 and x2/out2 may alias (in-place rotation): no __restrict__.
     const typename A::T *x1, typename A::T *out1, uint32_t nh1,
@@ -360,7 +371,7 @@ __device__ __forceinline__ void rope_block(
     const uint32_t part = bid % hsplit;
     const uint32_t row0 = bid / hsplit * R;
     const uint32_t half = rope_dim / 2;
-    for (uint32_t t = threadIdx.x; t < R * half; t += kRopeBlock) {
+    for (uint32_t t = threadIdx.x; t < R * half; t += BLOCK) {
         const uint32_t rr = t / half, i = t % half;
         const uint32_t row = row0 + rr;
         if (row >= rows) continue;
@@ -403,29 +414,29 @@ __device__ __forceinline__ void rope_block(
     // step, U slots per batch: all U loads are issued before any rotation or
     // store, so each thread keeps U 16-byte requests in flight.  Other shapes
     // enumerate items one by one with divisions.
-    const bool fixed_item = items_head <= kRopeBlock && kRopeBlock % items_head == 0;
+    const bool fixed_item = items_head <= BLOCK && BLOCK % items_head == 0;
     const uint32_t total_slots = nrows * heads;
     if constexpr (MODE == 0 && FELLM_ROPE_FAST && R == 1) {
         if (fixed_item) {
             const uint32_t it = threadIdx.x % items_head;
             uint32_t lo, hi;
             item_offsets(it, n_rot, head_dim, rope_dim, pairing, PV, lo, hi);
-            const uint32_t step = kRopeBlock / items_head;
+            const uint32_t step = BLOCK / items_head;
             if (it >= n_rot)
-                rope_fast_slots<A, PV, R, kRopePass>(x1, out1, nh1, x2, out2, w1, w2, row0, total_slots, h0, heads,
+                rope_fast_slots<A, PV, R, kRopePass, BLOCK>(x1, out1, nh1, x2, out2, w1, w2, row0, total_slots, h0, heads,
                                                      head_dim, lo, hi, 0, step, cs_all);
             else if (hi == lo + PV)
-                rope_fast_slots<A, PV, R, kRopeAdjacent>(x1, out1, nh1, x2, out2, w1, w2, row0, total_slots, h0,
+                rope_fast_slots<A, PV, R, kRopeAdjacent, BLOCK>(x1, out1, nh1, x2, out2, w1, w2, row0, total_slots, h0,
                                                          heads, head_dim, lo, hi, it * PV, step, cs_all);
             else
-                rope_fast_slots<A, PV, R, kRopeSplit>(x1, out1, nh1, x2, out2, w1, w2, row0, total_slots, h0, heads,
+                rope_fast_slots<A, PV, R, kRopeSplit, BLOCK>(x1, out1, nh1, x2, out2, w1, w2, row0, total_slots, h0, heads,
                                                       head_dim, lo, hi, it * PV, step, cs_all);
             return;
         }
     }
     if (fixed_item) {
         const uint32_t it = threadIdx.x % items_head;
-        const uint32_t step = kRopeBlock / items_head;
+        const uint32_t step = BLOCK / items_head;
         uint32_t slot = threadIdx.x / items_head;
         uint32_t rr = slot / heads, hd = slot % heads;
         for (; slot < total_slots; slot += step * FELLM_ROPE_UNROLL) {
@@ -453,7 +464,7 @@ __device__ __forceinline__ void rope_block(
             }
         }
     } else {
-        for (uint32_t t = threadIdx.x; t < total_slots * items_head; t += kRopeBlock) {
+        for (uint32_t t = threadIdx.x; t < total_slots * items_head; t += BLOCK) {
             const uint32_t it = t % items_head, slot = t / items_head;
             const uint32_t rr = slot / heads, hd = h0 + slot % heads;
             float e[2 * PV];
@@ -464,16 +475,17 @@ __device__ __forceinline__ void rope_block(
     }
 }
 
-template <typename A, typename C, int PV, int MODE, int R>
-__global__ __launch_bounds__(kRopeBlock) void rope_kernel(
+template <typename A, typename C, int PV, int MODE, int R, int BLOCK = kRopeBlock>
+__global__ __launch_bounds__(BLOCK) void rope_kernel(
     const typename A::T *x1, typename A::T *out1, uint32_t nh1, const typename A::T *x2, typename A::T *out2,
     uint32_t nh2, const typename A::T *__restrict__ x3, uint32_t rows, uint32_t head_dim, uint32_t rope_dim,
     uint32_t pairing, const float *__restrict__ inv_freqs, const uint32_t *__restrict__ rope_pos, uint32_t pos0,
     const uint32_t *__restrict__ kv_pos, KvDev kv, uint32_t *__restrict__ err, uint32_t hsplit) {
     __shared__ float2 cs_all[R][kMaxHalf / R];
     __shared__ uint64_t kbase_all[R];
-    rope_block<A, C, PV, MODE, R>(x1, out1, nh1, x2, out2, nh2, x3, rows, head_dim, rope_dim, pairing, inv_freqs,
-                                  rope_pos, pos0, kv_pos, kv, err, hsplit, blockIdx.x, cs_all, kbase_all);
+    rope_block<A, C, PV, MODE, R, BLOCK>(x1, out1, nh1, x2, out2, nh2, x3, rows, head_dim, rope_dim, pairing,
+                                         inv_freqs, rope_pos, pos0, kv_pos, kv, err, hsplit, blockIdx.x, cs_all,
+                                         kbase_all);
 }
 
 // Rows per workgroup.  Measured on MI355X (q+k, 32/8 heads, hd 128): at
@@ -581,7 +593,8 @@ extern "C" int fellm_rocm_rope(const void *x1, void *out1, uint32_t n_heads1, co
         auto go = [&]<int PV, int RR>() {
             const uint32_t groups = (rows + RR - 1) / RR;
             const uint32_t hs = rope_head_split(groups, n_heads1 + (x2 ? n_heads2 : 0));
-            FELLM_LAUNCH((rope_kernel<A, F16, PV, 0, RR>), dim3(groups * hs), dim3(kRopeBlock), 0, s,
+            constexpr int B = RR == 1 ? FELLM_ROPE_BLOCK1 : FELLM_ROPE_BLOCKN;
+            FELLM_LAUNCH((rope_kernel<A, F16, PV, 0, RR, B>), dim3(groups * hs), dim3(B), 0, s,
                                (const T *)x1, (T *)out1, n_heads1, (const T *)x2, (T *)out2, x2 ? n_heads2 : 0,
                                nullptr, rows, head_dim, rope_dim, pairing, inv_freqs, positions, position0, nullptr,
                                KvDev{}, nullptr, hs);
