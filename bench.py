@@ -41,8 +41,12 @@ METRIC = "achieved HBM GB/s (% of peak) per fused op; tokens/s for op chain at 8
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # The GPU idles at ~110 MHz and its clock ramps up under load: a short
+    # warm-up leaves part of the timed steps on the ramp (configs[1] chain:
+    # 35.3 M tokens/s at 5 warm-up / 50 timed steps, 37.2-37.6 M from 200
+    # warm-up steps on, flat to 2000 / 2000).
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--sets", type=int, default=3, help="rotating input sets")
     ap.add_argument("--only", default=None, help="with --suite: comma-separated suite entries to run")
     ap.add_argument("--no-cpu-baseline", action="store_true")
