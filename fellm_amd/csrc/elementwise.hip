@@ -118,7 +118,9 @@ __global__ __launch_bounds__(kEwBlock) void mathf_kernel(uint32_t fn, const floa
                                                          float *__restrict__ out, uint64_t n) {
     const uint64_t stride = (uint64_t)gridDim.x * kEwBlock;
     for (uint64_t i = (uint64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += stride)
-        out[i] = fn == 0 ? logf_glibc(in[i]) : sqrtf_rn(in[i]);
+        out[i] = fn == 0   ? logf_glibc(in[i])
+                 : fn == 1 ? sqrtf_rn(in[i])
+                           : __uint_as_float((uint32_t)BF16HW::store(in[i]));  // bf16 bits in the low half
 }
 
 // Largest bit distance between silu_fast and silu over every f32 g of the
@@ -192,7 +194,7 @@ extern "C" int fellm_rocm_silu_gate(const void *gate, const void *up, uint32_t i
     if (!gate || !up || !out) return FELLM_ERR_ARITY;
     hipStream_t s = as_stream(stream);
     return dispatch_act(in_dtype, [&]<typename I>() -> int {
-        if (out_dtype == in_dtype) return launch_silu<I, I>(gate, up, out, n_elems, s);
+        if (out_dtype == in_dtype) return launch_silu<I, typename HwStore<I>::type>(gate, up, out, n_elems, s);
         if (out_dtype == FELLM_DTYPE_F32) return launch_silu<I, F32>(gate, up, out, n_elems, s);
         return FELLM_ERR_DTYPE;
     });
@@ -253,7 +255,7 @@ extern "C" void fellm_rocm_timing_disarm(void) { fellm::g_launch_timing = fellm:
 
 extern "C" int fellm_rocm_mathf(uint32_t fn, const float *in, float *out, uint64_t n, void *stream) {
     using namespace fellm;
-    if (fn > 1) return FELLM_ERR_SHAPE;
+    if (fn > 2) return FELLM_ERR_SHAPE;
     if (n == 0) return FELLM_OK;
     if (!in || !out) return FELLM_ERR_ARITY;
     FELLM_LAUNCH(mathf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), fn, in, out, n);

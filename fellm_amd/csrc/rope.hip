@@ -29,13 +29,23 @@
 #define FELLM_ROPE_NT 2
 #endif
 // Build knob: MODE 0 slot walk with per-thread constants hoisted (1) or the
-// generic walk shared with MODE 1 (0), for one row per workgroup.  Measured
-// interleaved on one box: configs[1] q+k 15.0-15.4 against 15.5-16.3 us, f32
-// and split-half pairings 4-8% faster.  With four rows per workgroup the
-// hoisted walk needs 67 VGPRs for bf16 (7 waves against 8) and measured 61.4
-// against 59.5-60.2 us at configs[4], so row groups keep the generic walk.
+// generic walk shared with MODE 1 (0).  Measured interleaved on one box:
+// configs[1] q+k 15.0-15.4 against 15.5-16.3 us, f32 and split-half
+// pairings 4-8% faster.
 #ifndef FELLM_ROPE_FAST
 #define FELLM_ROPE_FAST 1
+#endif
+// Build knobs: the hoisted walk serves row groups of up to FAST_MAX_R rows,
+// and prefill RoPE launches ask for FELLM_ROPE_WAVES waves per SIMD.  With
+// row groups the hoisted walk needs 67 VGPRs for bf16 (7 waves): alone it
+// measured 61.4-62.8 us at configs[4]; with 8 waves requested it spills
+// 20 bytes per lane for bf16 and measured 57.0-57.1 against 58.7-59.3 us for
+// the generic walk (interleaved on one box), configs[1] level.
+#ifndef FELLM_ROPE_FAST_MAX_R
+#define FELLM_ROPE_FAST_MAX_R 4
+#endif
+#ifndef FELLM_ROPE_WAVES
+#define FELLM_ROPE_WAVES 8
 #endif
 // Build knob: (row, head) slots each thread loads before rotating/storing.
 #ifndef FELLM_ROPE_UNROLL
@@ -272,20 +282,23 @@ __device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typenam
     }
     uint32_t slot = threadIdx.x / (BLOCK / step);
     uint32_t rr = slot / heads, hd = slot % heads;
+    // Per slot only its row and head stay live across the batch; the
+    // element offset is recomputed at the store (cheaper in registers than
+    // keeping a 64-bit offset per slot).
+    auto slot_off = [&](uint32_t r, uint32_t h) -> size_t {
+        return h < nh1 ? (size_t)(row0 + r) * w1 + (size_t)h * head_dim
+                       : (size_t)(row0 + r) * w2 + (size_t)(h - nh1) * head_dim;
+    };
     for (; slot < total_slots; slot += step * U) {
         float e[U][2 * PV];
-        uint32_t srr[U];
-        size_t off[U];
-        bool first[U];
+        uint32_t srr[U], sh[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t h = h0 + hd;
-            first[u] = h < nh1;
             srr[u] = rr;
-            off[u] = first[u] ? (size_t)(row0 + rr) * w1 + (size_t)h * head_dim
-                              : (size_t)(row0 + rr) * w2 + (size_t)(h - nh1) * head_dim;
+            sh[u] = h;
             if (slot + u * step < total_slots) {
-                const T *src = (first[u] ? x1 : x2) + off[u];
+                const T *src = (h < nh1 ? x1 : x2) + slot_off(rr, h);
                 if constexpr (KIND == kRopeSplit) {
                     float a[PV], b[PV];
                     act_load<A, PV>(src + lo, a);
@@ -317,10 +330,12 @@ __device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typenam
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (slot + u * step >= total_slots) continue;
-            const T *src = (first[u] ? x1 : x2) + off[u];
-            T *dst = (first[u] ? out1 : out2);
+            const bool first = sh[u] < nh1;
+            const size_t off = slot_off(srr[u], sh[u]);
+            const T *src = (first ? x1 : x2) + off;
+            T *dst = (first ? out1 : out2);
             if (!dst) continue;
-            dst += off[u];
+            dst += off;
             if constexpr (KIND == kRopePass) {
                 if (dst == src) continue;  // in place: the span is already there
             } else {
@@ -416,7 +431,7 @@ __device__ __forceinline__ void rope_block(
     // enumerate items one by one with divisions.
     const bool fixed_item = items_head <= BLOCK && BLOCK % items_head == 0;
     const uint32_t total_slots = nrows * heads;
-    if constexpr (MODE == 0 && FELLM_ROPE_FAST && R == 1) {
+    if constexpr (MODE == 0 && FELLM_ROPE_FAST && R <= FELLM_ROPE_FAST_MAX_R) {
         if (fixed_item) {
             const uint32_t it = threadIdx.x % items_head;
             uint32_t lo, hi;
@@ -476,7 +491,8 @@ __device__ __forceinline__ void rope_block(
 }
 
 template <typename A, typename C, int PV, int MODE, int R, int BLOCK = kRopeBlock>
-__global__ __launch_bounds__(BLOCK) void rope_kernel(
+__global__ __launch_bounds__(BLOCK)
+__attribute__((amdgpu_waves_per_eu(MODE == 0 && BLOCK == 256 ? FELLM_ROPE_WAVES : 1))) void rope_kernel(
     const typename A::T *x1, typename A::T *out1, uint32_t nh1, const typename A::T *x2, typename A::T *out2,
     uint32_t nh2, const typename A::T *__restrict__ x3, uint32_t rows, uint32_t head_dim, uint32_t rope_dim,
     uint32_t pairing, const float *__restrict__ inv_freqs, const uint32_t *__restrict__ rope_pos, uint32_t pos0,
@@ -786,7 +802,7 @@ void decode_step_kernel(StepArgs<A> p) {
     } else if (role == 1) {
         add_rmsnorm_row<A, A, 256, 8, NCHUNK, true, true>(p.x, p.r, p.h, p.w, p.y, p.group, p.eps, b, red);
     } else {
-        silu_gate_blocks<A, A, 8, 2>(p.gate, p.up, p.act, p.n_silu, b, p.nb_silu, tab_lds);
+        silu_gate_blocks<A, typename HwStore<A>::type, 8, 2>(p.gate, p.up, p.act, p.n_silu, b, p.nb_silu, tab_lds);
     }
 }
 

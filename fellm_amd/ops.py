@@ -468,6 +468,14 @@ def sqrtf(x):
     return out
 
 
+def bf16_store_bits(x):
+    """bf16 bits (int32 tensor) of the device's bf16 activation store of f32 ``x`` (self-check)."""
+    _dev(x)
+    out = torch.empty_like(x)
+    _lib.call("fellm_rocm_mathf", 2, _p(x), _p(out), x.numel(), _stream())
+    return out.view(torch.int32)
+
+
 def sincosf(x):
     """Device glibc-exact (sinf(x), cosf(x)) (self-check of the restatement RoPE uses)."""
     _dev(x)

@@ -9,6 +9,9 @@
   host's glibc logf, all 2^32 inputs;
 * the device correctly rounded sqrtf against numpy's IEEE float32 sqrt, all
   2^32 inputs;
+* the bf16 activation store (round to nearest even, quiet NaN with its top
+  payload bits) against the oracle's rounding, all 2^32 inputs, bits exact
+  including NaNs;
 * SwiGLU's silu(g) = g / (1 + exp(-g)) (kernels/swiglu.rs:5-7) through the
   product kernel with up = 1, against the oracle, all 2^32 values of g.
   silu depends on g alone, so this proves the kernel's exp + division path
@@ -53,6 +56,10 @@ def _host_logf(start: int) -> np.ndarray:
 def _host_sqrtf(start: int) -> np.ndarray:
     with np.errstate(invalid="ignore"):
         return np.sqrt(_bits(start))
+
+
+def _host_bf16(start: int) -> np.ndarray:
+    return oracle.f32_to_bf16_bits(_bits(start)).astype(np.uint32).view(np.float32)
 
 
 def _host_silu(start: int) -> np.ndarray:
@@ -128,3 +135,13 @@ def test_sqrtf_all_inputs(dev):
         return ops.sqrtf(torch.from_numpy(_bits(start)).to(dev)).cpu().numpy()
 
     _sweep(dev_fn, _host_sqrtf, "sqrtf")
+
+
+def test_bf16_store_all_inputs(dev):
+    from fellm_amd import ops
+
+    def dev_fn(start):
+        bits = ops.bf16_store_bits(torch.from_numpy(_bits(start)).to(dev)).cpu().numpy()
+        return bits.view(np.uint32).view(np.float32)
+
+    _sweep(dev_fn, _host_bf16, "bf16 store")
