@@ -60,6 +60,16 @@
 // stays on the part-by-part loop: on this all-parts layout it measured
 // 19.0-19.3 us with 256 threads (level with the loop's 19.4), 21.0-21.1 with
 // 128 and 22.1-22.7 with 64.
+// Build knob: plain gathers through the looping staged layout (Q6_K)
+// assemble each row in LDS and write it with 16-byte stores (1), or store
+// each part's four 4-element runs directly (0).  A Q6_K part's outputs are
+// four 8-byte runs, so the direct stores issue 2.3x the store instructions
+// of Q4_K's 16-byte parts for the same bytes (SQ_INSTS_VMEM_WR).  Measured
+// at configs[2], interleaved on one box: 18.1-18.2 against 19.2-19.4 us.
+// The Q4_K layouts already store 16 bytes per part.
+#ifndef FELLM_EMB_LDS_OUT
+#define FELLM_EMB_LDS_OUT 1
+#endif
 #ifndef FELLM_EMB_Q4K_BLOCK
 #define FELLM_EMB_Q4K_BLOCK 128
 #endif
@@ -312,7 +322,7 @@ constexpr int kEmbBlock = FELLM_EMB_BLOCK;
 // into registers before storing anything, so all of its loads are in flight
 // together.  MAXC == 0 selects a looping variant for rows longer than
 // 8 * kEmbBlock parts (no fused norm).
-template <typename D, typename O, int MAXC, bool NORM, int BLOCK = kEmbBlock>
+template <typename D, typename O, int MAXC, bool NORM, int BLOCK = kEmbBlock, bool LDS_OUT = false>
 __global__ __launch_bounds__(BLOCK) void embedding_kernel(
     const uint8_t *__restrict__ table, uint64_t vocab, uint32_t dim, const uint32_t *__restrict__ ids,
     typename O::T *__restrict__ h, typename O::T *__restrict__ y, const float *__restrict__ w, float eps,
@@ -334,6 +344,11 @@ __global__ __launch_bounds__(BLOCK) void embedding_kernel(
         if (threadIdx.x < parts) raw0 = D::load(src, threadIdx.x);
         for (uint32_t t = threadIdx.x; t < dim / 64; t += BLOCK) stage_lds[t] = D::stage(src, t);
         __syncthreads();
+        using TO = typename O::T;
+        // LDS_OUT: the decoded row is assembled in LDS (after the scale
+        // slots) in natural order and then written with 16-byte
+        // non-temporal stores, instead of each part storing its short runs.
+        TO *out_lds = reinterpret_cast<TO *>(stage_lds + dim / 64);
         for (uint32_t p = threadIdx.x; p < parts; p += BLOCK) {
             float v[D::OUT];
             D::finish(p == threadIdx.x ? raw0 : D::load(src, p), p, stage_lds, v);
@@ -341,7 +356,23 @@ __global__ __launch_bounds__(BLOCK) void embedding_kernel(
 #pragma unroll
                 for (int k = 0; k < D::OUT; ++k) v[k] = 0.0f;
             }
-            store_part<D, O, true>(h + obase, p, v);
+            if constexpr (LDS_OUT) {
+#pragma unroll
+                for (int r = 0; r < D::RUNS; ++r) {
+                    Pack<TO, D::RUNLEN> pk;
+#pragma unroll
+                    for (int k = 0; k < D::RUNLEN; ++k) pk.v[k] = O::store(v[r * D::RUNLEN + k]);
+                    *reinterpret_cast<Pack<TO, D::RUNLEN> *>(out_lds + D::run_off(p, r)) = pk;
+                }
+            } else {
+                store_part<D, O, true>(h + obase, p, v);
+            }
+        }
+        if constexpr (LDS_OUT) {
+            constexpr int W = 16 / sizeof(TO);
+            __syncthreads();
+            for (uint32_t i = threadIdx.x; i < dim / W; i += BLOCK)
+                store_pack_nt<TO, W>(h + obase + (size_t)i * W, *reinterpret_cast<const Pack<TO, W> *>(out_lds + i * W));
         }
         return;
     } else if constexpr (MAXC == 0) {
@@ -539,6 +570,14 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
             FELLM_EMB_B(4)
             FELLM_EMB_B(8)
 #undef FELLM_EMB_B
+        }
+        if constexpr (D::STAGED && !regs && FELLM_EMB_LDS_OUT) {
+            const uint32_t out_bytes = dim * (uint32_t)sizeof(TO);
+            if (FELLM_EMB_LOOP && out_bytes % 16 == 0 && aligned_to(h, 16) && lds + out_bytes <= 65536) {
+                FELLM_LAUNCH((embedding_kernel<D, O, 0, false, kEmbBlock, true>), grid, block, lds + out_bytes, s, tb,
+                             vocab, dim, ids, (TO *)h, nullptr, nullptr, 0.0f, err);
+                return launch_status();
+            }
         }
         if (FELLM_EMB_LOOP && !regs) {
             FELLM_LAUNCH((embedding_kernel<D, O, 0, false>), grid, block, lds, s, tb, vocab, dim, ids, (TO *)h,
