@@ -445,11 +445,8 @@ __global__ __launch_bounds__(BLOCK) void embedding_kernel(
     }
 }
 
-// Plain (unquantized) gather, persistent: workgroup b copies rows b, b + G,
-// b + 2G, ... (G = the grid).  The id of the row after next is requested a
-// row ahead, and the next row's data are loaded before the current row is
-// stored, so neither the id's latency nor the data's is paid per row.  A
-// thread moves C parts of VEC elements per row.
+// One row's parts of this thread, for embedding_pipe_kernel below (an
+// out-of-range id reads row 0; the caller zeroes what it stores).
 template <typename D, int C>
 __device__ __forceinline__ void emb_pipe_load(const uint8_t *table, uint64_t vocab, uint64_t rb, uint32_t parts,
                                               uint32_t id, float (&v)[C][D::OUT]) {

@@ -15,6 +15,15 @@
 
 #include "norm_body.hpp"
 
+// Build knob: the one-wavefront-per-row layout reads the weights from one
+// LDS copy per workgroup (1) or from the caches per wavefront (0).  Per row
+// the f32 weights are twice the bytes of a 16-bit row, and two thirds of the
+// kernel's load instructions.  Measured at configs[4] (16384 x 2048 bf16,
+// interleaved on one box): 25.0-25.3 against 25.9-26.5 us.
+#ifndef FELLM_NORM_WAVE_WLDS
+#define FELLM_NORM_WAVE_WLDS 1
+#endif
+
 // Build knob: with many rows, rows of at most FELLM_NORM_WAVE_BYTES bytes
 // take one wavefront per row instead of one workgroup per row (0: never).
 // Measured on MI355X inside the op chains: 16384 x 2048 bf16 RMSNorm
@@ -139,6 +148,15 @@ __global__ __launch_bounds__(256) void add_rmsnorm_wave_kernel(
     using P = Pack<T, VEC>;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t row = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+    if constexpr (FELLM_NORM_WAVE_WLDS) {
+        // The workgroup's four rows share one copy of the weights in LDS
+        // (group floats, at most 8 KB), instead of each wavefront reading
+        // them from the caches.
+        extern __shared__ float4 w_lds4[];
+        for (uint32_t i = threadIdx.x; i < group / 4; i += 256) w_lds4[i] = reinterpret_cast<const float4 *>(w)[i];
+        __syncthreads();
+        w = reinterpret_cast<const float *>(w_lds4);
+    }
     if (row >= rows) return;  // whole wavefronts only: no block-level barrier follows
     const size_t off = (size_t)row * group;
     const uint32_t nvec = group / VEC;
@@ -190,14 +208,15 @@ int launch_wave(const void *x, const void *r, void *h, const float *w, void *y, 
     using TA = typename A::T;
     using TO = typename O::T;
     const dim3 grid((uint32_t)((rows + 3) / 4)), block(256);
+    const size_t wl = FELLM_NORM_WAVE_WLDS ? (size_t)group * sizeof(float) : 0;
     if (r == nullptr) {
-        FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, false, false>), grid, block, 0, s, (const TA *)x, nullptr,
+        FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, false, false>), grid, block, wl, s, (const TA *)x, nullptr,
                      nullptr, w, (TO *)y, group, (uint32_t)rows, eps);
     } else if (h == nullptr) {
-        FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, true, false>), grid, block, 0, s, (const TA *)x,
+        FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, true, false>), grid, block, wl, s, (const TA *)x,
                      (const TA *)r, nullptr, w, (TO *)y, group, (uint32_t)rows, eps);
     } else {
-        FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, true, true>), grid, block, 0, s, (const TA *)x,
+        FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, true, true>), grid, block, wl, s, (const TA *)x,
                      (const TA *)r, (TA *)h, w, (TO *)y, group, (uint32_t)rows, eps);
     }
     return launch_status();

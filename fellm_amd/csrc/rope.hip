@@ -264,7 +264,8 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
 // (uniform over its slots): 0 pass-through (unrotated span), 1 adjacent
 // pairs (e[2k], e[2k+1]) in one contiguous run, 2 split-half pairs
 // (e[k], e[PV+k]) in two runs `hi - lo` apart.  With one row per workgroup
-// (the only caller) the thread's PV (sin, cos) pairs are read from LDS once.
+// the thread's PV (sin, cos) pairs are read from LDS once; with row groups
+// they are read per slot from the slot's row.
 constexpr int kRopePass = 0, kRopeAdjacent = 1, kRopeSplit = 2;
 
 template <typename A, int PV, int R, int KIND, int BLOCK>
