@@ -81,6 +81,27 @@
 #ifndef FELLM_EMB_PIPE
 #define FELLM_EMB_PIPE 8
 #endif
+// Build knob: dense gathers in one-shot workgroups of this many threads per
+// row, every part of a thread loaded before its stores (0: the persistent
+// pipelined kernel when there are enough rows).
+#ifndef FELLM_EMB_DENSE_BLOCK
+#define FELLM_EMB_DENSE_BLOCK 0
+#endif
+// Build knob: workgroup size of the plain Q6_K gather that copies each raw
+// row segment into LDS with coalesced 16-byte loads and decodes it from there
+// (0: the part-by-part staged layout above), and the 256-element blocks a
+// workgroup takes (FELLM_EMB_Q6K_BPW; 0: the whole row).  Measured at
+// configs[2] (8192 Zipf rows of 3584, interleaved on one box), whole rows:
+// 64 threads 16.2-16.3 us, 128 17.6-17.7, 256 19.3-19.4 (the staged layout
+// 17.8-17.9); storing each part as soon as the next is decoded 16.6 (64) and
+// 17.6-17.8 (128); one wavefront per row walking rows with the next row's
+// chunks in flight 16.6-16.9 at 8 workgroups per CU, 17.2 at 4, 19.7 at 2.
+#ifndef FELLM_EMB_Q6K_LDS
+#define FELLM_EMB_Q6K_LDS 64
+#endif
+#ifndef FELLM_EMB_Q6K_BPW
+#define FELLM_EMB_Q6K_BPW 0
+#endif
 
 
 namespace fellm {
@@ -517,6 +538,126 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_pipe_kernel(
     if (bad_rows && threadIdx.x == 0 && err) atomicOr(err, 1u);
 }
 
+// Plain Q6_K gather through LDS.  A Q6_K row is dim/256 blocks of 210 bytes,
+// so blocks are only 2-byte aligned and a per-part layout reads each block
+// with short unaligned loads at 210-byte strides.  Here the workgroup first
+// copies the whole raw row into LDS with 16-byte loads of consecutive
+// addresses (the row's span rounded out to 16-byte boundaries, which never
+// leaves the pages the row lies on), then each thread decodes parts of 8
+// consecutive outputs from LDS and writes them with one 16-byte store of a
+// 16-bit output (a wavefront writes 1 KB of the row contiguously).
+// Output o = 8p' of block b, at n = o % 256 = 128 hh + 32 k + l:
+//   q  = ((ql[64 hh + 32 (k & 1) + l] >> 4 (k >> 1)) & 15)
+//        | ((qh[32 hh + l] >> 2k) & 3) << 4,
+//   y  = (d * sc[8 hh + l / 16 + 2k]) * (q - 32)      (dequant.rs:315-370).
+// NL 16-byte loads and NP parts per thread, all loads issued before the LDS
+// writes and all parts decoded before the stores.
+__device__ __forceinline__ uint64_t lds_u64_at(const uint32_t *w, uint32_t off) {
+    const uint32_t i = off / 4, sh = off % 4;
+    const uint32_t w0 = w[i], w1 = w[i + 1], w2 = w[i + 2];
+    return (uint64_t)__builtin_amdgcn_alignbyte(w1, w0, sh) |
+           ((uint64_t)__builtin_amdgcn_alignbyte(w2, w1, sh) << 32);
+}
+
+template <typename O, int BLOCK, int NL, int NP>
+__global__ __launch_bounds__(BLOCK) void q6k_gather_lds_kernel(const uint8_t *__restrict__ table, uint64_t vocab,
+                                                               uint32_t dim, const uint32_t *__restrict__ ids,
+                                                               uint32_t bpw, typename O::T *__restrict__ h,
+                                                               uint32_t *__restrict__ err) {
+    extern __shared__ uint4 raw_lds[];
+    // Workgroup = (row, segment of bpw blocks).
+    const uint32_t nb = dim / 256, nseg = (nb + bpw - 1) / bpw;
+    const uint32_t row = blockIdx.x / nseg, b0 = (blockIdx.x % nseg) * bpw;
+    const uint32_t nblk = nb - b0 < bpw ? nb - b0 : bpw;
+    const uint32_t id = ids[row];
+    const bool bad = id >= vocab;
+    if (bad && threadIdx.x == 0 && b0 == 0 && err) atomicOr(err, 1u);
+    const uint8_t *segp = table + (bad ? 0 : (uint64_t)id * nb * 210) + 210 * b0;
+    const uint32_t lead = (uint32_t)(reinterpret_cast<uintptr_t>(segp) & 15);
+    const uint4 *src = reinterpret_cast<const uint4 *>(segp - lead);
+    const uint32_t n16 = (lead + 210 * nblk + 15) / 16;
+    // Threads past the span re-read its last chunk (a cache hit), so every
+    // load is unconditional and the chunks stay in registers.
+    uint4 c[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const uint32_t j = i * BLOCK + threadIdx.x;
+        c[i] = src[j < n16 ? j : n16 - 1];
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) raw_lds[i * BLOCK + threadIdx.x] = c[i];  // LDS holds NL * BLOCK chunks
+    __syncthreads();
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(raw_lds);
+    const uint32_t parts = nblk * 32;
+    typename O::T *out = h + (size_t)row * dim + 256 * (size_t)b0;
+    float v[NP][8];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const uint32_t p = i * BLOCK + threadIdx.x;
+        if (p < parts) {
+            const uint32_t b = p / 32, n = 8 * (p % 32);
+            const uint32_t hh = n / 128, k = (n / 32) % 4, l = n % 32;
+            const uint32_t blk = lead + 210 * b;
+            const uint64_t ql = lds_u64_at(w, blk + 64 * hh + 32 * (k & 1) + l);
+            const uint64_t qh = lds_u64_at(w, blk + 128 + 32 * hh + l);
+            const uint32_t so = blk + 192 + 8 * hh + l / 16 + 2 * k;
+            const int32_t sc = (int8_t)(w[so / 4] >> (8 * (so % 4)));
+            const uint32_t dof = blk + 208;  // even, so the f16 never straddles a dword
+            const float d = half_bits_to_f32(w[dof / 4] >> (8 * (dof % 4)));
+            const float ds = d * (float)sc;
+            const uint32_t qs = 4 * (k >> 1), hs = 2 * k;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int32_t q = (int32_t)((((uint32_t)(ql >> (8 * e)) >> qs) & 15u) |
+                                            ((((uint32_t)(qh >> (8 * e)) >> hs) & 3u) << 4)) -
+                                  32;
+                v[i][e] = bad ? 0.0f : ds * (float)q;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const uint32_t p = i * BLOCK + threadIdx.x;
+        if (p < parts) store_f32_nt<O, 8>(out + 8 * (size_t)p, v[i]);
+    }
+}
+
+// Launches q6k_gather_lds_kernel when a thread's share fits the unrolled
+// counts (rows of up to 32768 elements at 128 threads); -1 otherwise.
+template <typename O>
+int launch_q6k_lds(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids, void *h,
+                   uint32_t *err, hipStream_t s) {
+    constexpr int B = FELLM_EMB_Q6K_LDS;
+    if constexpr (B == 0) {
+        return -1;
+    } else {
+        const uint32_t nb = dim / 256;
+        const uint32_t bpw = FELLM_EMB_Q6K_BPW && FELLM_EMB_Q6K_BPW < nb ? FELLM_EMB_Q6K_BPW : nb;
+        const uint64_t grid = (uint64_t)n_ids * ((nb + bpw - 1) / bpw);
+        if (grid > 0x7fffffffull) return -1;
+        const uint32_t n16 = (210 * bpw + 15 + 15) / 16;
+        const uint32_t nl = (n16 + B - 1) / B, np = (32 * bpw + B - 1) / B;
+        const uint8_t *tb = static_cast<const uint8_t *>(table);
+        using TO = typename O::T;
+        // Every thread writes its NL chunks; the segment's span (n16 chunks)
+        // plus the dword lds_u64_at may read past it fit below NL * B chunks.
+#define FELLM_Q6L(NL, NP)                                                                                      \
+    if (nl <= NL && np <= NP && (size_t)NL * B * 16 >= (size_t)n16 * 16 + 16) {                                \
+        FELLM_LAUNCH((q6k_gather_lds_kernel<O, B, NL, NP>), dim3((uint32_t)grid), dim3(B), (size_t)NL * B * 16, \
+                     s, tb, vocab, dim, ids, bpw, (TO *)h, err);                                               \
+        return launch_status();                                                                                \
+    }
+        FELLM_Q6L(1, 1)
+        FELLM_Q6L(1, 2)
+        FELLM_Q6L(2, 4)
+        FELLM_Q6L(4, 8)
+        FELLM_Q6L(8, 16)
+        FELLM_Q6L(16, 32)
+#undef FELLM_Q6L
+        return -1;
+    }
+}
+
 template <typename D, typename O>
 int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids,
                void *h, void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
@@ -551,6 +692,22 @@ int launch_emb(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *
                 FELLM_EMB_P(4) {}
 #undef FELLM_EMB_P
             }
+        }
+        if constexpr (requires { D::DENSE; } && FELLM_EMB_DENSE_BLOCK > 0) {
+            // One workgroup per row, every part of a thread loaded before its stores.
+            constexpr int B = FELLM_EMB_DENSE_BLOCK;
+            const uint32_t ch = (D::parts(dim) + B - 1) / B;
+#define FELLM_EMB_B(C)                                                                                         \
+    if (ch <= C) {                                                                                             \
+        FELLM_LAUNCH((embedding_kernel<D, O, C, false, B>), grid, dim3(B), lds, s, tb, vocab, dim, ids, (TO *)h, \
+                     nullptr, nullptr, 0.0f, err);                                                             \
+        return launch_status();                                                                                \
+    }
+            FELLM_EMB_B(1)
+            FELLM_EMB_B(2)
+            FELLM_EMB_B(4)
+            FELLM_EMB_B(8)
+#undef FELLM_EMB_B
         }
         constexpr bool regs = requires { D::ALL_PARTS_IN_REGS; };
         if constexpr (regs && FELLM_EMB_Q4K_BLOCK != kEmbBlock) {
@@ -609,6 +766,10 @@ int dispatch_table(const void *table, uint32_t table_dtype, uint64_t vocab, uint
             return launch_emb<Q4KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
         case FELLM_DTYPE_Q6K:
             if (dim % 256 || !aligned_to(table, 2)) return FELLM_ERR_SHAPE;
+            if (!w && ids && dim * sizeof(typename O::T) % 16 == 0) {
+                const int st = launch_q6k_lds<O>(table, vocab, dim, ids, n_ids, h, err, s);
+                if (st >= 0) return st;
+            }
             if (FELLM_EMB_STAGE) return launch_emb<Q6KStaged, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
             return launch_emb<Q6KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
         default:

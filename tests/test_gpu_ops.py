@@ -670,3 +670,23 @@ def test_zero_rows_are_noops(ops, dev):
     assert ids.numel() == 0 and wts.numel() == 0
     torch.cuda.synchronize()
 
+
+
+@pytest.mark.parametrize("offset", [2, 6, 10, 14])
+@pytest.mark.parametrize("dim", [256, 3584, 16384])
+def test_embedding_q6k_unaligned_table(ops, dev, offset, dim):
+    """Q6_K tables need only 2-byte alignment (210-byte blocks): a table that
+    starts `offset` bytes past a 16-byte boundary shifts every row's span
+    against the 16-byte loads that copy it; bit-exact against the oracle."""
+    from fellm_amd import synth
+
+    rng = np.random.default_rng(offset * 1000 + dim)
+    vocab = 97
+    table = synth.q6k_table(rng, vocab, dim)
+    ids = synth.zipf_ids(rng, 300, vocab)
+    ref = oracle.narrow(oracle.embedding(table, 14, vocab, dim, ids), "f16")
+    buf = torch.zeros(table.size + 16, dtype=torch.uint8, device=dev)
+    buf[offset:offset + table.size] = torch.from_numpy(table.reshape(-1)).to(dev)
+    got = ops.embedding(buf[offset:offset + table.size].view(table.shape), torch.from_numpy(ids.view(np.int32)).to(dev), dim=dim,
+                        qtype="q6k", out_dtype=KINDS["f16"])
+    assert_exact(from_dev(got), ref, f"embedding q6k table offset {offset} dim={dim}")
