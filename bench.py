@@ -146,6 +146,9 @@ def c3_ops(torch, ops, dev, n_sets, seed=3):
         Op("q4k_gather_rmsnorm", T * 2016 + 2 * out_b + T * 4,
            lambda s: ops.embedding_rmsnorm(q4, s["ids"], w, 1e-6, dim=D, qtype="q4k", h_out=s["out"],
                                            y_out=s["y"]), (1, T * 2016, 2 * out_b)),
+        Op("q6k_gather_rmsnorm", T * 2940 + 2 * out_b + T * 4,
+           lambda s: ops.embedding_rmsnorm(q6, s["ids"], w, 1e-6, dim=D, qtype="q6k", h_out=s["out"],
+                                           y_out=s["y"]), (1, T * 2940, 2 * out_b)),
     ]
     return chain, sets, T
 

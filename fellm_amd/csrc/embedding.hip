@@ -30,8 +30,14 @@
 #define FELLM_EMB_NT_LOAD 1
 #endif
 // Build knob: non-temporal stores for the fused gather + RMSNorm (1) or regular (0).
+// Regular stores make the fused kernel alone faster, but leave h and y dirty
+// in the caches for the next kernel to write back.  Measured at configs[2]
+// with the four ops run in turn (interleaved on one box): non-temporal
+// stores took the fused Q4_K / Q6_K gathers + RMSNorm from 22.7-22.8 /
+// 24.9-25.0 to 21.2-21.4 / 24.2 us and the plain Q4_K / Q6_K gathers that
+// follow them from 15.2-15.4 / 16.5-16.8 to 11.1-11.3 / 14.8-15.0 us.
 #ifndef FELLM_EMB_NORM_NT
-#define FELLM_EMB_NORM_NT 0
+#define FELLM_EMB_NORM_NT 1
 #endif
 #ifndef FELLM_EMB_BLOCK
 #define FELLM_EMB_BLOCK 256
@@ -95,9 +101,18 @@
 // 64 threads 16.2-16.3 us, 128 17.6-17.7, 256 19.3-19.4 (the staged layout
 // 17.8-17.9); storing each part as soon as the next is decoded 16.6 (64) and
 // 17.6-17.8 (128); one wavefront per row walking rows with the next row's
-// chunks in flight 16.6-16.9 at 8 workgroups per CU, 17.2 at 4, 19.7 at 2.
+// chunks in flight 16.6-16.9 at 8 workgroups per CU, 17.2 at 4, 19.7 at 2;
+// 7, 4, 2 or 1 blocks per workgroup 19.7, 21.6-21.8, 23.3-23.4, 34.8-35.0.
+// In isolation (the same call repeated, table rows warm in the caches) the
+// staged layout is faster (14.8-15.0 against 17.0-17.3 us); with a 768 MB
+// fill between calls the LDS layout is (21.6 against 22.8 us).
 #ifndef FELLM_EMB_Q6K_LDS
 #define FELLM_EMB_Q6K_LDS 64
+#endif
+// Build knob: the fused Q6_K gather + RMSNorm takes the same LDS layout (1)
+// for rows of up to 4096 elements (configs[2] 29.5 -> 25.1 us).
+#ifndef FELLM_EMB_Q6K_LDS_NORM
+#define FELLM_EMB_Q6K_LDS_NORM 1
 #endif
 #ifndef FELLM_EMB_Q6K_BPW
 #define FELLM_EMB_Q6K_BPW 0
@@ -337,6 +352,12 @@ __device__ __forceinline__ void store_part(typename O::T *row, uint32_t p, const
     }
 }
 
+// Stores of the fused gather + RMSNorm (FELLM_EMB_NORM_NT policy).
+template <typename O, int N>
+__device__ __forceinline__ void norm_out_store(typename O::T *p, const float (&v)[N]) {
+    if constexpr (FELLM_EMB_NORM_NT) store_f32_nt<O, N>(p, v); else store_f32<O, N>(p, v);
+}
+
 constexpr int kEmbBlock = FELLM_EMB_BLOCK;
 
 // One workgroup per token row.  Each thread decodes its (up to MAXC) parts
@@ -559,12 +580,19 @@ __device__ __forceinline__ uint64_t lds_u64_at(const uint32_t *w, uint32_t off) 
            ((uint64_t)__builtin_amdgcn_alignbyte(w2, w1, sh) << 32);
 }
 
-template <typename O, int BLOCK, int NL, int NP>
+//
+// NORM (whole rows, bpw = dim / 256): the gather fused with RMSNorm.  The
+// decoded row stays in registers for the sum of squares; h (when non-null)
+// and y = (v * scale) * w are stored once each.
+template <typename O, int BLOCK, int NL, int NP, bool NORM>
 __global__ __launch_bounds__(BLOCK) void q6k_gather_lds_kernel(const uint8_t *__restrict__ table, uint64_t vocab,
                                                                uint32_t dim, const uint32_t *__restrict__ ids,
                                                                uint32_t bpw, typename O::T *__restrict__ h,
+                                                               typename O::T *__restrict__ y,
+                                                               const float *__restrict__ w_norm, float eps,
                                                                uint32_t *__restrict__ err) {
     extern __shared__ uint4 raw_lds[];
+    __shared__ float red[BLOCK / kWave];
     // Workgroup = (row, segment of bpw blocks).
     const uint32_t nb = dim / 256, nseg = (nb + bpw - 1) / bpw;
     const uint32_t row = blockIdx.x / nseg, b0 = (blockIdx.x % nseg) * bpw;
@@ -615,10 +643,37 @@ __global__ __launch_bounds__(BLOCK) void q6k_gather_lds_kernel(const uint8_t *__
             }
         }
     }
+    if constexpr (!NORM) {
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const uint32_t p = i * BLOCK + threadIdx.x;
-        if (p < parts) store_f32_nt<O, 8>(out + 8 * (size_t)p, v[i]);
+        for (int i = 0; i < NP; ++i) {
+            const uint32_t p = i * BLOCK + threadIdx.x;
+            if (p < parts) store_f32_nt<O, 8>(out + 8 * (size_t)p, v[i]);
+        }
+    } else {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const uint32_t p = i * BLOCK + threadIdx.x;
+            if (p < parts) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+            }
+        }
+        ss = block_sum<BLOCK>(ss, red);
+        const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
+        typename O::T *yrow = y + (size_t)row * dim;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const uint32_t p = i * BLOCK + threadIdx.x;
+            if (p < parts) {
+                if (h) norm_out_store<O, 8>(out + 8 * (size_t)p, v[i]);
+                float wv[8], o[8];
+                load_f32<F32, 8>(w_norm + 8 * p, wv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = (v[i][e] * scale) * wv[e];
+                norm_out_store<O, 8>(yrow + 8 * (size_t)p, o);
+            }
+        }
     }
 }
 
@@ -626,25 +681,33 @@ __global__ __launch_bounds__(BLOCK) void q6k_gather_lds_kernel(const uint8_t *__
 // counts (rows of up to 32768 elements at 128 threads); -1 otherwise.
 template <typename O>
 int launch_q6k_lds(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids, void *h,
-                   uint32_t *err, hipStream_t s) {
+                   void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
     constexpr int B = FELLM_EMB_Q6K_LDS;
     if constexpr (B == 0) {
         return -1;
     } else {
+        if (w && !aligned_to(w, 32)) return -1;  // 8-float weight vectors
         const uint32_t nb = dim / 256;
-        const uint32_t bpw = FELLM_EMB_Q6K_BPW && FELLM_EMB_Q6K_BPW < nb ? FELLM_EMB_Q6K_BPW : nb;
+        const uint32_t bpw = !w && FELLM_EMB_Q6K_BPW && FELLM_EMB_Q6K_BPW < nb ? FELLM_EMB_Q6K_BPW : nb;
         const uint64_t grid = (uint64_t)n_ids * ((nb + bpw - 1) / bpw);
         if (grid > 0x7fffffffull) return -1;
         const uint32_t n16 = (210 * bpw + 15 + 15) / 16;
         const uint32_t nl = (n16 + B - 1) / B, np = (32 * bpw + B - 1) / B;
+        // The fused norm keeps the row in registers: longer rows take the
+        // 256-thread staged layout instead.
+        if (w && np > 8) return -1;
         const uint8_t *tb = static_cast<const uint8_t *>(table);
         using TO = typename O::T;
         // Every thread writes its NL chunks; the segment's span (n16 chunks)
         // plus the dword lds_u64_at may read past it fit below NL * B chunks.
 #define FELLM_Q6L(NL, NP)                                                                                      \
     if (nl <= NL && np <= NP && (size_t)NL * B * 16 >= (size_t)n16 * 16 + 16) {                                \
-        FELLM_LAUNCH((q6k_gather_lds_kernel<O, B, NL, NP>), dim3((uint32_t)grid), dim3(B), (size_t)NL * B * 16, \
-                     s, tb, vocab, dim, ids, bpw, (TO *)h, err);                                               \
+        if (w)                                                                                                 \
+            FELLM_LAUNCH((q6k_gather_lds_kernel<O, B, NL, NP, true>), dim3((uint32_t)grid), dim3(B),             \
+                         (size_t)NL * B * 16, s, tb, vocab, dim, ids, bpw, (TO *)h, (TO *)y, w, eps, err);     \
+        else                                                                                                   \
+            FELLM_LAUNCH((q6k_gather_lds_kernel<O, B, NL, NP, false>), dim3((uint32_t)grid), dim3(B),            \
+                         (size_t)NL * B * 16, s, tb, vocab, dim, ids, bpw, (TO *)h, nullptr, nullptr, 0.0f, err); \
         return launch_status();                                                                                \
     }
         FELLM_Q6L(1, 1)
@@ -766,8 +829,8 @@ int dispatch_table(const void *table, uint32_t table_dtype, uint64_t vocab, uint
             return launch_emb<Q4KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
         case FELLM_DTYPE_Q6K:
             if (dim % 256 || !aligned_to(table, 2)) return FELLM_ERR_SHAPE;
-            if (!w && ids && dim * sizeof(typename O::T) % 16 == 0) {
-                const int st = launch_q6k_lds<O>(table, vocab, dim, ids, n_ids, h, err, s);
+            if (ids && dim * sizeof(typename O::T) % 16 == 0 && (!w || FELLM_EMB_Q6K_LDS_NORM)) {
+                const int st = launch_q6k_lds<O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
                 if (st >= 0) return st;
             }
             if (FELLM_EMB_STAGE) return launch_emb<Q6KStaged, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);

@@ -118,12 +118,13 @@ def test_c3_quantized_gathers_full_size(ops, dev):
         torch.cuda.synchronize()
         ref = oracle.narrow(oracle.embedding(tab, code, tab.shape[0], D, ids[idx]), "f16")
         assert_exact(_rows(s["out"], idx), ref, f"c3 {op.name}")
-    chain[2].fn(s)
-    torch.cuda.synchronize()
-    rows = oracle.embedding(q4, 12, q4.shape[0], D, ids[idx])
-    assert_exact(_rows(s["out"], idx), oracle.narrow(rows, "f16"), "c3 gather+norm h")
-    assert_close(_rows(s["y"], idx), oracle.narrow(oracle.rmsnorm(rows, w, 1e-6), "f16"), "f16",
-                 what="c3 gather+norm y")
+    for op, tab, code in ((chain[2], q4, 12), (chain[3], q6, 14)):
+        op.fn(s)
+        torch.cuda.synchronize()
+        rows = oracle.embedding(tab, code, tab.shape[0], D, ids[idx])
+        assert_exact(_rows(s["out"], idx), oracle.narrow(rows, "f16"), f"c3 {op.name} h")
+        assert_close(_rows(s["y"], idx), oracle.narrow(oracle.rmsnorm(rows, w, 1e-6), "f16"), "f16",
+                     what=f"c3 {op.name} y")
 
 
 def test_c4_decode_step_full_size(ops, dev):
