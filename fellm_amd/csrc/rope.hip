@@ -803,7 +803,7 @@ void decode_step_kernel(StepArgs<A> p) {
     } else if (role == 1) {
         add_rmsnorm_row<A, A, 256, 8, NCHUNK, true, true>(p.x, p.r, p.h, p.w, p.y, p.group, p.eps, b, red);
     } else {
-        silu_gate_blocks<A, typename HwStore<A>::type, 8, 2>(p.gate, p.up, p.act, p.n_silu, b, p.nb_silu, tab_lds);
+        silu_gate_blocks<A, typename HwStore<A>::type, 8, 2, false>(p.gate, p.up, p.act, p.n_silu, b, p.nb_silu, tab_lds);
     }
 }
 
