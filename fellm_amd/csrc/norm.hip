@@ -148,6 +148,20 @@ __global__ __launch_bounds__(256) void add_rmsnorm_wave_kernel(
     using P = Pack<T, VEC>;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t row = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+    const bool live = row < rows;
+    const size_t off = (size_t)row * group;
+    const uint32_t nvec = group / VEC;
+    // The row's x and r are requested first: their latency overlaps the
+    // weight staging and its barrier.
+    P xv[NCH], rv[ADD ? NCH : 1];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t i = c * kWave + lane;
+        if (live && i < nvec) {
+            xv[c] = load_pack_nt<T, VEC>(x + off + (size_t)i * VEC);
+            if constexpr (ADD) rv[c] = load_pack_nt<T, VEC>(r + off + (size_t)i * VEC);
+        }
+    }
     if constexpr (FELLM_NORM_WAVE_WLDS) {
         // The workgroup's four rows share one copy of the weights in LDS
         // (group floats, at most 8 KB), instead of each wavefront reading
@@ -157,18 +171,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_wave_kernel(
         __syncthreads();
         w = reinterpret_cast<const float *>(w_lds4);
     }
-    if (row >= rows) return;  // whole wavefronts only: no block-level barrier follows
-    const size_t off = (size_t)row * group;
-    const uint32_t nvec = group / VEC;
-    P xv[NCH], rv[ADD ? NCH : 1];
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const uint32_t i = c * kWave + lane;
-        if (i < nvec) {
-            xv[c] = load_pack_nt<T, VEC>(x + off + (size_t)i * VEC);
-            if constexpr (ADD) rv[c] = load_pack_nt<T, VEC>(r + off + (size_t)i * VEC);
-        }
-    }
+    if (!live) return;  // whole wavefronts only: no block-level barrier follows
     float ss = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
