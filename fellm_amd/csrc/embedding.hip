@@ -93,26 +93,39 @@
 #ifndef FELLM_EMB_DENSE_BLOCK
 #define FELLM_EMB_DENSE_BLOCK 0
 #endif
-// Build knob: workgroup size of the plain Q6_K gather that copies each raw
-// row segment into LDS with coalesced 16-byte loads and decodes it from there
-// (0: the part-by-part staged layout above), and the 256-element blocks a
+// Build knobs of the K-quant gathers that copy each raw row (segment) into
+// LDS with coalesced 16-byte loads and decode it from there
+// (kquant_gather_lds_kernel): its workgroup size, which gathers take it
+// (plain Q6_K, fused Q6_K + RMSNorm, plain Q4_K, fused Q4_K + RMSNorm; the
+// others keep the staged layouts above), and the 256-element blocks a
 // workgroup takes (FELLM_EMB_Q6K_BPW; 0: the whole row).  Measured at
-// configs[2] (8192 Zipf rows of 3584, interleaved on one box), whole rows:
-// 64 threads 16.2-16.3 us, 128 17.6-17.7, 256 19.3-19.4 (the staged layout
-// 17.8-17.9); storing each part as soon as the next is decoded 16.6 (64) and
-// 17.6-17.8 (128); one wavefront per row walking rows with the next row's
-// chunks in flight 16.6-16.9 at 8 workgroups per CU, 17.2 at 4, 19.7 at 2;
-// 7, 4, 2 or 1 blocks per workgroup 19.7, 21.6-21.8, 23.3-23.4, 34.8-35.0.
-// In isolation (the same call repeated, table rows warm in the caches) the
-// staged layout is faster (14.8-15.0 against 17.0-17.3 us); with a 768 MB
-// fill between calls the LDS layout is (21.6 against 22.8 us).
-#ifndef FELLM_EMB_Q6K_LDS
-#define FELLM_EMB_Q6K_LDS 64
+// configs[2] (8192 Zipf rows of 3584, interleaved on one box), plain Q6_K,
+// whole rows: 64 threads 16.2-16.3 us, 128 17.6-17.7, 256 19.3-19.4 (the
+// staged layout 17.8-17.9); storing each part as soon as the next is decoded
+// 16.6 (64) and 17.6-17.8 (128); one wavefront per row walking rows with the
+// next row's chunks in flight 16.6-16.9 at 8 workgroups per CU, 17.2 at 4,
+// 19.7 at 2; 7, 4, 2 or 1 blocks per workgroup 19.7, 21.6-21.8, 23.3-23.4,
+// 34.8-35.0.  In isolation (the same call repeated, table rows warm in the
+// caches) the staged layout is faster (14.8-15.0 against 17.0-17.3 us); with
+// a 768 MB fill between calls the LDS layout is (21.6 against 22.8 us).  The
+// fused Q6_K gather + RMSNorm, rows of up to 4096 elements: 29.5 -> 25.1 us.
+// Q4_K's 16-byte-aligned blocks gain nothing from the copy: the LDS layout
+// measured 13.1-13.2 against 11.4 us (plain) and 25.2-25.4 against
+// 21.2-21.4 us (fused), so Q4_K keeps its staged 8-output parts.
+#ifndef FELLM_EMB_KQ_LDS_BLOCK
+#define FELLM_EMB_KQ_LDS_BLOCK 64
 #endif
-// Build knob: the fused Q6_K gather + RMSNorm takes the same LDS layout (1)
-// for rows of up to 4096 elements (configs[2] 29.5 -> 25.1 us).
+#ifndef FELLM_EMB_Q6K_LDS
+#define FELLM_EMB_Q6K_LDS 1
+#endif
 #ifndef FELLM_EMB_Q6K_LDS_NORM
 #define FELLM_EMB_Q6K_LDS_NORM 1
+#endif
+#ifndef FELLM_EMB_Q4K_LDS
+#define FELLM_EMB_Q4K_LDS 0
+#endif
+#ifndef FELLM_EMB_Q4K_LDS_NORM
+#define FELLM_EMB_Q4K_LDS_NORM 0
 #endif
 #ifndef FELLM_EMB_Q6K_BPW
 #define FELLM_EMB_Q6K_BPW 0
@@ -559,15 +572,16 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_pipe_kernel(
     if (bad_rows && threadIdx.x == 0 && err) atomicOr(err, 1u);
 }
 
-// Plain Q6_K gather through LDS.  A Q6_K row is dim/256 blocks of 210 bytes,
+// K-quant gathers through LDS.  A Q6_K row is dim/256 blocks of 210 bytes,
 // so blocks are only 2-byte aligned and a per-part layout reads each block
-// with short unaligned loads at 210-byte strides.  Here the workgroup first
+// with short unaligned loads at 210-byte strides (Q4_K: 144-byte blocks, one
+// 8-byte qs load per part at 144-byte strides).  Here the workgroup first
 // copies the whole raw row into LDS with 16-byte loads of consecutive
 // addresses (the row's span rounded out to 16-byte boundaries, which never
 // leaves the pages the row lies on), then each thread decodes parts of 8
 // consecutive outputs from LDS and writes them with one 16-byte store of a
 // 16-bit output (a wavefront writes 1 KB of the row contiguously).
-// Output o = 8p' of block b, at n = o % 256 = 128 hh + 32 k + l:
+// Q6_K output o = 8p' of block b, at n = o % 256 = 128 hh + 32 k + l:
 //   q  = ((ql[64 hh + 32 (k & 1) + l] >> 4 (k >> 1)) & 15)
 //        | ((qh[32 hh + l] >> 2k) & 3) << 4,
 //   y  = (d * sc[8 hh + l / 16 + 2k]) * (q - 32)      (dequant.rs:315-370).
@@ -584,13 +598,63 @@ __device__ __forceinline__ uint64_t lds_u64_at(const uint32_t *w, uint32_t off) 
 // NORM (whole rows, bpw = dim / 256): the gather fused with RMSNorm.  The
 // decoded row stays in registers for the sum of squares; h (when non-null)
 // and y = (v * scale) * w are stored once each.
-template <typename O, int BLOCK, int NL, int NP, bool NORM>
-__global__ __launch_bounds__(BLOCK) void q6k_gather_lds_kernel(const uint8_t *__restrict__ table, uint64_t vocab,
-                                                               uint32_t dim, const uint32_t *__restrict__ ids,
-                                                               uint32_t bpw, typename O::T *__restrict__ h,
-                                                               typename O::T *__restrict__ y,
-                                                               const float *__restrict__ w_norm, float eps,
-                                                               uint32_t *__restrict__ err) {
+// Formats of the LDS gather: kBytes per 256-element block, and decode8,
+// the 8 consecutive outputs n .. n+7 (n a multiple of 8) of the block whose
+// bytes start at byte `blk` of the LDS row copy `w`.
+struct Q6KLds {
+    static constexpr uint32_t kBytes = 210;
+    __device__ static void decode8(const uint32_t *w, uint32_t blk, uint32_t n, float (&v)[8]) {
+        const uint32_t hh = n / 128, k = (n / 32) % 4, l = n % 32;
+        const uint64_t ql = lds_u64_at(w, blk + 64 * hh + 32 * (k & 1) + l);
+        const uint64_t qh = lds_u64_at(w, blk + 128 + 32 * hh + l);
+        const uint32_t so = blk + 192 + 8 * hh + l / 16 + 2 * k;
+        const int32_t sc = (int8_t)(w[so / 4] >> (8 * (so % 4)));
+        const uint32_t dof = blk + 208;  // even, so the f16 never straddles a dword
+        const float d = half_bits_to_f32(w[dof / 4] >> (8 * (dof % 4)));
+        const float ds = d * (float)sc;
+        const uint32_t qs = 4 * (k >> 1), hs = 2 * k;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int32_t q = (int32_t)((((uint32_t)(ql >> (8 * e)) >> qs) & 15u) |
+                                        ((((uint32_t)(qh >> (8 * e)) >> hs) & 3u) << 4)) -
+                              32;
+            v[e] = ds * (float)q;
+        }
+    }
+};
+
+// Q4_K (dequant.rs:251-305): output n of a block is chunk c = n / 64, offset
+// j = n % 64: the low nibbles of qs[32c + j] for j < 32, else the high
+// nibbles of qs[32c + j - 32], scaled by group 2c (+1 for the high nibbles):
+// y = (d * sc) * q - (dmin * m).  Blocks are 144 = 9 * 16 bytes and the table
+// is 16-byte aligned, so every word read here is aligned.
+struct Q4KLds {
+    static constexpr uint32_t kBytes = 144;
+    __device__ static void decode8(const uint32_t *w, uint32_t blk, uint32_t n, float (&v)[8]) {
+        const uint32_t c = n / 64, j = n % 64, hi = j >= 32;
+        const uint32_t *hw = w + blk / 4;
+        const uint32_t h0 = hw[0];
+        const float d = half_bits_to_f32(h0 & 0xffffu), dmin = half_bits_to_f32(h0 >> 16);
+        uint32_t sc, m;
+        k4_scale_min(2 * c + hi, hw[1], hw[2], hw[3], sc, m);
+        const float dq = d * (float)sc, mq = dmin * (float)m;
+        const uint32_t qo = (blk + 16 + 32 * c + j % 32) / 4;
+        const uint32_t q0 = w[qo], q1 = w[qo + 1], sh = 4 * hi;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t b = ((e < 4 ? q0 : q1) >> (8 * (e % 4) + sh)) & 15u;
+            v[e] = dq * (float)b - mq;
+        }
+    }
+};
+
+template <typename F, typename O, int BLOCK, int NL, int NP, bool NORM>
+__global__ __launch_bounds__(BLOCK) void kquant_gather_lds_kernel(const uint8_t *__restrict__ table, uint64_t vocab,
+                                                                  uint32_t dim, const uint32_t *__restrict__ ids,
+                                                                  uint32_t bpw, typename O::T *__restrict__ h,
+                                                                  typename O::T *__restrict__ y,
+                                                                  const float *__restrict__ w_norm, float eps,
+                                                                  uint32_t *__restrict__ err) {
     extern __shared__ uint4 raw_lds[];
     __shared__ float red[BLOCK / kWave];
     // Workgroup = (row, segment of bpw blocks).
@@ -600,10 +664,10 @@ __global__ __launch_bounds__(BLOCK) void q6k_gather_lds_kernel(const uint8_t *__
     const uint32_t id = ids[row];
     const bool bad = id >= vocab;
     if (bad && threadIdx.x == 0 && b0 == 0 && err) atomicOr(err, 1u);
-    const uint8_t *segp = table + (bad ? 0 : (uint64_t)id * nb * 210) + 210 * b0;
+    const uint8_t *segp = table + (bad ? 0 : (uint64_t)id * nb * F::kBytes) + F::kBytes * b0;
     const uint32_t lead = (uint32_t)(reinterpret_cast<uintptr_t>(segp) & 15);
     const uint4 *src = reinterpret_cast<const uint4 *>(segp - lead);
-    const uint32_t n16 = (lead + 210 * nblk + 15) / 16;
+    const uint32_t n16 = (lead + F::kBytes * nblk + 15) / 16;
     // Threads past the span re-read its last chunk (a cache hit), so every
     // load is unconditional and the chunks stay in registers.
     uint4 c[NL];
@@ -623,23 +687,10 @@ __global__ __launch_bounds__(BLOCK) void q6k_gather_lds_kernel(const uint8_t *__
     for (int i = 0; i < NP; ++i) {
         const uint32_t p = i * BLOCK + threadIdx.x;
         if (p < parts) {
-            const uint32_t b = p / 32, n = 8 * (p % 32);
-            const uint32_t hh = n / 128, k = (n / 32) % 4, l = n % 32;
-            const uint32_t blk = lead + 210 * b;
-            const uint64_t ql = lds_u64_at(w, blk + 64 * hh + 32 * (k & 1) + l);
-            const uint64_t qh = lds_u64_at(w, blk + 128 + 32 * hh + l);
-            const uint32_t so = blk + 192 + 8 * hh + l / 16 + 2 * k;
-            const int32_t sc = (int8_t)(w[so / 4] >> (8 * (so % 4)));
-            const uint32_t dof = blk + 208;  // even, so the f16 never straddles a dword
-            const float d = half_bits_to_f32(w[dof / 4] >> (8 * (dof % 4)));
-            const float ds = d * (float)sc;
-            const uint32_t qs = 4 * (k >> 1), hs = 2 * k;
+            F::decode8(w, lead + F::kBytes * (p / 32), 8 * (p % 32), v[i]);
+            if (bad) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int32_t q = (int32_t)((((uint32_t)(ql >> (8 * e)) >> qs) & 15u) |
-                                            ((((uint32_t)(qh >> (8 * e)) >> hs) & 3u) << 4)) -
-                                  32;
-                v[i][e] = bad ? 0.0f : ds * (float)q;
+                for (int e = 0; e < 8; ++e) v[i][e] = 0.0f;
             }
         }
     }
@@ -677,12 +728,12 @@ __global__ __launch_bounds__(BLOCK) void q6k_gather_lds_kernel(const uint8_t *__
     }
 }
 
-// Launches q6k_gather_lds_kernel when a thread's share fits the unrolled
+// Launches kquant_gather_lds_kernel when a thread's share fits the unrolled
 // counts (rows of up to 32768 elements at 128 threads); -1 otherwise.
-template <typename O>
-int launch_q6k_lds(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids, void *h,
-                   void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
-    constexpr int B = FELLM_EMB_Q6K_LDS;
+template <typename F, typename O>
+int launch_kquant_lds(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids, void *h,
+                      void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
+    constexpr int B = FELLM_EMB_KQ_LDS_BLOCK;
     if constexpr (B == 0) {
         return -1;
     } else {
@@ -691,7 +742,7 @@ int launch_q6k_lds(const void *table, uint64_t vocab, uint32_t dim, const uint32
         const uint32_t bpw = !w && FELLM_EMB_Q6K_BPW && FELLM_EMB_Q6K_BPW < nb ? FELLM_EMB_Q6K_BPW : nb;
         const uint64_t grid = (uint64_t)n_ids * ((nb + bpw - 1) / bpw);
         if (grid > 0x7fffffffull) return -1;
-        const uint32_t n16 = (210 * bpw + 15 + 15) / 16;
+        const uint32_t n16 = (F::kBytes * bpw + 15 + 15) / 16;
         const uint32_t nl = (n16 + B - 1) / B, np = (32 * bpw + B - 1) / B;
         // The fused norm keeps the row in registers: longer rows take the
         // 256-thread staged layout instead.
@@ -703,10 +754,10 @@ int launch_q6k_lds(const void *table, uint64_t vocab, uint32_t dim, const uint32
 #define FELLM_Q6L(NL, NP)                                                                                      \
     if (nl <= NL && np <= NP && (size_t)NL * B * 16 >= (size_t)n16 * 16 + 16) {                                \
         if (w)                                                                                                 \
-            FELLM_LAUNCH((q6k_gather_lds_kernel<O, B, NL, NP, true>), dim3((uint32_t)grid), dim3(B),             \
+            FELLM_LAUNCH((kquant_gather_lds_kernel<F, O, B, NL, NP, true>), dim3((uint32_t)grid), dim3(B),             \
                          (size_t)NL * B * 16, s, tb, vocab, dim, ids, bpw, (TO *)h, (TO *)y, w, eps, err);     \
         else                                                                                                   \
-            FELLM_LAUNCH((q6k_gather_lds_kernel<O, B, NL, NP, false>), dim3((uint32_t)grid), dim3(B),            \
+            FELLM_LAUNCH((kquant_gather_lds_kernel<F, O, B, NL, NP, false>), dim3((uint32_t)grid), dim3(B),            \
                          (size_t)NL * B * 16, s, tb, vocab, dim, ids, bpw, (TO *)h, nullptr, nullptr, 0.0f, err); \
         return launch_status();                                                                                \
     }
@@ -824,13 +875,17 @@ int dispatch_table(const void *table, uint32_t table_dtype, uint64_t vocab, uint
     switch (table_dtype) {
         case FELLM_DTYPE_Q4K:
             if (dim % 256 || !aligned_to(table, 16)) return FELLM_ERR_SHAPE;
+            if (ids && dim * sizeof(typename O::T) % 16 == 0 && (w ? FELLM_EMB_Q4K_LDS_NORM : FELLM_EMB_Q4K_LDS)) {
+                const int st = launch_kquant_lds<Q4KLds, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
+                if (st >= 0) return st;
+            }
             if (FELLM_EMB_STAGE == 2) return launch_emb<Q4KStaged8, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
             if (FELLM_EMB_STAGE) return launch_emb<Q4KStaged, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
             return launch_emb<Q4KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
         case FELLM_DTYPE_Q6K:
             if (dim % 256 || !aligned_to(table, 2)) return FELLM_ERR_SHAPE;
-            if (ids && dim * sizeof(typename O::T) % 16 == 0 && (!w || FELLM_EMB_Q6K_LDS_NORM)) {
-                const int st = launch_q6k_lds<O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
+            if (ids && dim * sizeof(typename O::T) % 16 == 0 && (w ? FELLM_EMB_Q6K_LDS_NORM : FELLM_EMB_Q6K_LDS)) {
+                const int st = launch_kquant_lds<Q6KLds, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
                 if (st >= 0) return st;
             }
             if (FELLM_EMB_STAGE) return launch_emb<Q6KStaged, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);

@@ -692,29 +692,32 @@ def test_embedding_q6k_unaligned_table(ops, dev, offset, dim):
     assert_exact(from_dev(got), ref, f"embedding q6k table offset {offset} dim={dim}")
 
 
+@pytest.mark.parametrize("qtype", ["q4k", "q6k"])
 @pytest.mark.parametrize("dim,store_h", [(256, True), (2048, False), (3584, True), (4096, True), (6144, False)])
-def test_embedding_q6k_rmsnorm_rows(ops, dev, dim, store_h):
-    """Fused Q6_K gather + RMSNorm over thousands of Zipf rows with
+def test_embedding_kquant_rmsnorm_rows(ops, dev, qtype, dim, store_h):
+    """Fused Q4_K / Q6_K gather + RMSNorm over thousands of Zipf rows with
     out-of-range ids (zero rows, flag set), with and without the h output;
     rows of up to 4096 elements take the one-wavefront LDS layout, longer
     ones the staged layout.  h bit-exact, y within the RMSNorm tolerance."""
     from fellm_amd import synth
 
-    rng = np.random.default_rng(dim + store_h)
+    rng = np.random.default_rng(dim + store_h + len(qtype))
     vocab, n_rows = 400, 2051
-    table = synth.q6k_table(rng, vocab, dim)
+    code = 12 if qtype == "q4k" else 14
+    table = synth.q4k_table(rng, vocab, dim) if qtype == "q4k" else synth.q6k_table(rng, vocab, dim)
     ids = synth.zipf_ids(rng, n_rows, vocab)
     bad = rng.choice(n_rows, size=3, replace=False)
     ids[bad] = vocab + np.arange(3, dtype=np.uint32)
     ok = ids < vocab
     e = np.zeros((n_rows, dim), np.float32)
-    e[ok] = oracle.embedding(table, 14, vocab, dim, ids[ok])
+    e[ok] = oracle.embedding(table, code, vocab, dim, ids[ok])
     w = rng.normal(1.0, 0.1, size=dim).astype(np.float32)
     flag = torch.zeros(1, dtype=torch.int32, device=dev)
     h, y = ops.embedding_rmsnorm(torch.from_numpy(table).to(dev), torch.from_numpy(ids.view(np.int32)).to(dev),
-                                 torch.from_numpy(w).to(dev), 1e-6, dim=dim, qtype="q6k",
+                                 torch.from_numpy(w).to(dev), 1e-6, dim=dim, qtype=qtype,
                                  out_dtype=KINDS["bf16"], store_h=store_h, err_flag=flag)
     assert int(flag.item()) == 1
     if store_h:
-        assert_exact(from_dev(h), oracle.narrow(e, "bf16"), f"q6k fused h dim {dim}")
-    assert_close(from_dev(y), oracle.narrow(oracle.rmsnorm(e, w, 1e-6), "bf16"), "bf16", what=f"q6k fused y dim {dim}")
+        assert_exact(from_dev(h), oracle.narrow(e, "bf16"), f"{qtype} fused h dim {dim}")
+    assert_close(from_dev(y), oracle.narrow(oracle.rmsnorm(e, w, 1e-6), "bf16"), "bf16",
+                 what=f"{qtype} fused y dim {dim}")
