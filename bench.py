@@ -879,6 +879,123 @@ def cpu_baseline(budget_s: float, threads: int = 1, _native=None):
     return out
 
 
+def cpu_suite_ops(cfg: str):
+    """Per-op CPU samples of a config: (op name as the GPU suite names it,
+    rows of that op in the config, rows in the sample, callable).  The
+    oracle computes every op as backend-cpu does, in f32 at the op boundary
+    (gathers widen or dequantize to f32 rows); tables are 4096-row slices of
+    the config's table shape (a gather's cost per row does not depend on the
+    vocabulary), the paged arena 512 blocks."""
+    import numpy as np
+
+    import oracle
+    from fellm_amd import synth
+
+    rng = np.random.default_rng(11)
+    f32 = np.float32
+
+    def randn(*shape, std=1.0):
+        return (std * rng.normal(size=shape)).astype(f32)
+
+    ops = []
+
+    def chain(T_cfg, T, H, nq, nkv, hd, theta, I, eps, table_kind, with_add=True):
+        V = 4096
+        if table_kind == "f16":
+            table = rng.normal(0, 0.02, size=(V, H)).astype(np.float16).view(np.uint8)
+            code = 1
+        else:
+            table = rng.normal(0, 0.02, size=(V, H)).astype(f32).view(np.uint8)
+            code = 0
+        ids = rng.integers(0, V, size=T, dtype=np.uint32)
+        x, r, w = randn(T, H), randn(T, H, std=2.0), (1.0 + 0.1 * rng.normal(size=H)).astype(f32)
+        q, k = randn(T, nq * hd), randn(T, nkv * hd)
+        inv = oracle.rope_inv_freqs(theta, hd)
+        pos = np.arange(T, dtype=np.uint32)
+        g, u = randn(T, I), randn(T, I)
+        emb = "embedding_f16" if table_kind == "f16" else "embedding_f32"
+        ops.append((emb, T_cfg, T, lambda: oracle.embedding(table, code, V, H, ids)))
+        if with_add:
+            ops.append(("add_rmsnorm", T_cfg, T, lambda: oracle.rmsnorm(oracle.add(x, r), w, eps)))
+        else:
+            ops.append(("rmsnorm", T_cfg, T, lambda: oracle.rmsnorm(x, w, eps)))
+        ops.append(("rope_qk", T_cfg, T, lambda: (oracle.rope(q, nq, hd, hd, 0, inv, pos),
+                                                  oracle.rope(k, nkv, hd, hd, 0, inv, pos))))
+        ops.append(("swiglu", T_cfg, T, lambda: oracle.silu_gate(g, u)))
+
+    if cfg == "c1":
+        chain(64, 64, 2048, 32, 8, 64, 500000.0, 8192, 1e-5, "f32")
+    elif cfg == "c2":
+        chain(4096, 64, 4096, 32, 8, 128, 500000.0, 14336, 1e-5, "f16")
+    elif cfg == "c3":
+        V, D, T = 4096, 3584, 256
+        q4, q6 = synth.q4k_table(rng, V, D), synth.q6k_table(rng, V, D)
+        ids = synth.zipf_ids(rng, T, V)
+        w = (1.0 + 0.1 * rng.normal(size=D)).astype(f32)
+        ops.append(("q4k_gather", 8192, T, lambda: oracle.embedding(q4, 12, V, D, ids)))
+        ops.append(("q6k_gather", 8192, T, lambda: oracle.embedding(q6, 14, V, D, ids)))
+        ops.append(("q4k_gather_rmsnorm", 8192, T, lambda: oracle.rmsnorm(oracle.embedding(q4, 12, V, D, ids), w, 1e-6)))
+        ops.append(("q6k_gather_rmsnorm", 8192, T, lambda: oracle.rmsnorm(oracle.embedding(q6, 14, V, D, ids), w, 1e-6)))
+    elif cfg == "c4":
+        B, nq, nkv, hd, bs, nblk, H, I = 256, 64, 8, 128, 16, 512, 8192, 28672
+        stride = nkv * hd
+        bb = 2 * bs * stride * 2
+        pos, table, n_logical = synth.paged_layout(rng, B, nblk, bs, 32768)
+        arena = np.zeros(nblk * bb, np.uint8)
+        inv = oracle.rope_inv_freqs(500000.0, hd)
+        q, k, v = randn(B, nq * hd), randn(B, stride), randn(B, stride)
+        x, r, w = randn(B, H), randn(B, H, std=2.0), (1.0 + 0.1 * rng.normal(size=H)).astype(f32)
+        g, u = randn(B, I), randn(B, I)
+
+        def rope_kv():
+            oracle.rope(q, nq, hd, hd, 0, inv, pos)
+            kr = oracle.rope(k, nkv, hd, hd, 0, inv, pos)
+            oracle.kv_write_paged(kr, stride, pos, table, n_logical, 1, 0, bs, bb, arena, False, "bf16")
+            oracle.kv_write_paged(v, stride, pos, table, n_logical, 1, 0, bs, bb, arena, True, "bf16")
+
+        ops.append(("rope_kv_write", B, B, rope_kv))
+        ops.append(("add_rmsnorm", B, B, lambda: oracle.rmsnorm(oracle.add(x, r), w, 1e-5)))
+        ops.append(("swiglu", B, 32, lambda: oracle.silu_gate(g[:32], u[:32])))
+    elif cfg == "c5":
+        T, E, H, I, hd = 16384, 128, 2048, 768, 128
+        logits = randn(T, E)
+        ops.append(("router_topk", T, T, lambda: oracle.router(logits, 8)))
+        g, u = randn(1024, I), randn(1024, I)
+        ops.append(("swiglu_routed", T * 8, 1024, lambda: oracle.silu_gate(g, u)))
+        x, w = randn(512, H), (1.0 + 0.1 * rng.normal(size=H)).astype(f32)
+        ops.append(("rmsnorm", T, 512, lambda: oracle.rmsnorm(x, w, 1e-6)))
+        q, k = randn(256, 32 * hd), randn(256, 4 * hd)
+        inv = oracle.rope_inv_freqs(1e6, hd)
+        pos = np.arange(8000, 8256, dtype=np.uint32)
+        ops.append(("rope_qk", T, 256, lambda: (oracle.rope(q, 32, hd, hd, 0, inv, pos),
+                                                oracle.rope(k, 4, hd, hd, 0, inv, pos))))
+    return ops
+
+
+def cpu_suite(cfg: str, gpu_ops: dict | None, budget_s: float = 0.5) -> dict:
+    """Times each of the config's ops on the CPU (1 thread, the native oracle
+    build) for about budget_s each; reports rows/s, the full-config time
+    extrapolated per row, and the GPU's speedup over it where the GPU suite
+    timed the same op."""
+    out = {}
+    for name, rows_cfg, rows, fn in cpu_suite_ops(cfg):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s and n >= 3:
+                break
+        per_row_us = el / n / rows * 1e6
+        rec = {"sample_rows": rows, "config_rows": rows_cfg, "us_per_sample": round(el / n * 1e6, 1),
+               "rows_per_s": round(rows / (el / n), 1), "us_full_config_est": round(per_row_us * rows_cfg, 1)}
+        if gpu_ops and name in gpu_ops and "us_median" in gpu_ops[name]:
+            rec["gpu_speedup"] = round(per_row_us * rows_cfg / gpu_ops[name]["us_median"], 1)
+        out[name] = rec
+    return out
+
+
 # --------------------------------------------------------------------------- #
 def read_traffic():
     """HBM bytes per SwiGLU launch from the committed rocprofv3 PMC summary, if present."""
@@ -932,6 +1049,30 @@ def main():
             torch.cuda.empty_cache()
         if not args.only or "next_graph" in args.only.split(","):
             result["next_graph"] = decode_graph_report(torch, ops, dev, max(args.steps, 50), args.warmup)
+        if not args.no_cpu_baseline:
+            # The same ops on the host (1 thread, the oracle built -march=native
+            # as the reference is built), per op, after the GPU work.
+            import tempfile
+
+            import oracle
+
+            path, flags = oracle.build_native(Path(tempfile.mkdtemp(prefix="oracle_native_")))
+            oracle.use_library(path)
+            cpu = {"info": host_cpu_info(flags), "threads": 1,
+                   "method": "oracle/fellm_oracle.c (backend-cpu's operation order, f32 at the op boundary) on a "
+                             "sample of each op's rows for ~0.5 s; us_full_config_est = per-row time x the "
+                             "config's rows; gpu_speedup = that / the GPU median above"}
+            for cfg in ("c1", "c2", "c3", "c4", "c5"):
+                if args.only and cfg not in args.only.split(",") and "cpu" not in args.only.split(","):
+                    continue
+                cpu[cfg] = cpu_suite(cfg, result.get(cfg))
+                if cfg == "c4" and all(k in cpu[cfg] for k in ("rope_kv_write", "add_rmsnorm", "swiglu")):
+                    est = sum(cpu[cfg][k]["us_full_config_est"] for k in ("rope_kv_write", "add_rmsnorm", "swiglu"))
+                    rec = {"us_full_config_est": round(est, 1), "of": "the three ops above"}
+                    if result.get("c4", {}).get("decode_step_fused"):
+                        rec["gpu_speedup"] = round(est / result["c4"]["decode_step_fused"]["us_median"], 1)
+                    cpu[cfg]["decode_step_fused"] = rec
+            result["cpu"] = cpu
         print(json.dumps({"suite": result}, indent=1))
         return
 

@@ -70,3 +70,16 @@ def test_bench_traffic_summary_parses():
 
     t = bench.read_traffic()
     assert t is None or 300e6 < t < 400e6
+
+
+def test_bench_cpu_suite_reports_every_op():
+    """bench.py --suite's CPU leg: every op of a config is timed through the
+    oracle and reported with rows/s and the full-config extrapolation; the
+    GPU speedup appears only where a GPU time for the op is given."""
+    import bench
+
+    out = bench.cpu_suite("c1", {"swiglu": {"us_median": 10.0}}, budget_s=0.01)
+    assert set(out) == {"embedding_f32", "add_rmsnorm", "rope_qk", "swiglu"}
+    for name, rec in out.items():
+        assert rec["rows_per_s"] > 0 and rec["us_full_config_est"] > 0
+        assert ("gpu_speedup" in rec) == (name == "swiglu")
