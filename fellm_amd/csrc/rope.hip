@@ -737,13 +737,6 @@ extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q
 #ifndef FELLM_STEP_WAVES
 #define FELLM_STEP_WAVES 6
 #endif
-// Build knob: the SwiGLU role requests its loads before staging the exp
-// table (1) or after (0).  Measured at configs[3] (interleaved on one box):
-// 0 18.2-18.3 us; 1 19.1-19.2 us (it spills at 6 waves), 19.8-19.9 us with
-// the compiler's occupancy.
-#ifndef FELLM_STEP_SILU_LOAD_FIRST
-#define FELLM_STEP_SILU_LOAD_FIRST 0
-#endif
 #ifndef FELLM_STEP_ORDER
 #define FELLM_STEP_ORDER 0
 #endif
@@ -810,7 +803,7 @@ void decode_step_kernel(StepArgs<A> p) {
     } else if (role == 1) {
         add_rmsnorm_row<A, A, 256, 8, NCHUNK, true, true>(p.x, p.r, p.h, p.w, p.y, p.group, p.eps, b, red);
     } else {
-        silu_gate_blocks<A, typename HwStore<A>::type, 8, 2, FELLM_STEP_SILU_LOAD_FIRST>(p.gate, p.up, p.act, p.n_silu, b, p.nb_silu, tab_lds);
+        silu_gate_blocks<A, typename HwStore<A>::type, 8, 2>(p.gate, p.up, p.act, p.n_silu, b, p.nb_silu, tab_lds);
     }
 }
 

@@ -12,12 +12,6 @@ namespace {
 
 constexpr int kEwBlock = 256;
 
-// Build knob: each thread's first loads are issued before the exp table is
-// staged in LDS (1) or after (0).  The fused decode step keeps 0: with its
-// occupancy request the early loads would spill.
-#ifndef FELLM_SWIGLU_LOAD_FIRST
-#define FELLM_SWIGLU_LOAD_FIRST 1
-#endif
 // Build knob: 16-bit outputs take the interval fast path of silu_mul_fast (1).
 #ifndef FELLM_SWIGLU_FAST
 #define FELLM_SWIGLU_FAST 1
@@ -41,14 +35,15 @@ __device__ __forceinline__ void store_raw_nt(typename O::T *p, const typename O:
 // SwiGLU over n elements by a grid of nblk kEwBlock-thread workgroups, this
 // workgroup being number bid (every thread calls it; contains a barrier).
 // tab_lds: 32 u64 of LDS for the expf table.
-template <typename I, typename O, int VEC, int UNROLL, bool LOAD_FIRST = FELLM_SWIGLU_LOAD_FIRST>
+template <typename I, typename O, int VEC, int UNROLL>
 __device__ __forceinline__ void silu_gate_blocks(const typename I::T *__restrict__ g,
                                                  const typename I::T *__restrict__ u, typename O::T *__restrict__ out,
                                                  uint64_t n, uint32_t bid, uint32_t nblk, uint64_t *tab_lds) {
+    const uint64_t *tab = stage_expf_table(tab_lds);
     const uint64_t nvec = n / VEC;
     const uint64_t stride = (uint64_t)nblk * kEwBlock * UNROLL;
-    uint64_t base = (uint64_t)bid * kEwBlock * UNROLL + threadIdx.x;
-    auto load = [&](float (&gv)[UNROLL][VEC], float (&uv)[UNROLL][VEC]) {
+    for (uint64_t base = (uint64_t)bid * kEwBlock * UNROLL + threadIdx.x; base < nvec; base += stride) {
+        float gv[UNROLL][VEC], uv[UNROLL][VEC];
 #pragma unroll
         for (int j = 0; j < UNROLL; ++j) {
             const uint64_t i = base + (uint64_t)j * kEwBlock;
@@ -57,8 +52,6 @@ __device__ __forceinline__ void silu_gate_blocks(const typename I::T *__restrict
                 load_f32_nt<I, VEC>(u + i * VEC, uv[j]);
             }
         }
-    };
-    auto finish = [&](const uint64_t *tab, const float (&gv)[UNROLL][VEC], const float (&uv)[UNROLL][VEC]) {
 #pragma unroll
         for (int j = 0; j < UNROLL; ++j) {
             const uint64_t i = base + (uint64_t)j * kEwBlock;
@@ -79,26 +72,6 @@ __device__ __forceinline__ void silu_gate_blocks(const typename I::T *__restrict
                     store_f32_nt<O, VEC>(out + i * VEC, o);
                 }
             }
-        }
-    };
-    const uint64_t *tab;
-    if constexpr (LOAD_FIRST) {
-        // The first batch is requested before the exp table is staged (a
-        // barrier), so its latency overlaps the staging.
-        float gv[UNROLL][VEC], uv[UNROLL][VEC];
-        if (base < nvec) load(gv, uv);
-        tab = stage_expf_table(tab_lds);
-        while (base < nvec) {
-            finish(tab, gv, uv);
-            base += stride;
-            if (base < nvec) load(gv, uv);
-        }
-    } else {
-        tab = stage_expf_table(tab_lds);
-        for (; base < nvec; base += stride) {
-            float gv[UNROLL][VEC], uv[UNROLL][VEC];
-            load(gv, uv);
-            finish(tab, gv, uv);
         }
     }
     // Tail (n % VEC elements), handled by the first threads of block 0.
