@@ -60,7 +60,8 @@ def _stale(src: str, build_dir: Path) -> bool:
     obj = build_dir / (Path(src).stem + ".o")
     if not obj.exists():
         return True
-    deps = [CSRC / src, CSRC / "common.hpp", ROOT / "include" / "fellm_abi.h", ROOT / "include" / "fellm_rocm.h"]
+    # Every header the sources may include: csrc/*.hpp and include/*.h.
+    deps = [CSRC / src, *CSRC.glob("*.hpp"), *(ROOT / "include").glob("*.h")]
     return any(d.stat().st_mtime > obj.stat().st_mtime for d in deps if d.exists())
 
 
