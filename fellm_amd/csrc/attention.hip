@@ -472,7 +472,14 @@ __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine(const fl
 // 128 splits (1024 wavefronts) rather than 256.
 constexpr uint32_t kMinSplitBlocks = 2;
 constexpr uint32_t kTargetWaves = 1024;
-constexpr uint32_t kDeepWalk = 64;  // blocks per wavefront from which DEPTH 2 is used
+// Build knob: blocks per wavefront from which DEPTH 2 is used.  Measured
+// (interleaved on one box): one Llama-3-8B sequence of 32768 keys (splits of
+// 16 blocks) 37.8-37.9 us from 64, 33.9 us from 4, 8 or 16; 2048 keys (splits
+// of 2 blocks) and 256 sequences x 4096 keys level.
+#ifndef FELLM_ATT_DEEP_WALK
+#define FELLM_ATT_DEEP_WALK 8
+#endif
+constexpr uint32_t kDeepWalk = FELLM_ATT_DEEP_WALK;
 uint32_t choose_splits(uint32_t batch, uint32_t n_kv, uint32_t max_seq) {
     const uint32_t pairs = batch * n_kv;
     const uint32_t blocks = (max_seq + kBlockTokens - 1) / kBlockTokens;
@@ -492,8 +499,9 @@ int launch_decode(const void *q, void *out, uint32_t batch, uint32_t n_heads, ui
     if (splits > 1 && (!ws || ws_bytes < need)) splits = 1;
     const uint32_t blocks = (max_seq + kBlockTokens - 1) / kBlockTokens;
     const uint32_t bps = (blocks + splits - 1) / splits;
-    // Two blocks in flight pay off on long walks (256 sequences x 4096 keys:
-    // 754 -> 720 us); splits of a few blocks do better with one.
+    // Two blocks in flight pay off on walks of 8 blocks and more (256
+    // sequences x 4096 keys: 754 -> 720 us); splits of a few blocks do better
+    // with one.
     if (bps >= kDeepWalk)
         FELLM_LAUNCH((paged_decode_kernel<Q, O, C, HD, GM, 2>), dim3(batch * n_kv * splits), dim3(kWave), 0,
                            st, static_cast<const typename Q::T *>(q), static_cast<typename O::T *>(out), ws, lens,
