@@ -471,7 +471,13 @@ __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine(const fl
 // 16-block splits and 17.5 us with 2-block ones; 32768 keys did best at
 // 128 splits (1024 wavefronts) rather than 256.
 constexpr uint32_t kMinSplitBlocks = 2;
-constexpr uint32_t kTargetWaves = 1024;
+// Build knob: wavefronts the split policy aims for.  With two blocks in
+// flight from 8-block walks, one 32768-key sequence measured 34.0-34.2 us at
+// 1024, 41.3-41.4 at 2048 and 52.3 at 512 (interleaved on one box).
+#ifndef FELLM_ATT_TARGET_WAVES
+#define FELLM_ATT_TARGET_WAVES 1024
+#endif
+constexpr uint32_t kTargetWaves = FELLM_ATT_TARGET_WAVES;
 // Build knob: blocks per wavefront from which DEPTH 2 is used.  Measured
 // (interleaved on one box): one Llama-3-8B sequence of 32768 keys (splits of
 // 16 blocks) 37.8-37.9 us from 64, 33.9 us from 4, 8 or 16; 2048 keys (splits
