@@ -83,7 +83,11 @@
 // gather (0: one workgroup per row).  Measured at configs[1] (4096 f16 rows of
 // 4096, interleaved on one box): one workgroup per row 13.2-13.4 us; 2 per CU
 // 16.6-16.7 us; 4 per CU 13.4-13.5 us; 8 per CU (the occupancy limit of
-// 256-thread workgroups) 12.3-12.4 us.
+// 256-thread workgroups) 12.3-12.4 us.  With other workgroup sizes
+// (FELLM_EMB_BLOCK): 512 threads at 4 or 2 per CU 13.0-13.2 us, 128 threads
+// at 16 per CU 13.0-13.2 us, against 12.4 us.  A one-shot grid with every
+// part of a row loaded before its stores: 64 threads per row 13.1, 128 12.7,
+// 256 13.8, 512 13.1 us.
 #ifndef FELLM_EMB_PIPE
 #define FELLM_EMB_PIPE 8
 #endif
