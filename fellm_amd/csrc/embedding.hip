@@ -15,7 +15,9 @@
 //           straight from global memory and shared via L1 by the 16 parts of
 //           the block;
 //   Q6_K  : 16 elements = 4 runs of 4, read with unaligned dword loads
-//           (210-byte blocks are only 2-byte aligned).
+//           (210-byte blocks are only 2-byte aligned).  Gathers by id take
+//           kquant_gather_lds_kernel instead: the raw row is copied into LDS
+//           with coalesced 16-byte loads and decoded there in 8-output parts.
 // The arithmetic order is the reference's, with FMA contraction disabled at
 // compile time:  Q4_K  y = (d*sc)*q - (dmin*m);   Q6_K  y = (d*sc)*(q-32).
 // With NORM the decoded row stays in registers for the sum of squares and
