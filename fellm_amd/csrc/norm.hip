@@ -38,6 +38,13 @@
 #ifndef FELLM_NORM_PIPE
 #define FELLM_NORM_PIPE 3
 #endif
+// Build knob: threads per workgroup of the wavefront-per-row kernel (one row
+// per wavefront; the workgroup's rows share one LDS copy of the weights).
+// Measured at configs[4] (16384 x 2048 bf16, interleaved on one box): 256
+// 25.1-25.2 us, 512 25.1-25.2, 1024 26.8-27.0, 128 27.2-27.6.
+#ifndef FELLM_NORM_WAVE_BLOCK
+#define FELLM_NORM_WAVE_BLOCK 256
+#endif
 #ifndef FELLM_NORM_WAVE_BYTES
 #define FELLM_NORM_WAVE_BYTES 4096
 #endif
@@ -140,14 +147,14 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_pipe_kernel(const typename 
 // stay in registers in storage form, h is rounded in place, and y is formed
 // from it with the weights read per chunk.
 template <typename A, typename O, int NCH, bool ADD, bool STORE_H>
-__global__ __launch_bounds__(256) void add_rmsnorm_wave_kernel(
+__global__ __launch_bounds__(FELLM_NORM_WAVE_BLOCK) void add_rmsnorm_wave_kernel(
     const typename A::T *x, const typename A::T *r, typename A::T *h, const float *__restrict__ w,
     typename O::T *y, uint32_t group, uint32_t rows, float eps) {
     using T = typename A::T;
     constexpr int VEC = 16 / sizeof(T);
     using P = Pack<T, VEC>;
     const uint32_t lane = threadIdx.x % kWave;
-    const uint32_t row = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+    const uint32_t row = blockIdx.x * (FELLM_NORM_WAVE_BLOCK / kWave) + threadIdx.x / kWave;
     const bool live = row < rows;
     const size_t off = (size_t)row * group;
     const uint32_t nvec = group / VEC;
@@ -167,7 +174,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_wave_kernel(
         // (group floats, at most 8 KB), instead of each wavefront reading
         // them from the caches.
         extern __shared__ float4 w_lds4[];
-        for (uint32_t i = threadIdx.x; i < group / 4; i += 256) w_lds4[i] = reinterpret_cast<const float4 *>(w)[i];
+        for (uint32_t i = threadIdx.x; i < group / 4; i += FELLM_NORM_WAVE_BLOCK)
+            w_lds4[i] = reinterpret_cast<const float4 *>(w)[i];
         __syncthreads();
         w = reinterpret_cast<const float *>(w_lds4);
     }
@@ -210,7 +218,8 @@ int launch_wave(const void *x, const void *r, void *h, const float *w, void *y, 
                 float eps, hipStream_t s) {
     using TA = typename A::T;
     using TO = typename O::T;
-    const dim3 grid((uint32_t)((rows + 3) / 4)), block(256);
+    constexpr uint32_t RPB = FELLM_NORM_WAVE_BLOCK / kWave;  // rows per workgroup
+    const dim3 grid((uint32_t)((rows + RPB - 1) / RPB)), block(FELLM_NORM_WAVE_BLOCK);
     const size_t wl = FELLM_NORM_WAVE_WLDS ? (size_t)group * sizeof(float) : 0;
     if (r == nullptr) {
         FELLM_LAUNCH((add_rmsnorm_wave_kernel<A, O, NCH, false, false>), grid, block, wl, s, (const TA *)x, nullptr,
