@@ -150,6 +150,16 @@ def c3_ops(torch, ops, dev, n_sets, seed=3):
            lambda s: ops.embedding_rmsnorm(q6, s["ids"], w, 1e-6, dim=D, qtype="q6k", h_out=s["out"],
                                            y_out=s["y"]), (1, T * 2940, 2 * out_b)),
     ]
+    # The CUDA plugin's other quantized embedding keys (Q5_K, Q8_0) at the same
+    # shape; drawn after the ids so the four ops above see the same inputs.
+    q5 = torch.from_numpy(synth.q5k_table(rng, V, D)).to(dev)
+    q8 = torch.from_numpy(synth.q8_0_table(rng, V, D)).to(dev)
+    chain += [
+        Op("q5k_gather", T * 2464 + out_b + T * 4, lambda s: ops.embedding(q5, s["ids"], dim=D, qtype="q5k",
+                                                                           out=s["out"]), (1, T * 2464, out_b)),
+        Op("q8_0_gather", T * 3808 + out_b + T * 4, lambda s: ops.embedding(q8, s["ids"], dim=D, qtype="q8_0",
+                                                                            out=s["out"]), (1, T * 3808, out_b)),
+    ]
     return chain, sets, T
 
 
@@ -936,6 +946,9 @@ def cpu_suite_ops(cfg: str):
         ops.append(("q6k_gather", 8192, T, lambda: oracle.embedding(q6, 14, V, D, ids)))
         ops.append(("q4k_gather_rmsnorm", 8192, T, lambda: oracle.rmsnorm(oracle.embedding(q4, 12, V, D, ids), w, 1e-6)))
         ops.append(("q6k_gather_rmsnorm", 8192, T, lambda: oracle.rmsnorm(oracle.embedding(q6, 14, V, D, ids), w, 1e-6)))
+        q5, q8 = synth.q5k_table(rng, V, D), synth.q8_0_table(rng, V, D)
+        ops.append(("q5k_gather", 8192, T, lambda: oracle.embedding(q5, 13, V, D, ids)))
+        ops.append(("q8_0_gather", 8192, T, lambda: oracle.embedding(q8, 8, V, D, ids)))
     elif cfg == "c4":
         B, nq, nkv, hd, bs, nblk, H, I = 256, 64, 8, 128, 16, 512, 8192, 28672
         stride = nkv * hd

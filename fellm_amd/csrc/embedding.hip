@@ -3,7 +3,8 @@
 // Reference: crates/backend-cpu/src/backend.rs:1026-1046 (launch_embedding)
 //   -> kernels/embedding.rs:10-23 (embedding_row) -> dequant.rs:19-55
 //   F32 copy, F16 widen (half::f16::to_f32), BF16 bits << 16,
-//   Q4_K dequant.rs:251-305, Q6_K dequant.rs:315-370.
+//   Q4_K dequant.rs:251-305, Q6_K dequant.rs:315-370, Q5_K dequant.rs:59-107,
+//   Q8_0 dequant.rs:172-192 (the last two only through the LDS gather).
 //
 // One workgroup gathers one token row.  A row is cut into "parts", each a
 // fixed set of output elements one thread produces:
@@ -608,7 +609,7 @@ __device__ __forceinline__ uint64_t lds_u64_at(const uint32_t *w, uint32_t off) 
 // the 8 consecutive outputs n .. n+7 (n a multiple of 8) of the block whose
 // bytes start at byte `blk` of the LDS row copy `w`.
 struct Q6KLds {
-    static constexpr uint32_t kBytes = 210;
+    static constexpr uint32_t kBytes = 210, kElems = 256;
     __device__ static void decode8(const uint32_t *w, uint32_t blk, uint32_t n, float (&v)[8]) {
         const uint32_t hh = n / 128, k = (n / 32) % 4, l = n % 32;
         const uint64_t ql = lds_u64_at(w, blk + 64 * hh + 32 * (k & 1) + l);
@@ -635,7 +636,7 @@ struct Q6KLds {
 // y = (d * sc) * q - (dmin * m).  Blocks are 144 = 9 * 16 bytes and the table
 // is 16-byte aligned, so every word read here is aligned.
 struct Q4KLds {
-    static constexpr uint32_t kBytes = 144;
+    static constexpr uint32_t kBytes = 144, kElems = 256;
     __device__ static void decode8(const uint32_t *w, uint32_t blk, uint32_t n, float (&v)[8]) {
         const uint32_t c = n / 64, j = n % 64, hi = j >= 32;
         const uint32_t *hw = w + blk / 4;
@@ -654,6 +655,48 @@ struct Q4KLds {
     }
 };
 
+// Q5_K (dequant.rs:59-107): 176-byte blocks of d, dmin, 12 scale bytes,
+// qh[32] at 16 and qs[128] at 48.  Output n is chunk c = n / 64, offset
+// j = n % 64, l = j % 32: the low (j < 32) or high nibble of qs[32c + l]
+// plus 16 when bit 2c (low) or 2c + 1 (high) of qh[l] is set, scaled by
+// group 2c (+1 for the high nibbles): y = (d * sc) * q - (dmin * m).
+// 176 = 11 * 16, so with a 4-byte-aligned table every word read is aligned.
+struct Q5KLds {
+    static constexpr uint32_t kBytes = 176, kElems = 256;
+    __device__ static void decode8(const uint32_t *w, uint32_t blk, uint32_t n, float (&v)[8]) {
+        const uint32_t c = n / 64, j = n % 64, hi = j >= 32, l = j % 32;
+        const uint32_t *hw = w + blk / 4;
+        const uint32_t h0 = hw[0];
+        const float d = half_bits_to_f32(h0 & 0xffffu), dmin = half_bits_to_f32(h0 >> 16);
+        uint32_t sc, m;
+        k4_scale_min(2 * c + hi, hw[1], hw[2], hw[3], sc, m);
+        const float dq = d * (float)sc, mq = dmin * (float)m;
+        const uint32_t qo = (blk + 48 + 32 * c + l) / 4, ho = (blk + 16 + l) / 4;
+        const uint32_t q0 = w[qo], q1 = w[qo + 1], g0 = w[ho], g1 = w[ho + 1];
+        const uint32_t sh = 4 * hi, hb = 2 * c + hi;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t lo = ((e < 4 ? q0 : q1) >> (8 * (e % 4) + sh)) & 15u;
+            const uint32_t up = (((e < 4 ? g0 : g1) >> (8 * (e % 4) + hb)) & 1u) << 4;
+            v[e] = dq * (float)(lo + up) - mq;
+        }
+    }
+};
+
+// Q8_0 (dequant.rs:172-192): 34-byte blocks of 32 elements, f16 d then 32
+// int8 values, y = d * (float)q.  Blocks are only 2-byte aligned: d sits at
+// an even offset (never straddling a dword) and the 8 values of a part are
+// assembled from unaligned LDS words.
+struct Q8_0Lds {
+    static constexpr uint32_t kBytes = 34, kElems = 32;
+    __device__ static void decode8(const uint32_t *w, uint32_t blk, uint32_t n, float (&v)[8]) {
+        const float d = half_bits_to_f32(w[blk / 4] >> (8 * (blk % 4)));
+        const uint64_t q = lds_u64_at(w, blk + 2 + n);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = d * (float)(int8_t)(q >> (8 * e));
+    }
+};
+
 template <typename F, typename O, int BLOCK, int NL, int NP, bool NORM>
 __global__ __launch_bounds__(BLOCK) void kquant_gather_lds_kernel(const uint8_t *__restrict__ table, uint64_t vocab,
                                                                   uint32_t dim, const uint32_t *__restrict__ ids,
@@ -663,11 +706,13 @@ __global__ __launch_bounds__(BLOCK) void kquant_gather_lds_kernel(const uint8_t 
                                                                   uint32_t *__restrict__ err) {
     extern __shared__ uint4 raw_lds[];
     __shared__ float red[BLOCK / kWave];
-    // Workgroup = (row, segment of bpw blocks).
-    const uint32_t nb = dim / 256, nseg = (nb + bpw - 1) / bpw;
+    // Workgroup = (row, segment of bpw blocks).  Without ids (a Cast) row r
+    // of the table is gathered.
+    constexpr uint32_t PPB = F::kElems / 8;  // parts per block
+    const uint32_t nb = dim / F::kElems, nseg = (nb + bpw - 1) / bpw;
     const uint32_t row = blockIdx.x / nseg, b0 = (blockIdx.x % nseg) * bpw;
     const uint32_t nblk = nb - b0 < bpw ? nb - b0 : bpw;
-    const uint32_t id = ids[row];
+    const uint32_t id = ids ? ids[row] : row;
     const bool bad = id >= vocab;
     if (bad && threadIdx.x == 0 && b0 == 0 && err) atomicOr(err, 1u);
     const uint8_t *segp = table + (bad ? 0 : (uint64_t)id * nb * F::kBytes) + F::kBytes * b0;
@@ -686,14 +731,14 @@ __global__ __launch_bounds__(BLOCK) void kquant_gather_lds_kernel(const uint8_t 
     for (int i = 0; i < NL; ++i) raw_lds[i * BLOCK + threadIdx.x] = c[i];  // LDS holds NL * BLOCK chunks
     __syncthreads();
     const uint32_t *w = reinterpret_cast<const uint32_t *>(raw_lds);
-    const uint32_t parts = nblk * 32;
-    typename O::T *out = h + (size_t)row * dim + 256 * (size_t)b0;
+    const uint32_t parts = nblk * PPB;
+    typename O::T *out = h + (size_t)row * dim + F::kElems * (size_t)b0;
     float v[NP][8];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         const uint32_t p = i * BLOCK + threadIdx.x;
         if (p < parts) {
-            F::decode8(w, lead + F::kBytes * (p / 32), 8 * (p % 32), v[i]);
+            F::decode8(w, lead + F::kBytes * (p / PPB), 8 * (p % PPB), v[i]);
             if (bad) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[i][e] = 0.0f;
@@ -734,24 +779,32 @@ __global__ __launch_bounds__(BLOCK) void kquant_gather_lds_kernel(const uint8_t 
     }
 }
 
-// Launches kquant_gather_lds_kernel when a thread's share fits the unrolled
-// counts (rows of up to 32768 elements at 128 threads); -1 otherwise.
-template <typename F, typename O>
-int launch_kquant_lds(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids, void *h,
-                      void *y, const float *w, float eps, uint32_t *err, hipStream_t s) {
-    constexpr int B = FELLM_EMB_KQ_LDS_BLOCK;
+// Launches kquant_gather_lds_kernel with B threads per workgroup when a
+// thread's share fits the unrolled counts (whole rows of up to 16384
+// elements at 64 threads); -1 otherwise.  Without the norm, `split` cuts
+// rows that do not fit into segments of blocks, one workgroup each.
+template <typename F, typename O, int B>
+int launch_kquant_lds_b(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids,
+                        void *h, void *y, const float *w, float eps, uint32_t *err, hipStream_t s, bool split) {
     if constexpr (B == 0) {
         return -1;
     } else {
         if (w && !aligned_to(w, 32)) return -1;  // 8-float weight vectors
-        const uint32_t nb = dim / 256;
-        const uint32_t bpw = !w && FELLM_EMB_Q6K_BPW && FELLM_EMB_Q6K_BPW < nb ? FELLM_EMB_Q6K_BPW : nb;
+        constexpr uint32_t PPB = F::kElems / 8;
+        const uint32_t nb = dim / F::kElems;
+        uint32_t bpw = !w && FELLM_EMB_Q6K_BPW && FELLM_EMB_Q6K_BPW < nb ? FELLM_EMB_Q6K_BPW : nb;
+        // Chunks a segment of bpw blocks spans (its start rounded down and its
+        // end rounded up to 16 bytes) and parts a thread decodes.
+        auto n16_of = [](uint32_t nblk) { return (F::kBytes * nblk + 15 + 15) / 16; };
+        if (split && !w && (n16_of(bpw) * 16 + 16 > 16u * B * 16 || (PPB * bpw + B - 1) / B > 32)) {
+            const uint32_t by_lds = (8u * B * 16 - 16 - 30) / F::kBytes, by_parts = 16u * B / PPB;
+            bpw = by_lds < by_parts ? by_lds : by_parts;
+        }
         const uint64_t grid = (uint64_t)n_ids * ((nb + bpw - 1) / bpw);
         if (grid > 0x7fffffffull) return -1;
-        const uint32_t n16 = (F::kBytes * bpw + 15 + 15) / 16;
-        const uint32_t nl = (n16 + B - 1) / B, np = (32 * bpw + B - 1) / B;
-        // The fused norm keeps the row in registers: longer rows take the
-        // 256-thread staged layout instead.
+        const uint32_t n16 = n16_of(bpw);
+        const uint32_t nl = (n16 + B - 1) / B, np = (PPB * bpw + B - 1) / B;
+        // The fused norm keeps the row in registers: at most 8 parts a thread.
         if (w && np > 8) return -1;
         const uint8_t *tb = static_cast<const uint8_t *>(table);
         using TO = typename O::T;
@@ -771,11 +824,28 @@ int launch_kquant_lds(const void *table, uint64_t vocab, uint32_t dim, const uin
         FELLM_Q6L(1, 2)
         FELLM_Q6L(2, 4)
         FELLM_Q6L(4, 8)
-        FELLM_Q6L(8, 16)
-        FELLM_Q6L(16, 32)
+        if (!w) {
+            FELLM_Q6L(8, 16)
+            FELLM_Q6L(16, 32)
+        } else {
+            FELLM_Q6L(8, 8)  // Q8_0 rows carry 34/32 bytes per element
+        }
 #undef FELLM_Q6L
         return -1;
     }
+}
+
+// The LDS gather at FELLM_EMB_KQ_LDS_BLOCK threads.  Q4_K and Q6_K keep
+// their staged layouts for what it does not fit; Q5_K and Q8_0 (`full`) have
+// only this kernel, so a fused norm over longer rows takes 256-thread
+// workgroups and longer plain rows are split into segments.
+template <typename F, typename O>
+int launch_kquant_lds(const void *table, uint64_t vocab, uint32_t dim, const uint32_t *ids, uint32_t n_ids, void *h,
+                      void *y, const float *w, float eps, uint32_t *err, hipStream_t s, bool full = false) {
+    const int st = launch_kquant_lds_b<F, O, FELLM_EMB_KQ_LDS_BLOCK>(table, vocab, dim, ids, n_ids, h, y, w, eps, err,
+                                                                     s, full);
+    if (st >= 0 || !full || !w) return st;
+    return launch_kquant_lds_b<F, O, 256>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s, false);
 }
 
 template <typename D, typename O>
@@ -896,6 +966,16 @@ int dispatch_table(const void *table, uint32_t table_dtype, uint64_t vocab, uint
             }
             if (FELLM_EMB_STAGE) return launch_emb<Q6KStaged, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
             return launch_emb<Q6KDec, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s);
+        case FELLM_DTYPE_Q5K: {
+            if (dim % 256 || !aligned_to(table, 4) || dim * sizeof(typename O::T) % 16) return FELLM_ERR_SHAPE;
+            const int st = launch_kquant_lds<Q5KLds, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s, true);
+            return st >= 0 ? st : FELLM_ERR_SHAPE;
+        }
+        case FELLM_DTYPE_Q8_0: {
+            if (dim % 32 || !aligned_to(table, 2) || dim * sizeof(typename O::T) % 16) return FELLM_ERR_SHAPE;
+            const int st = launch_kquant_lds<Q8_0Lds, O>(table, vocab, dim, ids, n_ids, h, y, w, eps, err, s, true);
+            return st >= 0 ? st : FELLM_ERR_SHAPE;
+        }
         default:
             break;
     }
@@ -996,6 +1076,20 @@ extern "C" int fellm_rocm_cast(const void *src, uint32_t src_dtype, void *dst, u
                 if (!aligned_to(src, 2)) return FELLM_ERR_SHAPE;
                 return launch_emb<Q6KDec, F32>(src, rows, dim, nullptr, (uint32_t)rows, dst, nullptr, nullptr, 0.0f,
                                                nullptr, s);
+            }
+            case FELLM_DTYPE_Q5K:
+            case FELLM_DTYPE_Q8_0: {
+                // Through the LDS gather with row r = table row r (no ids).
+                const bool q5 = src_dtype == FELLM_DTYPE_Q5K;
+                if (n_elems % (q5 ? 256 : 32) || !out_vec || !aligned_to(src, q5 ? 4 : 2)) return FELLM_ERR_SHAPE;
+                const uint32_t dim = cast_dim(n_elems, q5 ? 256 : 32);
+                if (!dim) return FELLM_ERR_SHAPE;
+                const uint64_t rows = n_elems / dim;
+                const int st = q5 ? launch_kquant_lds<Q5KLds, F32>(src, rows, dim, nullptr, (uint32_t)rows, dst, nullptr,
+                                                                   nullptr, 0.0f, nullptr, s, true)
+                                  : launch_kquant_lds<Q8_0Lds, F32>(src, rows, dim, nullptr, (uint32_t)rows, dst,
+                                                                    nullptr, nullptr, 0.0f, nullptr, s, true);
+                return st >= 0 ? st : FELLM_ERR_SHAPE;
             }
             default: return FELLM_ERR_DTYPE;
         }

@@ -807,7 +807,9 @@ const void *stage_ids(State &st, const std::vector<uint32_t> &ids) {
 uint64_t table_row_bytes(uint32_t dt, uint64_t dim) {
     switch (dt) {
         case FELLM_DTYPE_Q4K: return dim % 256 ? 0 : dim / 256 * 144;
+        case FELLM_DTYPE_Q5K: return dim % 256 ? 0 : dim / 256 * 176;
         case FELLM_DTYPE_Q6K: return dim % 256 ? 0 : dim / 256 * 210;
+        case FELLM_DTYPE_Q8_0: return dim % 32 ? 0 : dim / 32 * 34;
         default: return dim * dtype_size(dt);
     }
 }
@@ -928,9 +930,9 @@ int launch_cast_convert(const FellmOpAttrs *attrs, const FellmTensorRef *in, uin
     return guarded(attrs, in, n_in, out, n_out, 1, 1, false, [&](State &st) {
         const uint32_t sdt = in[0].dtype, ddt = out[0].dtype;
         const size_t n = elems(out[0], ddt);
-        const bool quant = sdt == FELLM_DTYPE_Q4K || sdt == FELLM_DTYPE_Q6K;
-        const size_t need = quant ? (n % 256 ? 0 : n / 256 * (sdt == FELLM_DTYPE_Q4K ? 144 : 210))
-                                  : n * dtype_size(sdt);
+        const bool quant = sdt == FELLM_DTYPE_Q4K || sdt == FELLM_DTYPE_Q5K || sdt == FELLM_DTYPE_Q6K ||
+                           sdt == FELLM_DTYPE_Q8_0;
+        const size_t need = quant ? table_row_bytes(sdt, n) : n * dtype_size(sdt);
         if (!need || in[0].byte_len < need) fail(FELLM_ERR_SHAPE);
         void *src = ensure_input(st, in[0]);
         void *dst = ensure_output(st, out[0]);
@@ -997,6 +999,7 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
         if (!vt || !vt->register_op) return FELLM_ERR_ARITY;
         const uint32_t F32 = FELLM_DTYPE_F32, F16 = FELLM_DTYPE_F16, BF16 = FELLM_DTYPE_BF16;
         const uint32_t Q4K = FELLM_DTYPE_Q4K, Q5K = FELLM_DTYPE_Q5K, Q6K = FELLM_DTYPE_Q6K, U32 = FELLM_DTYPE_U32;
+        const uint32_t Q8_0 = FELLM_DTYPE_Q8_0;
         struct R {
             uint32_t op;
             std::initializer_list<uint32_t> ins;
@@ -1016,6 +1019,8 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
             {FELLM_OP_CAST, {F32}, BF16, launch_cast_convert},
             {FELLM_OP_CAST, {Q4K}, F32, launch_cast_convert},
             {FELLM_OP_CAST, {Q6K}, F32, launch_cast_convert},
+            {FELLM_OP_CAST, {Q5K}, F32, launch_cast_convert},
+            {FELLM_OP_CAST, {Q8_0}, F32, launch_cast_convert},
             {FELLM_OP_RMSNORM, {F32, F32}, F32, launch_rmsnorm},
             {FELLM_OP_SILU_GATE, {F32, F32}, F32, launch_silu_gate},
             {FELLM_OP_ROPE, {F32, F32}, F32, launch_rope},
@@ -1025,6 +1030,8 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
             {FELLM_OP_EMBEDDING, {BF16, U32}, F32, launch_embedding},
             {FELLM_OP_EMBEDDING, {Q4K, U32}, F32, launch_embedding},
             {FELLM_OP_EMBEDDING, {Q6K, U32}, F32, launch_embedding},
+            {FELLM_OP_EMBEDDING, {Q5K, U32}, F32, launch_embedding},
+            {FELLM_OP_EMBEDDING, {Q8_0, U32}, F32, launch_embedding},
             // backend-cpu also serves F16 tables (backend.rs:453-467).
             {FELLM_OP_EMBEDDING, {F16, U32}, F32, launch_embedding},
             // 16-bit activation variants.
@@ -1042,6 +1049,8 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
             {FELLM_OP_EMBEDDING, {BF16, U32}, BF16, launch_embedding},
             {FELLM_OP_EMBEDDING, {Q4K, U32}, F16, launch_embedding},
             {FELLM_OP_EMBEDDING, {Q6K, U32}, F16, launch_embedding},
+            {FELLM_OP_EMBEDDING, {Q5K, U32}, F16, launch_embedding},
+            {FELLM_OP_EMBEDDING, {Q8_0, U32}, F16, launch_embedding},
             // GateUpSwiGlu for every K-quant gate/up pair (backend-cpu accepts any
             // supported matvec dtype pair, backend.rs:430-435; the CUDA plugin
             // registers the same-dtype pairs, lib.rs:467-496).
@@ -1072,6 +1081,8 @@ int _fellm_plugin_register_kernels(FellmKernelRegistryVtable *vt) {
             {kOpEmbeddingRmsNorm, {F16, U32, F32}, F16, launch_embedding_rmsnorm},
             {kOpEmbeddingRmsNorm, {Q4K, U32, F32}, F16, launch_embedding_rmsnorm},
             {kOpEmbeddingRmsNorm, {Q6K, U32, F32}, F16, launch_embedding_rmsnorm},
+            {kOpEmbeddingRmsNorm, {Q5K, U32, F32}, F16, launch_embedding_rmsnorm},
+            {kOpEmbeddingRmsNorm, {Q8_0, U32, F32}, F16, launch_embedding_rmsnorm},
         };
         int idx = 0;
         for (const R &r : regs) {

@@ -93,10 +93,14 @@ def add(a, b, out=None):
     return out
 
 
+# Quantized embedding tables: the K-quants and Q8_0 (34-byte blocks of 32).
+TABLE_QTYPES = {**{k: v[0] for k, v in QTYPES.items()}, "q8_0": DType.Q8_0}
+
+
 def _table_code(table: torch.Tensor, qtype: str | None) -> int:
     if qtype is None:
         return _code(table)
-    return int(QTYPES[qtype][0])
+    return int(TABLE_QTYPES[qtype])
 
 
 def embedding(table, ids, *, dim: int | None = None, qtype: str | None = None, out=None,
@@ -104,7 +108,7 @@ def embedding(table, ids, *, dim: int | None = None, qtype: str | None = None, o
     """Gather rows ``table[ids]``.
 
     Dense tables are ``[vocab, dim]`` f32/f16/bf16 tensors.  Quantized tables
-    (``qtype`` "q4k" or "q6k") are uint8 ``[vocab, row_bytes]`` with ``dim``
+    (``qtype`` "q4k", "q5k", "q6k" or "q8_0") are uint8 ``[vocab, row_bytes]`` with ``dim``
     elements per row.  ``ids`` is int32 (read as u32).
     """
     _dev(table, ids)

@@ -72,6 +72,16 @@ def q5k_table(rng: np.random.Generator, vocab: int, dim: int) -> np.ndarray:
     return blocks.reshape(vocab, nb * 176)
 
 
+def q8_0_table(rng: np.random.Generator, vocab: int, dim: int) -> np.ndarray:
+    """uint8 [vocab, dim/32*34]: per 32-element block d ~ f16(|N(0, 0.01)|), then 32 uniform int8."""
+    assert dim % 32 == 0
+    nb = dim // 32
+    blocks = np.empty((vocab, nb, 34), np.uint8)
+    blocks[..., 0:2] = _abs_normal_f16_bits(rng, (vocab, nb), 0.01).view(np.uint8).reshape(vocab, nb, 2)
+    blocks[..., 2:] = rng.integers(0, 256, size=(vocab, nb, 32), dtype=np.uint8)
+    return blocks.reshape(vocab, nb * 34)
+
+
 KQUANT_TABLES = {12: q4k_table, 13: q5k_table, 14: q6k_table}
 KQUANT_BLOCK_BYTES = {12: 144, 13: 176, 14: 210}
 

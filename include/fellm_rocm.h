@@ -61,8 +61,11 @@ int fellm_rocm_add(const void *a, const void *b, uint32_t in_dtype, void *out, u
 /*
  * Embedding gather: out[t, :] = dequant(table[ids[t], :]).
  *   replaces: Embedding (backend.rs:1026-1046, kernels/embedding.rs:10-23,
- *             dequant.rs:19-55 F32/F16/BF16, :251-305 Q4_K, :315-370 Q6_K).
- * table_dtype: F32, F16, BF16, Q4K or Q6K (Q4K/Q6K need dim % 256 == 0).
+ *             dequant.rs:19-55 F32/F16/BF16, :251-305 Q4_K, :315-370 Q6_K,
+ *             :59-107 Q5_K, :172-192 Q8_0; the CUDA plugin's Q5_K and Q8_0 keys,
+ *             plugins/cuda_kernels/src/lib.rs:637-661).
+ * table_dtype: F32, F16, BF16, Q4K, Q5K, Q6K (dim % 256 == 0) or Q8_0 (dim % 32 == 0).
+ * Q5K tables must be 4-byte aligned, Q8_0 and Q6K tables 2-byte aligned.
  * out_dtype:   F32, F16 or BF16.
  * An id >= vocab yields a zero row and sets *err_flag (device u32, may be NULL)
  * to 1; the CPU reference rejects such ids.
@@ -291,8 +294,8 @@ int fellm_rocm_attention_f32kv(const float *q, float *out, uint32_t rows, uint32
  *   replaces: launch_cast (crates/backend-cpu/src/backend.rs:1603-1667).
  * Pairs (as the CPU backend): F32->F32, F16->F32, BF16->F32 (exact widening),
  * F32->F16 (round to nearest even), F32->BF16 (truncation: the top 16 bits),
- * Q4K->F32 and Q6K->F32 (dequantization of the block stream, n_elems % 256 == 0,
- * dst 16-byte aligned).  Other pairs return FELLM_ERR_DTYPE.
+ * Q4K/Q5K/Q6K->F32 (dequantization of the block stream, n_elems % 256 == 0,
+ * dst 16-byte aligned) and Q8_0->F32 (n_elems % 32 == 0).  Other pairs return FELLM_ERR_DTYPE.
  */
 int fellm_rocm_cast(const void *src, uint32_t src_dtype, void *dst, uint32_t dst_dtype, uint64_t n_elems,
                     void *stream);

@@ -8,9 +8,10 @@
  * Paths are relative to the FeLLM repository root.
  *
  * Parity pins (see tests/test_oracle.py):
- *   dequant Q4_K / Q5_K / Q6_K, get_scale_min_k4 — reference known-answer
+ *   dequant Q4_K / Q5_K / Q6_K / Q8_0, get_scale_min_k4 — reference known-answer
  *     tests (dequant.rs:377-398, :435-476, :478-498), closed-form blocks from
  *     crates/fellm-plugin-host/tests/load_cuda_kernels.rs:194-199, :257-263,
+ *     the Q8_0 block of load_cuda_kernels.rs:131-140 (d = 1, values 1..=32),
  *     and an independent per-element decode on random blocks.
  *   f16 / bf16 conversions — numpy's IEEE binary16 and exhaustive bit checks.
  *   rmsnorm — norm.rs:60-81 tests, closed forms, f64 recomputation.  The
@@ -194,8 +195,7 @@ static int dequantize_q4_k(const uint8_t *src, float *dst, size_t n) {
     return 0;
 }
 
-/* dequant.rs:59-107 (Q5_K: only used to port the reference's golden fixture,
- * which pins the shared d/dmin/get_scale_min_k4 machinery). */
+/* dequant.rs:59-107 (Q5_K: block layout d, dmin, 12 scale bytes, qh[32], qs[128]). */
 static int dequantize_q5_k(const uint8_t *src, float *dst, size_t n) {
     if (n % QK_K) return -1;
     for (size_t b = 0; b < n / QK_K; ++b) {
@@ -263,11 +263,24 @@ static int dequantize_q6_k(const uint8_t *src, float *dst, size_t n) {
     return 0;
 }
 
+/* dequant.rs:172-192 (Q8_0: 34-byte blocks of 32, f16 d then 32 int8,
+ * y = d * (q as f32)). */
+static int dequantize_q8_0(const uint8_t *src, float *dst, size_t n) {
+    if (n % 32) return -1;
+    for (size_t b = 0; b < n / 32; ++b) {
+        const uint8_t *base = src + b * 34;
+        const float d = f16_to_f32(le16(base));
+        for (int i = 0; i < 32; ++i) dst[b * 32 + i] = d * (float)(int8_t)base[2 + i];
+    }
+    return 0;
+}
+
 /* Row bytes for `dim` elements of a table dtype (DType::byte_size). */
 size_t oracle_row_bytes(uint32_t dtype, size_t dim) {
     switch (dtype) {
         case 0: return dim * 4;
         case 1: case 30: return dim * 2;
+        case 8: return dim % 32 ? 0 : dim / 32 * 34;
         case 12: return dim / QK_K * 144;
         case 13: return dim / QK_K * 176;
         case 14: return dim / QK_K * 210;
@@ -275,12 +288,13 @@ size_t oracle_row_bytes(uint32_t dtype, size_t dim) {
     }
 }
 
-/* dequant.rs:19-55 (F32, F16, BF16, Q4_K, Q5_K, Q6_K arms) */
+/* dequant.rs:19-55 (F32, F16, BF16, Q8_0, Q4_K, Q5_K, Q6_K arms) */
 int oracle_dequantize_row(uint32_t dtype, const uint8_t *src, float *dst, size_t n) {
     switch (dtype) {
         case 0: memcpy(dst, src, n * 4); return 0;
         case 1: for (size_t i = 0; i < n; ++i) dst[i] = f16_to_f32(le16(src + 2 * i)); return 0;
         case 30: for (size_t i = 0; i < n; ++i) dst[i] = bf16_to_f32(le16(src + 2 * i)); return 0;
+        case 8: return dequantize_q8_0(src, dst, n);
         case 12: return dequantize_q4_k(src, dst, n);
         case 13: return dequantize_q5_k(src, dst, n);
         case 14: return dequantize_q6_k(src, dst, n);

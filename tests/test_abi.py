@@ -113,11 +113,18 @@ REFERENCE_KEYS = [
     (abi.OpKind.EMBEDDING, [abi.DType.BF16, abi.DType.U32], abi.DType.F32),
     (abi.OpKind.EMBEDDING, [abi.DType.Q4K, abi.DType.U32], abi.DType.F32),
     (abi.OpKind.EMBEDDING, [abi.DType.Q6K, abi.DType.U32], abi.DType.F32),
+    (abi.OpKind.EMBEDDING, [abi.DType.Q5K, abi.DType.U32], abi.DType.F32),
+    # load_cuda_kernels.rs:107-111 asserts this key on the CUDA plugin.
+    (abi.OpKind.EMBEDDING, [abi.DType.Q8_0, abi.DType.U32], abi.DType.F32),
 ]
 NEW_KEYS = [
     (abi.OpKind.RMSNORM, [abi.DType.F16, abi.DType.F32], abi.DType.F16),
     (abi.OpKind.SILU_GATE, [abi.DType.BF16, abi.DType.BF16], abi.DType.BF16),
     (abi.OpKind.EMBEDDING, [abi.DType.Q4K, abi.DType.U32], abi.DType.F16),
+    (abi.OpKind.EMBEDDING, [abi.DType.Q5K, abi.DType.U32], abi.DType.F16),
+    (abi.OpKind.EMBEDDING, [abi.DType.Q8_0, abi.DType.U32], abi.DType.F16),
+    (abi.OpKind.CAST, [abi.DType.Q5K], abi.DType.F32),
+    (abi.OpKind.CAST, [abi.DType.Q8_0], abi.DType.F32),
     (abi.OP_ADD_RMSNORM, [abi.DType.F16, abi.DType.F16, abi.DType.F32], abi.DType.F16),
     (abi.OP_ROPE_KV_WRITE, [abi.DType.BF16, abi.DType.BF16, abi.DType.BF16, abi.DType.F32], abi.DType.BF16),
     (abi.OP_ROUTER_TOPK, [abi.DType.F32], abi.DType.U32),

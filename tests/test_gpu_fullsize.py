@@ -3,10 +3,14 @@
 Each config's chain is built exactly as bench.py builds it (same shapes,
 seeds and launch paths), run once, and 64-128 seeded sample rows of every
 op's output are compared with the oracle on the same input rows:
+  * configs[0] (Llama-3.2-1B, 64 tokens, f32; every row): embedding gather
+    from the full 128256 x 2048 table, RMSNorm (alone and fused with a
+    residual add), RoPE q+k 32/8 heads at positions 0..63, SwiGLU 64 x 8192;
   * configs[1] (Llama-3-8B prefill, T 4096, f16): embedding gather, residual
     add + RMSNorm, RoPE q+k, SwiGLU;
   * configs[2] (Qwen2-7B, Q4_K / Q6_K tables 152064 x 3584, Zipf ids): both
-    gathers and the fused gather + RMSNorm;
+    gathers and the fused gather + RMSNorm; Q5_K and Q8_0 tables of the same
+    shape;
   * configs[3] (Llama-3-70B decode, 256 sequences, 4.29 GB bf16 paged arena):
     RoPE + K/V append (q rows and the K/V slot bytes), add + RMSNorm, SwiGLU;
   * configs[4] (Qwen3-30B-A3B, 16384 tokens): router top-8 (every row),
@@ -56,6 +60,52 @@ def _run(chain, s):
     for op in chain:
         op.fn(s)
     torch.cuda.synchronize()
+
+
+def test_c1_chain_full_size(ops, dev):
+    """configs[0] as stated: one seed; table ~N(0, 0.02) of 128256 x 2048 f32,
+    64 uniform ids, RMSNorm weight ~N(1, 0.1) at eps 1e-5, RoPE hd 64 with 32 Q
+    and 8 KV heads at theta 5e5 and positions 0..63, gate and up ~N(0, 1) of
+    64 x 8192.  The gathered rows feed the RMSNorm, as in the model."""
+    V, H, T, nq, nkv, hd, I = 128256, 2048, 64, 32, 8, 64, 8192
+    rng = np.random.default_rng(100)
+    table = np.empty((V, H), np.float32)
+    for i in range(0, V, 16384):  # f32 draws, in slices to bound host memory
+        n = min(16384, V - i)
+        table[i:i + n] = rng.standard_normal(size=(n, H), dtype=np.float32) * np.float32(0.02)
+    ids = rng.integers(0, V, size=T, dtype=np.uint32)
+    w = (1.0 + 0.1 * rng.standard_normal(size=H)).astype(np.float32)
+    r = (2.0 * rng.standard_normal(size=(T, H))).astype(np.float32)
+    q = rng.standard_normal(size=(T, nq * hd)).astype(np.float32)
+    k = rng.standard_normal(size=(T, nkv * hd)).astype(np.float32)
+    g = rng.standard_normal(size=(T, I)).astype(np.float32)
+    u = rng.standard_normal(size=(T, I)).astype(np.float32)
+
+    def d(a):
+        return torch.from_numpy(a).to(dev)
+
+    tab_d = d(table)
+    del table
+    emb = ops.embedding(tab_d, d(ids.view(np.int32)), out_dtype=torch.float32)
+    w_d = d(w)
+    y = ops.rmsnorm(emb, w_d, 1e-5)
+    h2, y2 = ops.add_rmsnorm(emb, d(r), w_d, 1e-5)
+    inv = ops.rope_inv_freqs(500000.0, hd).to(dev)
+    qo, ko = ops.rope(d(q), inv, head_dim=hd, x2=d(k))
+    act = ops.silu_gate(d(g), d(u))
+    torch.cuda.synchronize()
+    rows = tab_d[torch.from_numpy(ids.astype(np.int64)).to(dev)].cpu().numpy()
+    e_ref = oracle.embedding(rows.view(np.uint8), 0, T, H, np.arange(T, dtype=np.uint32))
+    assert_exact(emb.cpu().numpy(), e_ref, "c1 embedding")
+    assert_close(y.cpu().numpy(), oracle.rmsnorm(e_ref, w, 1e-5), "f32", what="c1 rmsnorm")
+    h_ref, y2_ref = oracle.add_rmsnorm(e_ref, r, w, 1e-5, "f32")
+    assert_exact(h2.cpu().numpy(), h_ref, "c1 h")
+    assert_close(y2.cpu().numpy(), y2_ref, "f32", what="c1 add + rmsnorm")
+    inv_ref = oracle.rope_inv_freqs(500000.0, hd)
+    pos = np.arange(T, dtype=np.uint32)
+    assert_exact(qo.cpu().numpy(), oracle.rope(q, nq, hd, hd, 0, inv_ref, pos), "c1 rope q")
+    assert_exact(ko.cpu().numpy(), oracle.rope(k, nkv, hd, hd, 0, inv_ref, pos), "c1 rope k")
+    assert_exact(act.cpu().numpy(), oracle.silu_gate(g, u), "c1 swiglu")
 
 
 def test_c2_chain_full_size(ops, dev):
@@ -125,6 +175,12 @@ def test_c3_quantized_gathers_full_size(ops, dev):
         assert_exact(_rows(s["out"], idx), oracle.narrow(rows, "f16"), f"c3 {op.name} h")
         assert_close(_rows(s["y"], idx), oracle.narrow(oracle.rmsnorm(rows, w, 1e-6), "f16"), "f16",
                      what=f"c3 {op.name} y")
+    for op, name, code in ((chain[4], "q5", 13), (chain[5], "q8", 8)):
+        tab = _closure(op.fn, name).cpu().numpy()
+        op.fn(s)
+        torch.cuda.synchronize()
+        ref = oracle.narrow(oracle.embedding(tab, code, tab.shape[0], D, ids[idx]), "f16")
+        assert_exact(_rows(s["out"], idx), ref, f"c3 {op.name}")
 
 
 def test_c4_decode_step_full_size(ops, dev):

@@ -112,11 +112,15 @@ def test_register_device_tensor(host):
     assert np.array_equal(materialize(host, out, D.F32), np.arange(256, dtype=np.float32) + 1)
 
 
-@pytest.mark.parametrize("qt,out_dt", [(D.Q4K, D.F32), (D.Q6K, D.F16), (D.Q4K, D.F16)])
+_QTABLE = {D.Q4K: synth.q4k_table, D.Q5K: synth.q5k_table, D.Q6K: synth.q6k_table, D.Q8_0: synth.q8_0_table}
+
+
+@pytest.mark.parametrize("qt,out_dt", [(D.Q4K, D.F32), (D.Q6K, D.F16), (D.Q4K, D.F16), (D.Q5K, D.F32), (D.Q5K, D.F16),
+                                       (D.Q8_0, D.F32), (D.Q8_0, D.F16)])
 def test_embedding_quant(host, qt, out_dt):
     rng = np.random.default_rng(int(qt) + int(out_dt))
     vocab, dim = 200, 1024
-    table = synth.q4k_table(rng, vocab, dim) if qt == D.Q4K else synth.q6k_table(rng, vocab, dim)
+    table = _QTABLE[qt](rng, vocab, dim)
     ids = rng.integers(0, vocab, size=50, dtype=np.uint32)
     out = np.zeros((50, dim), np.float32 if out_dt == D.F32 else np.float16)
     run(host, abi.OpKind.EMBEDDING, [qt, D.U32], out_dt, abi.OpAttrs(),
@@ -128,6 +132,20 @@ def test_embedding_quant(host, qt, out_dt):
         assert_exact(got, ref, "plugin q-embedding")
     else:
         assert_exact(got.view(np.uint16), oracle.narrow(ref, "f16"), "plugin q-embedding f16")
+
+
+def test_embedding_q8_0_reference_block(host):
+    """The Q8_0 block of the reference's CUDA test (load_cuda_kernels.rs:131-140: d = 1.0, values
+    1..=32) as a one-row table, gathered through the registry's Embedding [Q8_0, U32] -> F32 key."""
+    table = np.zeros(34, np.uint8)
+    table[0:2] = [0x00, 0x3C]
+    table[2:] = np.arange(1, 33)
+    ids = np.zeros(3, np.uint32)
+    out = np.zeros((3, 32), np.float32)
+    run(host, abi.OpKind.EMBEDDING, [D.Q8_0, D.U32], D.F32, abi.OpAttrs(),
+        [tref(table, D.Q8_0, [1, 32], logical_id=2999), tref(ids, D.U32)], [tmut(out, D.F32, [3, 32])])
+    got = materialize(host, out, D.F32)
+    assert np.array_equal(got, np.tile(np.arange(1, 33, dtype=np.float32), (3, 1)))
 
 
 def test_embedding_weight_cached_by_logical_id(host):

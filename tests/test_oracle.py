@@ -21,7 +21,7 @@ import oracle
 from fellm_amd import synth
 
 GOLD = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
-F32, F16, Q4K, Q5K, Q6K, BF16 = 0, 1, 12, 13, 14, 30
+F32, F16, Q8_0, Q4K, Q5K, Q6K, BF16 = 0, 1, 8, 12, 13, 14, 30
 
 
 # ---- dtype edges ----------------------------------------------------------------
@@ -161,16 +161,67 @@ def _q6k_per_element(block: np.ndarray) -> np.ndarray:
     return ((d[:, None] * sc).astype(np.float32) * q.astype(np.float32)).astype(np.float32).reshape(-1)
 
 
-@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+def _q5k_per_element(block: np.ndarray) -> np.ndarray:
+    """Per-element Q5_K decode with the CUDA plugin's indexing (oxide_kernels.rs:3687-3719,
+    q5k_dequant_at): group j / 32, qs chunk j / 64 at byte 48, high bit (1 or 2) << 2 * chunk of
+    qh[j % 32] at byte 16; y = d * sc * q - dmin * m, evaluated left to right."""
+    nb = block.size // 176
+    b = block.reshape(nb, 176)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    sc, mn = _scales_mins_masked(b[:, 4:16].copy())
+    j = np.arange(256)
+    group, lane, chunk = j // 32, j % 32, j // 64
+    low = j % 64 < 32
+    raw = b[:, 48 + chunk * 32 + lane]
+    bit = np.where(low, 1, 2) << (chunk * 2)
+    hi = (b[:, 16 + lane] & bit) != 0
+    q = (np.where(low, raw & 15, raw >> 4) + np.where(hi, 16, 0)).astype(np.float32)
+    d_sc = (d[:, None] * sc[:, group].astype(np.float32)).astype(np.float32)
+    m = (dmin[:, None] * mn[:, group].astype(np.float32)).astype(np.float32)
+    return ((d_sc * q).astype(np.float32) - m).astype(np.float32).reshape(-1)
+
+
+def _q8_0_per_element(row: np.ndarray) -> np.ndarray:
+    """Per-element Q8_0 decode with the CUDA plugin's indexing (oxide_kernels.rs:2559-2581,
+    embedding_q8_0_rows): d at the 34-byte block's start, int8 value at 2 + lane."""
+    b = row.reshape(-1, 34)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    q = b[:, 2:].view(np.int8).astype(np.float32)
+    return (d[:, None] * q).astype(np.float32).reshape(-1)
+
+
+_PER_ELEMENT = {"q4k": (Q4K, _q4k_per_element), "q5k": (Q5K, _q5k_per_element), "q6k": (Q6K, _q6k_per_element),
+                "q8_0": (Q8_0, _q8_0_per_element)}
+
+
+@pytest.mark.parametrize("kind", ["q4k", "q5k", "q6k", "q8_0"])
 def test_quant_decode_matches_per_element_restatement(kind):
     rng = np.random.default_rng(17)
     dim = 2048
-    table = synth.q4k_table(rng, 64, dim) if kind == "q4k" else synth.q6k_table(rng, 64, dim)
-    code = Q4K if kind == "q4k" else Q6K
+    code, per_element = _PER_ELEMENT[kind]
+    table = {"q4k": synth.q4k_table, "q5k": synth.q5k_table, "q6k": synth.q6k_table,
+             "q8_0": synth.q8_0_table}[kind](rng, 64, dim)
     for row in range(64):
         got = oracle.dequantize_row(code, table[row], dim)
-        ref = _q4k_per_element(table[row]) if kind == "q4k" else _q6k_per_element(table[row])
+        ref = per_element(table[row])
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"row {row}"
+
+
+def test_q8_0_reference_block():
+    """The Q8_0 block of the reference's CUDA matmul test: d = 1.0, values 1..=32; its dots with
+    rows of ones and twos are the test's expected 528 and 1056."""
+    g = GOLD["q8_0_one_to_32_block"]
+    block = np.zeros(34, np.uint8)
+    block[0:2] = [0x00, 0x3C]
+    block[2:] = np.arange(1, 33)
+    v = oracle.dequantize_row(Q8_0, block, 32)
+    assert v.tolist() == g["values"]
+    assert float(v.sum()) == g["dot_ones"] and float((2 * v).sum()) == g["dot_twos"]
+    # Negative values are two's-complement int8 (`as i8`, dequant.rs:187).
+    block[2:] = np.arange(0x80, 0xA0)
+    assert oracle.dequantize_row(Q8_0, block, 32).tolist() == list(range(-128, -96))
+    assert oracle.row_bytes(Q8_0, 96) == 102 and oracle.row_bytes(Q8_0, 100) == 0
 
 
 def test_embedding_gathers_rows_exactly():
