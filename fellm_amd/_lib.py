@@ -75,6 +75,7 @@ _SIGNATURES = {
     "fellm_rocm_mathf": (I32, [U32, P, P, U64, P]),
     "fellm_rocm_timing_arm": (I32, [P, P]),
     "fellm_rocm_attention_f32kv": (I32, [P, P, U32, U32, U32, U32, P, P, U32, U32, P, P, U32, F32, P]),
+    "fellm_rocm_attention_f32kv_rows": (I32, [P, P, U32, U32, U32, U32, P, P, U32, F32, U32, U32, P]),
     "fellm_rocm_decode_step": (I32, [C.POINTER(FellmRocmDecodeStep), P]),
     "fellm_rocm_stream_probe": (I32, [P, P, U64, P, U64, U32, P]),
     "fellm_rocm_timing_disarm": (None, []),

@@ -564,16 +564,34 @@ template <int VD, int GM>
 __global__ __launch_bounds__(kF32kvWaves * kWave) void attention_f32kv_kernel(
     const float *__restrict__ q, float *__restrict__ out, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
     const float *__restrict__ k1, const float *__restrict__ v1, uint32_t b1, uint32_t e1,
-    const float *__restrict__ k2, const float *__restrict__ v2, uint32_t n2, float scale) {
+    const float *__restrict__ k2, const float *__restrict__ v2, uint32_t n2, float scale, uint32_t rows,
+    uint32_t row_mode, uint32_t window, uint32_t head_major) {
     extern __shared__ float f32kv_lds[];
+    __shared__ uint64_t exp_tab[32];
     const uint32_t G = n_heads / n_kv;
     const uint32_t row = blockIdx.x / n_kv, g = blockIdx.x % n_kv;
     const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const size_t kv_w = (size_t)n_kv * hd;  // elements per K/V row
     float *q_lds = f32kv_lds;                        // [G][hd]
     float *p_lds = f32kv_lds + GM * hd;              // [waves][GM][64]
-    const float *qrow = q + ((size_t)row * n_heads + (size_t)g * G) * hd;
-    for (uint32_t i = threadIdx.x; i < G * hd; i += kF32kvWaves * kWave) q_lds[i] = qrow[i];
+    // q (and out) rows: [row][head][d], or head-major [head][row][d].
+    const size_t hstride = head_major ? (size_t)rows * hd : hd;
+    const size_t qbase = head_major ? ((size_t)g * G * rows + row) * hd : ((size_t)row * n_heads + (size_t)g * G) * hd;
+    for (uint32_t i = threadIdx.x; i < G * hd; i += kF32kvWaves * kWave)
+        q_lds[i] = q[qbase + (size_t)(i / hd) * hstride + i % hd];
+    if (threadIdx.x < 32) exp_tab[threadIdx.x] = make_expf_table().tab[threadIdx.x];
+    // This row's keys of the first pair: [b1, e1) as given (row_mode 0);
+    // causal with the query rows ending at key e1 - 1 (row_mode 1: keys up to
+    // e1 - rows + row, the last `window` of them when window > 0); or within
+    // `window` of the row index (row_mode 2, all keys when window == 0).
+    if (row_mode == 1) {
+        const uint32_t last = e1 - rows + row;
+        e1 = last + 1;
+        b1 = window && e1 > window ? e1 - window : 0;
+    } else if (row_mode == 2) {
+        b1 = window && row + 1 > window ? row + 1 - window : 0;
+        if (window && row + window < e1) e1 = row + window;
+    }
     __syncthreads();
 
     const uint32_t n1 = e1 > b1 ? e1 - b1 : 0, n = n1 + n2;
@@ -615,8 +633,8 @@ __global__ __launch_bounds__(kF32kvWaves * kWave) void attention_f32kv_kernel(
             if (h >= (int)G) continue;
             const float s = valid ? sc[h] * scale : -__builtin_inff();
             const float m_new = fmaxf(m[h], wave_max(s));
-            alpha[h] = m[h] > -__builtin_inff() ? __expf(m[h] - m_new) : 0.0f;
-            const float p = valid ? __expf(s - m_new) : 0.0f;
+            alpha[h] = m[h] > -__builtin_inff() ? expf_glibc(m[h] - m_new, exp_tab) : 0.0f;
+            const float p = valid ? expf_glibc(s - m_new, exp_tab) : 0.0f;
             l[h] = l[h] * alpha[h] + wave_sum(p);
             m[h] = m_new;
             pw[h * kWave + lane] = p;
@@ -682,8 +700,8 @@ __global__ __launch_bounds__(kF32kvWaves * kWave) void attention_f32kv_kernel(
                 const float mo = sh[0], lo = sh[1];
                 const float mn = fmaxf(m[h], mo);
                 if (mn == -__builtin_inff()) continue;
-                const float a = m[h] > -__builtin_inff() ? __expf(m[h] - mn) : 0.0f;
-                const float b = mo > -__builtin_inff() ? __expf(mo - mn) : 0.0f;
+                const float a = m[h] > -__builtin_inff() ? expf_glibc(m[h] - mn, exp_tab) : 0.0f;
+                const float b = mo > -__builtin_inff() ? expf_glibc(mo - mn, exp_tab) : 0.0f;
                 l[h] = l[h] * a + lo * b;
                 m[h] = mn;
 #pragma unroll
@@ -695,7 +713,7 @@ __global__ __launch_bounds__(kF32kvWaves * kWave) void attention_f32kv_kernel(
         }
     }
     if (wave == 0) {
-        float *orow = out + ((size_t)row * n_heads + (size_t)g * G) * hd;
+        float *orow = out + qbase;
 #pragma unroll
         for (int h = 0; h < GM; ++h) {
             if (h >= (int)G) continue;
@@ -703,7 +721,7 @@ __global__ __launch_bounds__(kF32kvWaves * kWave) void attention_f32kv_kernel(
 #pragma unroll
             for (int c = 0; c < VD; ++c) {
                 const uint32_t d = lane + c * kWave;
-                if (d < hd) orow[(size_t)h * hd + d] = l[h] > 0.0f ? acc[h][c] * inv : 0.0f;
+                if (d < hd) orow[(size_t)h * hstride + d] = l[h] > 0.0f ? acc[h][c] * inv : 0.0f;
             }
         }
     }
@@ -759,11 +777,13 @@ extern "C" int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void 
     return FELLM_ERR_DTYPE;
 }
 
-extern "C" int fellm_rocm_attention_f32kv(const float *q, float *out, uint32_t rows, uint32_t n_heads,
-                                          uint32_t n_kv_heads, uint32_t head_dim, const float *k1, const float *v1,
-                                          uint32_t begin1, uint32_t end1, const float *k2, const float *v2, uint32_t n2,
-                                          float scale, void *stream) {
-    using namespace fellm;
+namespace fellm {
+namespace {
+
+int attention_f32kv_common(const float *q, float *out, uint32_t rows, uint32_t n_heads, uint32_t n_kv_heads,
+                           uint32_t head_dim, const float *k1, const float *v1, uint32_t begin1, uint32_t end1,
+                           const float *k2, const float *v2, uint32_t n2, float scale, uint32_t row_mode,
+                           uint32_t window, uint32_t head_major, void *stream) {
     if (!q || !out) return FELLM_ERR_ARITY;
     if (end1 > begin1 && (!k1 || !v1)) return FELLM_ERR_ARITY;
     if (n2 && (!k2 || !v2)) return FELLM_ERR_ARITY;
@@ -781,7 +801,8 @@ extern "C" int fellm_rocm_attention_f32kv(const float *q, float *out, uint32_t r
         const size_t b = (size_t)GM * (2 + head_dim);
         const size_t lds = (a > b ? a : b) * sizeof(float);
         FELLM_LAUNCH((attention_f32kv_kernel<VD, GM>), dim3(rows * n_kv_heads), dim3(kF32kvWaves * kWave), lds, st,
-                     q, out, n_heads, n_kv_heads, head_dim, k1, v1, begin1, end1, k2, v2, n2, scale);
+                     q, out, n_heads, n_kv_heads, head_dim, k1, v1, begin1, end1, k2, v2, n2, scale, rows, row_mode,
+                     window, head_major);
         return launch_status();
     };
     auto go_vd = [&]<int GM>() -> int {
@@ -794,4 +815,26 @@ extern "C" int fellm_rocm_attention_f32kv(const float *q, float *out, uint32_t r
     if (G <= 4) return go_vd.template operator()<4>();
     if (G <= 8) return go_vd.template operator()<8>();
     return go_vd.template operator()<16>();
+}
+
+}  // namespace
+}  // namespace fellm
+
+extern "C" int fellm_rocm_attention_f32kv(const float *q, float *out, uint32_t rows, uint32_t n_heads,
+                                          uint32_t n_kv_heads, uint32_t head_dim, const float *k1, const float *v1,
+                                          uint32_t begin1, uint32_t end1, const float *k2, const float *v2, uint32_t n2,
+                                          float scale, void *stream) {
+    return fellm::attention_f32kv_common(q, out, rows, n_heads, n_kv_heads, head_dim, k1, v1, begin1, end1, k2, v2,
+                                         n2, scale, 0, 0, 0, stream);
+}
+
+extern "C" int fellm_rocm_attention_f32kv_rows(const float *q, float *out, uint32_t query_len, uint32_t n_heads,
+                                               uint32_t n_kv_heads, uint32_t head_dim, const float *k,
+                                               const float *v, uint32_t kv_len, float scale, uint32_t causal,
+                                               uint32_t window, void *stream) {
+    if (query_len == 0) return FELLM_OK;
+    if (causal && kv_len < query_len) return FELLM_ERR_SHAPE;  // the query rows end at the last key
+    if (kv_len == 0) return FELLM_ERR_SHAPE;
+    return fellm::attention_f32kv_common(q, out, query_len, n_heads, n_kv_heads, head_dim, k, v, 0, kv_len, nullptr,
+                                         nullptr, 0, scale, causal ? 1 : 2, window, 1, stream);
 }

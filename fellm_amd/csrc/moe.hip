@@ -494,7 +494,12 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 uint32_t *g_scratch_ptr[kMaxDevices];
 
-// Device address of `scratch` on the current device, looked up once per device.
+// Device address of `scratch` on the current device, looked up once per device
+// and kept for the life of the process.  The cache assumes the device is not
+// reset and the library not unloaded in between: after hipDeviceReset the
+// array's allocation is gone and a cached address would be stale, so a caller
+// that resets a device must not call the allocation-free entry point again in
+// that process.
 static_assert(kDispatchScratchWords == (uint64_t)kMaxDispatchBlocks * kMoeMaxExperts,
               "the scratch buffer holds the per-block counts of the largest dispatch grid");
 

@@ -70,6 +70,10 @@ struct Mirror {
     void *dev = nullptr;
     size_t bytes = 0;
     bool device_valid = false;
+    // While !device_valid: bytes [0, valid_prefix) of the device copy already
+    // equal the host's (an input read row by row, such as a K/V buffer that
+    // grows by one row per decode step, uploads only the rows it lacks).
+    size_t valid_prefix = 0;
 };
 
 struct State {
@@ -142,6 +146,8 @@ void ensure_capacity(Mirror &m, size_t bytes) {
     if (m.dev) hip_check(hipFree(m.dev));
     m.dev = nullptr;
     m.bytes = 0;
+    m.device_valid = false;
+    m.valid_prefix = 0;
     hip_check(hipMalloc(&m.dev, bytes ? bytes : 1));
     m.bytes = bytes;
 }
@@ -178,8 +184,27 @@ void *ensure_input(State &st, const FellmTensorRef &t) {
     Mirror &m = st.act[{reinterpret_cast<uintptr_t>(t.data), (size_t)t.byte_len}];
     if (!m.device_valid) {
         ensure_capacity(m, t.byte_len);
-        upload(st, m.dev, t.data, t.byte_len);
+        upload(st, static_cast<uint8_t *>(m.dev) + m.valid_prefix, static_cast<const uint8_t *>(t.data) + m.valid_prefix,
+               t.byte_len - m.valid_prefix);
         m.device_valid = true;
+        m.valid_prefix = 0;
+    }
+    return m.dev;
+}
+
+// Device address of an activation input of which a launch reads only the
+// first `bytes`: the mirror is keyed by the whole tensor (as every other
+// launch keys it) and only the rows it does not hold yet are uploaded.
+void *ensure_input_prefix(State &st, const FellmTensorRef &t, size_t bytes) {
+    if (!t.data || t.byte_len == 0) fail(FELLM_ERR_ARITY);
+    if (bytes >= t.byte_len || t.logical_id != 0 || find_external(st, t.data, t.byte_len)) return ensure_input(st, t);
+    Mirror &m = st.act[{reinterpret_cast<uintptr_t>(t.data), (size_t)t.byte_len}];
+    if (m.device_valid) return m.dev;
+    ensure_capacity(m, t.byte_len);
+    if (m.valid_prefix < bytes) {
+        upload(st, static_cast<uint8_t *>(m.dev) + m.valid_prefix, static_cast<const uint8_t *>(t.data) + m.valid_prefix,
+               bytes - m.valid_prefix);
+        m.valid_prefix = bytes;
     }
     return m.dev;
 }
@@ -197,6 +222,7 @@ void *ensure_output(State &st, const FellmTensorMut &t, bool inout = false) {
     if (inout && !m.device_valid) upload(st, m.dev, t.data, t.byte_len);
     st.touched_outputs.emplace_back(&m, m.device_valid);
     m.device_valid = false;  // until the launch completes on the stream
+    m.valid_prefix = 0;      // the device copy no longer follows the host's
     return m.dev;
 }
 
@@ -648,22 +674,16 @@ int launch_rope_kv_write(const FellmOpAttrs *attrs, const FellmTensorRef *in, ui
 // when attention_mode == 0.  K/V come from the device arena (f16, or bf16 when
 // cast_to is BF16, as rope_kv_write writes it).  block_size == 0 and the canvas
 // form go to launch_attention_f32kv.
-// A TensorRef for the first `bytes` of t (the rows an attention launch
-// reads), so that only those are mirrored, as the CUDA plugin's slices do.
-FellmTensorRef prefix_ref(const FellmTensorRef &t, size_t bytes) {
-    FellmTensorRef r = t;
-    r.byte_len = bytes;
-    return r;
-}
-
 // The non-paged Attention arms, f32 throughout (as both reference backends
 // read these K/V inputs as f32):
-//  * contiguous decode, block_size == 0 (backend.rs:1371-1397; CUDA
-//    launchers.rs:3719-3760): q is one row, keys 0..past_len of K/V
-//    inputs 1 and 2; a window keeps the last `window` keys when causal
-//    (attention_mode 0) and the first `window` otherwise, as the CPU
-//    backend's FA2-style loop does for one query row
-//    (attention_provider.rs:305-318);
+//  * contiguous, block_size == 0 (backend.rs:1371-1397; CUDA
+//    launchers.rs:3719-3760): query_len rows (default 1) of q, head-major
+//    as the CPU backend's host FA2 path reads them (attention_provider.rs:
+//    251-385), against keys 0..past_len of K/V inputs 1 and 2: causal
+//    (attention_mode 0) up to key past_len + 1 - query_len + row, the last
+//    `window` of those when windowed; otherwise keys within `window` of the
+//    row index (all keys without a window).  One row reduces to the decode
+//    form: the last `window` keys when causal, the first ones otherwise;
 //  * canvas, attention_mode 1 with five inputs (backend.rs:1412-1535; CUDA
 //    launchers.rs:3270-3333): query_len rows, each attending the prefix keys
 //    [past_len - window, past_len) of inputs 1 and 2 and every canvas key of
@@ -678,7 +698,7 @@ void launch_attention_f32kv(State &st, const FellmOpAttrs &a, const FellmTensorR
     const size_t nh = a.n_heads ? a.n_heads : 1, nkv = a.n_kv_heads ? a.n_kv_heads : 1, hd = a.head_dim;
     if (!hd) fail(FELLM_ERR_SHAPE);
     const size_t kvw = nkv * hd, past = a.past_len, window = a.attention_window;
-    const size_t rows = canvas ? (a.query_len ? a.query_len : 1) : 1;
+    const size_t rows = a.query_len ? a.query_len : 1;
     const size_t qn = elems(in[0], FELLM_DTYPE_F32);
     if (qn != rows * nh * hd || elems(out[0], FELLM_DTYPE_F32) != qn) fail(FELLM_ERR_SHAPE);
     size_t b1 = 0, e1 = 0, n_prefix_rows = 0, n2 = 0;
@@ -694,26 +714,40 @@ void launch_attention_f32kv(State &st, const FellmOpAttrs &a, const FellmTensorR
         n_prefix_rows = past;
         n2 = rows;
     } else {
+        // Keys 0..past_len; query_len rows (q and out head-major), causal
+        // with the rows ending at the last key, or windowed around the row
+        // index when not causal (attention_provider.rs:306-318).
         const size_t seq = past + 1;
         if (elems(in[1], FELLM_DTYPE_F32) < seq * kvw || elems(in[2], FELLM_DTYPE_F32) < seq * kvw)
             fail(FELLM_ERR_SHAPE);
-        b1 = 0;
-        e1 = seq;
-        if (window) {
-            if (a.attention_mode == 0) b1 = seq > window ? seq - window : 0;
-            else e1 = window < seq ? window : seq;
-        }
-        n_prefix_rows = seq;
+        const bool causal = a.attention_mode == 0;
+        if (causal && seq < rows) fail(FELLM_ERR_SHAPE);
+        void *q = ensure_input(st, in[0]);
+        void *k = ensure_input_prefix(st, in[1], seq * kvw * 4);
+        void *v = ensure_input_prefix(st, in[2], seq * kvw * 4);
+        void *o = ensure_output(st, out[0]);
+        check(fellm_rocm_attention_f32kv_rows((const float *)q, (float *)o, (uint32_t)rows, (uint32_t)nh,
+                                              (uint32_t)nkv, (uint32_t)hd, (const float *)k, (const float *)v,
+                                              (uint32_t)seq, a.scale, causal ? 1u : 0u, (uint32_t)window,
+                                              stream_ptr(st)));
+        finish_outputs(st, out, 1);
+        return;
     }
     void *q = ensure_input(st, in[0]);
     void *k1 = nullptr, *v1 = nullptr, *k2 = nullptr, *v2 = nullptr;
+    // Only the rows read are uploaded.  The mirrors are keyed by the whole
+    // K/V tensors, so each decode step uploads just the rows appended since
+    // the last one, and _fellm_plugin_invalidate_f32 over the tensor (after a
+    // host rewrite) reaches them.  The CUDA plugin keys a mirror per prefix
+    // slice instead (launchers.rs:3719-3760), which allocates and uploads the
+    // whole prefix again at every step.
     if (n_prefix_rows) {
-        k1 = ensure_input(st, prefix_ref(in[1], n_prefix_rows * kvw * 4));
-        v1 = ensure_input(st, prefix_ref(in[2], n_prefix_rows * kvw * 4));
+        k1 = ensure_input_prefix(st, in[1], n_prefix_rows * kvw * 4);
+        v1 = ensure_input_prefix(st, in[2], n_prefix_rows * kvw * 4);
     }
     if (n2) {
-        k2 = ensure_input(st, prefix_ref(in[3], n2 * kvw * 4));
-        v2 = ensure_input(st, prefix_ref(in[4], n2 * kvw * 4));
+        k2 = ensure_input_prefix(st, in[3], n2 * kvw * 4);
+        v2 = ensure_input_prefix(st, in[4], n2 * kvw * 4);
     }
     void *o = ensure_output(st, out[0]);
     check(fellm_rocm_attention_f32kv((const float *)q, (float *)o, (uint32_t)rows, (uint32_t)nh, (uint32_t)nkv,
@@ -1110,8 +1144,18 @@ void _fellm_plugin_invalidate_f32(const float *ptr, size_t nbytes) {
         if (!ptr || nbytes == 0) return;
         State &st = state();
         std::lock_guard<std::mutex> lock(st.mu);
-        auto it = st.act.find({reinterpret_cast<uintptr_t>(ptr), nbytes});
-        if (it != st.act.end()) it->second.device_valid = false;
+        // Every activation mirror whose host range overlaps the written one
+        // goes stale; a mirror that only followed the host keeps the rows
+        // before the write.
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(ptr), hi = lo + nbytes;
+        for (auto &kv : st.act) {
+            const uintptr_t a = kv.first.first, b = a + kv.first.second;
+            if (b <= lo || a >= hi) continue;
+            Mirror &m = kv.second;
+            const size_t keep = lo > a ? lo - a : 0;
+            m.valid_prefix = m.device_valid ? 0 : (m.valid_prefix < keep ? m.valid_prefix : keep);
+            m.device_valid = false;
+        }
     } catch (...) {
     }
 }

@@ -290,6 +290,21 @@ int fellm_rocm_attention_f32kv(const float *q, float *out, uint32_t rows, uint32
                                const float *k2, const float *v2, uint32_t n2, float scale, void *stream);
 
 /*
+ * Attention of query_len rows over one contiguous f32 K/V pair of kv_len rows,
+ * the CPU backend's host FA2 path for the non-paged Attention launch.
+ *   replaces: backend.rs:1371-1397 -> attention_provider.rs:251-385
+ *             (fa2_style_attention_f32).
+ * q, out: head-major [n_heads, query_len, head_dim]; k, v: [kv_len, n_kv_heads * head_dim].
+ * causal != 0: row i attends keys 0 .. kv_len - query_len + i (the last
+ * `window` of them when window > 0; kv_len >= query_len).  causal == 0: keys
+ * within `window` of i (|i - j| < window), every key when window == 0.
+ * scale <= 0 means 1/sqrt(head_dim).  Softmax exp is the glibc-exact expf.
+ */
+int fellm_rocm_attention_f32kv_rows(const float *q, float *out, uint32_t query_len, uint32_t n_heads,
+                                    uint32_t n_kv_heads, uint32_t head_dim, const float *k, const float *v,
+                                    uint32_t kv_len, float scale, uint32_t causal, uint32_t window, void *stream);
+
+/*
  * Cast: dst = src converted elementwise, n_elems elements.
  *   replaces: launch_cast (crates/backend-cpu/src/backend.rs:1603-1667).
  * Pairs (as the CPU backend): F32->F32, F16->F32, BF16->F32 (exact widening),
@@ -351,7 +366,8 @@ int fellm_rocm_moe_dispatch(const uint32_t *ids, uint64_t tokens, uint32_t top_k
  * on a device looks the array's address up (hipGetSymbolAddress) with that
  * device current.  All calls on one GPU share the array: calls that overlap
  * on one GPU (concurrent streams or host threads) race and must be
- * serialised by the caller.
+ * serialised by the caller.  The looked-up address is kept for the process:
+ * after hipDeviceReset of a device, do not call this entry point on it again.
  */
 uint64_t fellm_rocm_moe_dispatch_noalloc_max_bytes(void);
 int fellm_rocm_moe_dispatch_noalloc(const uint32_t *ids, uint64_t tokens, uint32_t top_k, uint32_t n_experts,

@@ -61,6 +61,7 @@ def lib(path: Path | None = None) -> C.CDLL:
             "oracle_sincosf": (None, [P, P, P, S]),
             "oracle_logf": (None, [P, P, S]),
             "oracle_attention_f32kv": (None, [P, P, S, S, S, S, P, P, S, S, P, P, S, F]),
+            "oracle_fa2_attention_f32": (None, [P, P, P, P, S, S, S, S, S, F, C.c_int, S, S, S]),
             "oracle_get_scale_min_k4": (None, [S, P, P, P]),
             "oracle_row_bytes": (S, [U32, S]),
             "oracle_dequantize_row": (C.c_int, [U32, P, P, S]),
@@ -419,4 +420,16 @@ def attention_f32kv(q: np.ndarray, n_heads: int, n_kv: int, head_dim: int, k1, v
     vb = _c(v2, np.float32) if v2 is not None else np.zeros(1, np.float32)
     lib().oracle_attention_f32kv(_p(q), _p(out), rows, n_heads, n_kv, head_dim, _p(ka), _p(va), b1, e1, _p(kb),
                                  _p(vb), n2, scale)
+    return out
+
+
+def fa2_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, n_heads: int, n_kv: int, head_dim: int,
+                  query_len: int, kv_len: int, scale: float, causal: bool, window: int = 0,
+                  q_tile: int = 16, kv_tile: int = 16) -> np.ndarray:
+    """The CPU backend's host FA2 attention (attention_provider.rs:251-385): q and the result
+    head-major [n_heads, query_len, head_dim]; k, v [kv_len, n_kv * head_dim]."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    out = np.zeros(n_heads * query_len * head_dim, np.float32)
+    lib().oracle_fa2_attention_f32(_p(q), _p(k), _p(v), _p(out), n_heads, n_kv, head_dim, query_len, kv_len, scale,
+                                   int(causal), window, q_tile, kv_tile)
     return out

@@ -539,6 +539,91 @@ void oracle_attention_f32kv(const float *q, float *out, size_t rows, size_t n_he
     free(sc);
 }
 
+/* Contiguous-K/V attention with query_len rows, the CPU backend's default
+ * host path (backend.rs:1385-1391 -> attention_provider.rs:251-385,
+ * fa2_style_attention_f32): q and out head-major ([h][qi][d]), K/V rows
+ * [kj][kv_h][d]; query blocks of br rows, key tiles of bc keys (the dispatch
+ * defaults 16/16 raised to at least 4/16, backend.rs:1278-1279).  Causal:
+ * key kj <= kv_len - query_len + qi, and within `window` of that bound when
+ * window > 0; not causal with window > 0: |qi - kj| < window.  Per tile: the
+ * max of the finite scores, alpha = exp(m - m_new) rescales out and l, then
+ * p = exp(s - m_new) accumulates into out (key order) and a tile sum added to l. */
+void oracle_fa2_attention_f32(const float *q, const float *k, const float *v, float *out, size_t n_heads,
+                              size_t n_kv_heads, size_t hd, size_t query_len, size_t kv_len, float scale, int causal,
+                              size_t window, size_t q_tile, size_t kv_tile) {
+    const size_t n_kv = n_kv_heads ? n_kv_heads : 1;
+    size_t group = n_heads / n_kv;
+    if (!group) group = 1;
+    const size_t br = q_tile ? q_tile : 1, bc = kv_tile ? kv_tile : 1;
+    float *m = (float *)malloc(br * sizeof(float)), *l = (float *)malloc(br * sizeof(float));
+    float *scores = (float *)malloc(bc * sizeof(float));
+    for (size_t h = 0; h < n_heads; ++h) {
+        const size_t kv_h = h / group;
+        for (size_t q0 = 0; q0 < query_len; q0 += br) {
+            const size_t q1 = q0 + br < query_len ? q0 + br : query_len;
+            for (size_t i = 0; i < q1 - q0; ++i) {
+                m[i] = -INFINITY;
+                l[i] = 0.0f;
+                memset(out + (h * query_len + q0 + i) * hd, 0, hd * sizeof(float));
+            }
+            for (size_t k0 = 0; k0 < kv_len; k0 += bc) {
+                const size_t k1 = k0 + bc < kv_len ? k0 + bc : kv_len;
+                for (size_t qi = q0; qi < q1; ++qi) {
+                    const size_t li = qi - q0;
+                    const float *qr = q + (h * query_len + qi) * hd;
+                    float *orow = out + (h * query_len + qi) * hd;
+                    for (size_t kj = k0; kj < k1; ++kj) {
+                        scores[kj - k0] = -INFINITY;
+                        if (causal) {
+                            const size_t max_k = kv_len - query_len + qi;
+                            if (kj > max_k) continue;
+                            if (window > 0 && max_k - kj >= window) continue;
+                        } else if (window > 0) {
+                            const size_t dist = qi > kj ? qi - kj : kj - qi;
+                            if (dist >= window) continue;
+                        }
+                        const float *kr = k + (kj * n_kv + kv_h) * hd;
+                        float sc = 0.0f;
+                        for (size_t d = 0; d < hd; ++d) sc += qr[d] * kr[d];
+                        scores[kj - k0] = sc * scale;
+                    }
+                    float mt = -INFINITY;
+                    for (size_t j = 0; j < k1 - k0; ++j)
+                        if (isfinite(scores[j]) && scores[j] > mt) mt = scores[j];
+                    if (!isfinite(mt)) continue;
+                    const float mn = mt > m[li] ? mt : m[li];
+                    const float alpha = isfinite(m[li]) ? expf(m[li] - mn) : 0.0f;
+                    if (alpha != 1.0f) {
+                        for (size_t d = 0; d < hd; ++d) orow[d] *= alpha;
+                        l[li] *= alpha;
+                    }
+                    float lt = 0.0f;
+                    for (size_t kj = k0; kj < k1; ++kj) {
+                        const float sc = scores[kj - k0];
+                        if (!isfinite(sc)) continue;
+                        const float p = expf(sc - mn);
+                        lt += p;
+                        const float *vr = v + (kj * n_kv + kv_h) * hd;
+                        for (size_t d = 0; d < hd; ++d) orow[d] += p * vr[d];
+                    }
+                    l[li] += lt;
+                    m[li] = mn;
+                }
+            }
+            for (size_t qi = q0; qi < q1; ++qi) {
+                if (l[qi - q0] > 0.0f) {
+                    const float inv = 1.0f / l[qi - q0];
+                    float *orow = out + (h * query_len + qi) * hd;
+                    for (size_t d = 0; d < hd; ++d) orow[d] *= inv;
+                }
+            }
+        }
+    }
+    free(m);
+    free(l);
+    free(scores);
+}
+
 /* ---- next: quantized gate/up GEMV with the SwiGLU epilogue ---------------
  * backend.rs:944-1002 (launch_gate_up_swiglu) -> matmul.rs:404-531
  * (matvec_quant_multi: x quantized once to Q8_K, every row of gate then up

@@ -190,3 +190,40 @@ def test_attention_f32kv_empty_and_errors(ops):
                                           None, None, 0, 0.0, s) == -2  # heads not a multiple of KV heads
     assert lib.fellm_rocm_attention_f32kv(x.data_ptr(), x.data_ptr(), 1, 32, 1, 128, x.data_ptr(), x.data_ptr(), 0,
                                           1, None, None, 0, 0.0, s) == -2  # 32 heads per KV head
+
+
+@pytest.mark.parametrize("ql,kvl,causal,window", [(1, 37, True, 0), (5, 37, True, 0), (16, 16, True, 0),
+                                                  (20, 300, True, 8), (7, 33, False, 0), (9, 40, False, 5),
+                                                  (33, 33, True, 1), (64, 1000, True, 0), (3, 2, False, 4)])
+def test_attention_f32kv_rows(ops, ql, kvl, causal, window):
+    """query_len rows over contiguous f32 K/V (the CPU backend's host FA2 path,
+    attention_provider.rs:251-385): head-major q and out, the causal bound
+    kv_len - query_len + row and its window, or the non-causal row window;
+    against the oracle's restatement of that path."""
+    from fellm_amd import _lib
+
+    rng = np.random.default_rng(ql * 1000 + kvl + window)
+    nh, nkv, hd = 16, 4, 128
+    q = rng.normal(size=nh * ql * hd).astype(np.float32)
+    k = rng.normal(size=(kvl, nkv * hd)).astype(np.float32)
+    v = rng.normal(size=(kvl, nkv * hd)).astype(np.float32)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    dev = torch.device("cuda:0")
+    qd, kd, vd = (torch.from_numpy(a).to(dev) for a in (q, k, v))
+    out = torch.full_like(qd, float("nan"))
+    rc = _lib.lib().fellm_rocm_attention_f32kv_rows(qd.data_ptr(), out.data_ptr(), ql, nh, nkv, hd, kd.data_ptr(),
+                                                    vd.data_ptr(), kvl, 0.0, int(causal), window,
+                                                    torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, rc
+    got = out.cpu().numpy()
+    ref = oracle.fa2_attention(q, k, v, nh, nkv, hd, ql, kvl, scale, causal, window)
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(v).max() + np.abs(ref).max() * 2.0 ** -23
+
+
+def test_attention_f32kv_rows_rejects_more_rows_than_keys(ops):
+    from fellm_amd import _lib
+
+    x = torch.zeros(4096, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    assert _lib.lib().fellm_rocm_attention_f32kv_rows(x.data_ptr(), x.data_ptr(), 4, 4, 2, 64, x.data_ptr(),
+                                                      x.data_ptr(), 3, 0.0, 1, 0, s) == -2

@@ -464,6 +464,59 @@ def test_attention_contiguous_decode(host, window, mode):
     assert np.abs(got - ref).max() <= 2e-5 * np.abs(v).max() + np.abs(ref).max() * 2.0 ** -23
 
 
+def _contiguous_decode(host, q, k, v, nh, nkv, hd, past):
+    out = np.zeros_like(q)
+    run(host, abi.OpKind.ATTENTION, [D.F32, D.F32, D.F32], D.F32,
+        abi.OpAttrs(n_heads=nh, n_kv_heads=nkv, head_dim=hd, past_len=past, block_size=0),
+        [tref(q, D.F32), tref(k, D.F32), tref(v, D.F32)], [tmut(out, D.F32)])
+    ref = oracle.attention_f32kv(q[None], nh, nkv, hd, k, v, 0, past + 1)[0]
+    got = materialize(host, out, D.F32)
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(v).max() + np.abs(ref).max() * 2.0 ** -23
+
+
+def test_attention_contiguous_decode_follows_host_kv(host):
+    """The K/V mirrors of contiguous decode are keyed by the whole tensors:
+    rows appended by the host between steps are uploaded as the key range
+    grows, and after a host rewrite of rows already read,
+    _fellm_plugin_invalidate_f32 over the tensor makes the next launch read
+    the new values (the same past_len twice, with the rewrite in between)."""
+    rng = np.random.default_rng(77)
+    nh, nkv, hd, cap = 8, 2, 64, 64
+    q = rng.normal(size=nh * hd).astype(np.float32)
+    k = np.zeros((cap, nkv * hd), np.float32)
+    v = np.zeros((cap, nkv * hd), np.float32)
+    for past in range(0, 12):  # decode steps: the host appends row `past`, then attends 0..past
+        k[past] = rng.normal(size=nkv * hd)
+        v[past] = rng.normal(size=nkv * hd)
+        _contiguous_decode(host, q, k, v, nh, nkv, hd, past)
+    k[:12] = rng.normal(size=(12, nkv * hd))
+    v[3] = 10.0 * rng.normal(size=nkv * hd)
+    host.invalidate(k.ctypes.data, k.nbytes)
+    host.invalidate(v.ctypes.data + 3 * v.itemsize * nkv * hd, v.itemsize * nkv * hd)  # one row of v
+    _contiguous_decode(host, q, k, v, nh, nkv, hd, 11)
+
+
+@pytest.mark.parametrize("ql,mode,window", [(6, 0, 0), (6, 0, 4), (5, 1, 3)])
+def test_attention_contiguous_query_rows(host, ql, mode, window):
+    """Contiguous Attention with query_len > 1 rows: q and out head-major, the
+    causal mask offset by kv_len - query_len (backend.rs:1385-1391 ->
+    attention_provider.rs:251-385)."""
+    rng = np.random.default_rng(50 + ql + mode + window)
+    nh, nkv, hd, past = 8, 2, 64, 40
+    q = rng.normal(size=nh * ql * hd).astype(np.float32)
+    k = rng.normal(size=(48, nkv * hd)).astype(np.float32)
+    v = rng.normal(size=(48, nkv * hd)).astype(np.float32)
+    out = np.zeros_like(q)
+    run(host, abi.OpKind.ATTENTION, [D.F32, D.F32, D.F32], D.F32,
+        abi.OpAttrs(n_heads=nh, n_kv_heads=nkv, head_dim=hd, past_len=past, block_size=0, attention_window=window,
+                    attention_mode=mode, query_len=ql),
+        [tref(q, D.F32), tref(k, D.F32), tref(v, D.F32)], [tmut(out, D.F32)])
+    ref = oracle.fa2_attention(q, k[:past + 1], v[:past + 1], nh, nkv, hd, ql, past + 1,
+                               float(np.float32(1 / np.sqrt(hd))), mode == 0, window)
+    got = materialize(host, out, D.F32)
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(v).max() + np.abs(ref).max() * 2.0 ** -23
+
+
 def test_attention_canvas(host):
     """Attention [F32 x 5] in canvas mode (attention_mode 1): query_len rows,
     each attending the prefix keys [past - window, past) of inputs 1, 2 and

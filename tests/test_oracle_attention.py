@@ -210,3 +210,67 @@ def test_attention_f32kv_closed_forms_and_segments():
     assert np.array_equal(two, cat)
     scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
     assert np.abs(two - _f64_attention(q, nh, nkv, hd, k[4:], v[4:], scale)).max() < 2e-6 * np.abs(v).max()
+
+
+def _masked_softmax_f64(q, k, v, nh, nkv, hd, ql, kvl, scale, causal, window):
+    """Dense f64 restatement from the mask rules alone (one explicit mask
+    matrix, no tiles or online softmax): q head-major [nh, ql, hd]."""
+    qh = q.reshape(nh, ql, hd).astype(np.float64)
+    kh = k.reshape(kvl, nkv, hd).astype(np.float64)
+    vh = v.reshape(kvl, nkv, hd).astype(np.float64)
+    qi = np.arange(ql)[:, None]
+    kj = np.arange(kvl)[None, :]
+    if causal:
+        bound = kvl - ql + qi
+        allow = kj <= bound
+        if window:
+            allow &= (bound - kj) < window
+    elif window:
+        allow = np.abs(qi - kj) < window
+    else:
+        allow = np.ones((ql, kvl), bool)
+    out = np.zeros((nh, ql, hd))
+    g = nh // nkv
+    for h in range(nh):
+        s = qh[h] @ kh[:, h // g].T * scale
+        s = np.where(allow, s, -np.inf)
+        mx = s.max(axis=1, keepdims=True)
+        e = np.where(allow, np.exp(s - np.where(np.isfinite(mx), mx, 0)), 0.0)
+        den = e.sum(axis=1, keepdims=True)
+        out[h] = np.where(den > 0, (e / np.where(den > 0, den, 1)) @ vh[:, h // g], 0.0)
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("ql,kvl,causal,window", [(1, 37, True, 0), (5, 37, True, 0), (16, 16, True, 0),
+                                                  (20, 70, True, 8), (7, 33, False, 0), (9, 40, False, 5),
+                                                  (33, 33, True, 1)])
+def test_fa2_attention_matches_masked_f64(ql, kvl, causal, window):
+    """The host FA2 restatement against a dense f64 softmax built from the
+    mask rules alone (attention_provider.rs:306-318): causal bound
+    kv_len - query_len + qi with its window, the non-causal |qi - kj| window.
+    A dropped mask term, a wrong offset or a transposed head/row index fails."""
+    rng = np.random.default_rng(ql * 100 + kvl + window)
+    nh, nkv, hd = 8, 2, 32
+    q = rng.normal(size=nh * ql * hd).astype(np.float32)
+    k = rng.normal(size=(kvl, nkv * hd)).astype(np.float32)
+    v = rng.normal(size=(kvl, nkv * hd)).astype(np.float32)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    got = oracle.fa2_attention(q, k, v, nh, nkv, hd, ql, kvl, scale, causal, window)
+    ref = _masked_softmax_f64(q, k, v, nh, nkv, hd, ql, kvl, scale, causal, window)
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(v).max()
+    # Tiles of other sizes reorder the online softmax only.
+    alt = oracle.fa2_attention(q, k, v, nh, nkv, hd, ql, kvl, scale, causal, window, q_tile=4, kv_tile=64)
+    assert np.abs(alt - got).max() <= 2e-5 * np.abs(v).max()
+
+
+def test_fa2_attention_one_row_equals_decode_oracle():
+    """query_len 1, causal: the decode form (keys 0..kv_len) of the two-pass oracle."""
+    rng = np.random.default_rng(5)
+    nh, nkv, hd, kvl = 16, 4, 64, 90
+    q = rng.normal(size=nh * hd).astype(np.float32)
+    k = rng.normal(size=(kvl, nkv * hd)).astype(np.float32)
+    v = rng.normal(size=(kvl, nkv * hd)).astype(np.float32)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    got = oracle.fa2_attention(q, k, v, nh, nkv, hd, 1, kvl, scale, True)
+    ref = oracle.attention_f32kv(q[None], nh, nkv, hd, k, v, 0, kvl, scale=scale)[0]
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(v).max()
