@@ -285,6 +285,16 @@ __device__ __forceinline__ uint64_t group_max_u64(uint64_t v) {
     return v;
 }
 
+template <int G>
+__device__ __forceinline__ uint32_t dpp_max_group(uint32_t v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "group size");
+    if constexpr (G >= 16) { const uint32_t o = dpp_u32<0x140>(v); v = o > v ? o : v; }
+    if constexpr (G >= 8) { const uint32_t o = dpp_u32<0x141>(v); v = o > v ? o : v; }
+    if constexpr (G >= 4) { const uint32_t o = dpp_u32<0x4E>(v); v = o > v ? o : v; }
+    if constexpr (G >= 2) { const uint32_t o = dpp_u32<0xB1>(v); v = o > v ? o : v; }
+    return v;
+}
+
 // Block-wide f32 sum; every thread gets the result.  `scratch` holds one
 // float per wave.  Contains __syncthreads, so all threads must call it.
 template <int BLOCK>
@@ -362,6 +372,36 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
     y = __fma_rn(zz, r2, y);
     y = __dmul_rn(y, s);
     return (float)y;
+}
+
+// expf_glibc without branches, for x <= 0 or NaN (softmax's exp(l - max)):
+// the main path runs on x raised to glibc's underflow bound, and the cases
+// glibc treats apart (x below that bound, -inf: 0; NaN: x + x) are selected
+// afterwards.  On this domain glibc's own special cases are exactly these,
+// and every other input takes the same main path, so the results are
+// identical (checked on every non-positive and NaN input).
+__device__ __forceinline__ float expf_glibc_nonpos(float x, const uint64_t *tab) {
+    const float lo = -0x1.9fe368p6f;
+    const float xc = x < lo ? lo : (x != x ? 0.0f : x);
+    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)xc;
+    const double z = InvLn2N * xd;
+    const double kd = __builtin_rint(z);
+    const int32_t ki = (int32_t)kd;
+    const double r = __fma_rn(InvLn2N, xd, -kd);
+    uint64_t t = tab[ki & 31];
+    t += (uint64_t)(int64_t)ki << 47;
+    const double sc = __longlong_as_double((long long)t);
+    const double zz = __fma_rn(C0, r, C1);
+    const double r2 = __dmul_rn(r, r);
+    double y = __fma_rn(C2, r, 1.0);
+    y = __fma_rn(zz, r2, y);
+    y = __dmul_rn(y, sc);
+    const float res = (float)y;
+    return x < lo ? 0.0f : (x != x ? x + x : res);
 }
 
 // ---------------------------------------------------------------------------

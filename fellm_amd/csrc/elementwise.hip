@@ -116,11 +116,14 @@ __global__ __launch_bounds__(kEwBlock) void sincosf_kernel(const float *__restri
 
 __global__ __launch_bounds__(kEwBlock) void mathf_kernel(uint32_t fn, const float *__restrict__ in,
                                                          float *__restrict__ out, uint64_t n) {
+    __shared__ uint64_t tab_lds[32];
+    const uint64_t *tab = stage_expf_table(tab_lds);
     const uint64_t stride = (uint64_t)gridDim.x * kEwBlock;
     for (uint64_t i = (uint64_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += stride)
         out[i] = fn == 0   ? logf_glibc(in[i])
                  : fn == 1 ? sqrtf_rn(in[i])
-                           : __uint_as_float((uint32_t)BF16HW::store(in[i]));  // bf16 bits in the low half
+                 : fn == 2 ? __uint_as_float((uint32_t)BF16HW::store(in[i]))  // bf16 bits in the low half
+                           : expf_glibc_nonpos(in[i], tab);
 }
 
 // Largest bit distance between silu_fast and silu over every f32 g of the
@@ -255,7 +258,7 @@ extern "C" void fellm_rocm_timing_disarm(void) { fellm::g_launch_timing = fellm:
 
 extern "C" int fellm_rocm_mathf(uint32_t fn, const float *in, float *out, uint64_t n, void *stream) {
     using namespace fellm;
-    if (fn > 2) return FELLM_ERR_SHAPE;
+    if (fn > 3) return FELLM_ERR_SHAPE;
     if (n == 0) return FELLM_OK;
     if (!in || !out) return FELLM_ERR_ARITY;
     FELLM_LAUNCH(mathf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), fn, in, out, n);

@@ -1,7 +1,8 @@
 """Exhaustive GPU checks over every 32-bit input pattern.
 
 * the device expf restatement against the host's glibc expf (the libm the
-  reference's f32::exp calls), all 2^32 inputs;
+  reference's f32::exp calls), all 2^32 inputs; the router's branch-free
+  form on every non-positive and NaN input;
 * the device sinf/cosf restatement (RoPE's per-row sin/cos table) against
   the host's glibc sinf and cosf (f32::sin_cos, kernels/rope.rs:46-58), all
   2^32 inputs;
@@ -95,6 +96,26 @@ def test_expf_all_inputs(dev):
 
     _sweep(dev_fn, _host_expf, "expf")
     del buf
+
+
+def test_expf_nonpos_all_inputs(dev):
+    """The router's branch-free expf (softmax arguments l - max <= 0) against
+    glibc expf on every non-positive and NaN input."""
+    from fellm_amd import _lib, ops
+
+    lib = _lib.lib()
+
+    def dev_fn(start):
+        x = torch.from_numpy(_bits(start)).to(dev)
+        out = torch.empty_like(x)
+        assert lib.fellm_rocm_mathf(3, x.data_ptr(), out.data_ptr(), x.numel(),
+                                    torch.cuda.current_stream().cuda_stream) == 0
+        # Positive inputs are outside the domain: they take the general
+        # device expf (itself checked against glibc on every input above).
+        keep = (x <= 0) | torch.isnan(x)
+        return torch.where(keep, out, ops.expf(x)).cpu().numpy()
+
+    _sweep(dev_fn, _host_expf, "expf_nonpos")
 
 
 def test_silu_all_inputs(dev):

@@ -483,6 +483,44 @@ def test_router_topk(ops, dev, n_exp, k, gating, norm, rsf):
     assert_exact(from_dev(w), w_ref, "weights")
 
 
+@pytest.mark.parametrize("gating", [1, 2])
+@pytest.mark.parametrize("n_exp,k", [(128, 8), (128, 5), (256, 8), (64, 4)])
+def test_router_near_ties_and_specials(ops, dev, gating, n_exp, k):
+    """Rows built against the ranking's shortcut (unique 32-bit keys of
+    truncated scores, checked for near-ties): logits one ulp apart at the
+    rank k-1 / k boundary and inside the top k, exact duplicates of the k-th
+    logit at a lower expert id, all-equal rows, -inf / +inf / NaN logits, and
+    logits spread far enough that exp(l - max) falls under 2^-100 (the
+    division's IEEE fallback).  Ids and weights bit-exact against the oracle
+    on every row."""
+    rng = np.random.default_rng(n_exp * 10 + k + gating)
+    tokens = 4099
+    logits = rng.normal(size=(tokens, n_exp)).astype(np.float32)
+    order = np.argsort(-logits, axis=1, kind="stable")
+    for r in range(0, 600, 3):  # one ulp above/below the k-th logit at another expert
+        j_k, j_o = order[r, k - 1], order[r, k + 2]
+        logits[r, j_o] = np.nextafter(logits[r, j_k], np.float32(np.inf if r % 2 else -np.inf))
+    for r in range(1, 600, 3):  # an exact duplicate of the k-th logit
+        logits[r, order[r, k + 1]] = logits[r, order[r, k - 1]]
+    for r in range(2, 600, 3):  # a near-tie inside the top k
+        logits[r, order[r, 1]] = np.nextafter(logits[r, order[r, 0]], np.float32(-np.inf))
+    logits[700] = 1.25
+    logits[701, :5] = -np.inf
+    logits[702, 3] = np.inf
+    logits[703, 7] = np.nan
+    logits[704] *= 80.0  # e down to exp(-600): zero, and below 2^-100
+    logits[705] = np.linspace(-90.0, 0.0, n_exp, dtype=np.float32)
+    logits[706] = -12.0 * np.arange(n_exp, dtype=np.float32)  # selected e down to exp(-84), subnormal
+    logits[707] = -np.float32(60.0) - np.arange(n_exp, dtype=np.float32) / 4  # e around 2^-87 .. 2^-133
+    logits[707, 0] = 0.0
+    ids_ref, w_ref = oracle.router(logits, k, gating, True, 0.0)
+    ids, w = ops.router_topk(torch.from_numpy(logits).to(dev), k, gating_func=gating)
+    got_ids, got_w = from_dev(ids), from_dev(w)
+    assert_exact(got_ids, ids_ref, "ids")
+    nan = np.isnan(w_ref) & np.isnan(got_w)
+    assert_exact(np.where(nan, 0, got_w), np.where(nan, 0, w_ref), "weights")
+
+
 @pytest.mark.parametrize("kind", ["f16", "bf16"])
 @pytest.mark.parametrize("rows", [2051, 8193, 16385])
 def test_rope_many_rows(ops, dev, kind, rows):
