@@ -15,13 +15,13 @@
 // A group of G lanes per token (n_experts <= 512, EPL experts per lane).  exp
 // is the glibc-exact restatement and the denominator is folded serially in
 // expert order lane to lane, so scores, ranking and weights are bit-exact with
-// the CPU.  Ranking, for scores in [0, 1] and k <= G: unique 32-bit keys
-// (truncated score bits, inverted expert id) ordered by max/min sorting
-// networks within a lane and merged across the group's lanes, checked for
-// near-ties; otherwise (and for near-ties) 64-bit keys
-// (total-order(score) << 32 | ~expert) and k group max-reductions pick the
-// winners in rank order, ties resolved towards the lower expert id exactly as
-// the CPU's comparator does.
+// the CPU.  Ranking, for non-negative scores and k <= G: unique 64-bit keys
+// (score bits << 32 | ~expert, whose order is the CPU comparator's: score
+// descending, ties to the lower expert id) held as doubles, ordered by f64
+// max/min sorting networks within a lane and merged across the group's lanes.
+// Softmax ranks the exps before the denominator is known and re-sorts the
+// winners' quotients.  Otherwise 64-bit keys (total-order(score) << 32 |
+// ~expert) and k group max-reductions pick the winners in rank order.
 #include "common.hpp"
 
 namespace fellm {
@@ -164,69 +164,56 @@ __device__ __forceinline__ void rank_top8(const K (&a)[EPL], uint32_t k, K (&L)[
     else below = dpp_max_group<G>(below);
 }
 
+// Keys (hi, lo) as doubles for the networks: see kmax.
+constexpr uint32_t kHiBias = 0x00100000u;
+__device__ __forceinline__ double dkey(uint32_t hi, uint32_t lo) {
+    return __longlong_as_double((long long)(((uint64_t)(hi + kHiBias) << 32) | lo));
+}
+__device__ __forceinline__ uint32_t dkey_hi(double v) {
+    return (uint32_t)((uint64_t)__double_as_longlong(v) >> 32) - kHiBias;
+}
+__device__ __forceinline__ uint32_t dkey_lo(double v) { return (uint32_t)(uint64_t)__double_as_longlong(v); }
+
 // The k-of-n_exp selection of one token held by its G lanes (scores s of
 // experts e0 .. e0 + EPL - 1 in this lane), the renormalisation and the
-// stores.  s_lds holds EPL floats per thread of the workgroup.
+// stores.
 template <int EPL, int G, bool TRY_FAST = true>
-__device__ __forceinline__ void select_and_store(const float (&s)[EPL], bool scores_unit, uint32_t lane,
-                                                 uint32_t sub, uint32_t token, bool active, uint32_t n_exp,
-                                                 uint32_t k, uint32_t norm, float rsf, uint32_t *__restrict__ ids,
-                                                 float *__restrict__ weights, float *s_lds) {
+__device__ __forceinline__ void select_and_store(const float (&s)[EPL], uint32_t lane, uint32_t sub, uint32_t token,
+                                                 bool active, uint32_t n_exp, uint32_t k, uint32_t norm, float rsf,
+                                                 uint32_t *__restrict__ ids, float *__restrict__ weights) {
     const uint32_t e0 = sub * EPL;
     const float scale = rsf == 0.0f ? 1.0f : rsf;
     if constexpr (TRY_FAST && kFastRank<EPL, G>) {
-        // Scores in [0, 1] (softmax, sigmoid) and k <= G.  Keys: the top
-        // 32 - IDB bits of the score's bit pattern (below 2^30), then the
-        // inverted expert id, so they are unique and max/min networks order
-        // them.  Truncation only confuses scores equal in their kept bits: if
-        // the kept bits strictly decrease along the first k + 1 keys, that
-        // order is exactly the reference's (score desc, expert asc) order of
-        // the top k, because a strict drop in the kept bits is a strict drop
-        // in the score, and every key past rank k lies below rank k - 1 in
-        // kept bits.  Otherwise (a near-tie, or a score outside [0, 1] such
-        // as NaN) the wavefront takes the k-round selection below.
-        constexpr uint32_t CAP = G * EPL, IDB = ilog2_u32(CAP), SH = IDB - 2;
-        if (scores_unit && k <= (uint32_t)G && n_exp <= CAP) {
-            uint32_t a[EPL];
+        // k <= G and every score non-negative and not NaN (softmax, sigmoid,
+        // sqrt-softplus): exact unique keys (score bits, ~expert), whose order
+        // is the reference's (score desc, expert asc), through the networks;
+        // the group's top 8 in every lane.  Otherwise (a NaN, -0.0) the
+        // wavefront takes the k-round selection below.
+        if (k <= (uint32_t)G && n_exp <= (uint32_t)(G * EPL)) {
+            double a[EPL];
             bool bad = false;
 #pragma unroll
             for (int j = 0; j < EPL; ++j) {
                 const uint32_t e = e0 + j, b = __float_as_uint(s[j]);
                 const bool real = active && e < n_exp;
-                bad |= real && b > 0x3F800000u;
-                a[j] = real ? ((b >> SH) << IDB) | (CAP - 1 - e) : 0u;
+                bad |= real && b > 0x7F800000u;
+                a[j] = real && b <= 0x7F800000u ? dkey(b, 0xFFFFFFFFu - e) : 0.0;
             }
-            uint32_t L[8], below;
-            rank_top8<EPL, G, uint32_t>(a, k, L, below);
-            bool tie = false;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                if ((uint32_t)i < k) {
-                    const uint32_t nx = (uint32_t)i + 1 < k ? L[i + 1 < 8 ? i + 1 : 7] : below;
-                    tie |= (L[i] >> IDB) == (nx >> IDB);
-                }
-            }
-            const uint64_t gmask = ((1ull << G) - 1) << (lane - sub);
-            const bool ok = !tie && (__ballot(bad) & gmask) == 0;
-            if (__ballot(active && !ok) == 0) {
+            double L[8], below;
+            rank_top8<EPL, G, double>(a, k, L, below);
+            if (__ballot(active && bad) == 0) {
                 // Rank r goes to lane r of the group; every lane sums the k
                 // selected raw scores in rank order, as finish_selected does.
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) s_lds[threadIdx.x * EPL + j] = s[j];
-                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                const float *ts = s_lds + (threadIdx.x - sub) * EPL;  // the token's scores by expert
                 float sum = 0.0f, mine = 0.0f;
                 uint32_t my_e = 0;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     if ((uint32_t)i < k) {
-                        const uint32_t e = CAP - 1 - (L[i] & (CAP - 1));
-                        const float v = ts[e];
+                        const float v = __uint_as_float(dkey_hi(L[i]));
                         sum += v;
                         if ((uint32_t)i == sub) {
                             mine = v;
-                            my_e = e;
+                            my_e = 0xFFFFFFFFu - dkey_lo(L[i]);
                         }
                     }
                 }
@@ -348,7 +335,6 @@ __global__ __launch_bounds__(kRouterBlock) void router_topk_grouped(
     const float *__restrict__ logits, uint32_t tokens, uint32_t n_exp, uint32_t k, uint32_t gating,
     uint32_t norm, float rsf, uint32_t *__restrict__ ids, float *__restrict__ weights) {
     __shared__ uint64_t tab_lds[32];
-    __shared__ float s_lds[kRouterBlock * EPL];
     const uint64_t *tab = stage_expf_table(tab_lds);
     constexpr int TPW = kWave / G;  // tokens per wavefront
     const uint32_t lane = threadIdx.x % kWave, sub = lane % G;
@@ -414,8 +400,7 @@ __global__ __launch_bounds__(kRouterBlock) void router_topk_grouped(
         d = __shfl(d, G - 1, G);  // the last lane of the group holds the full fold
         if (d > 0.0f) divide_by(s, d);
     }
-    select_and_store<EPL, G>(s, gating == 1 || gating == 2, lane, sub, token, active, n_exp, k, norm, rsf, ids,
-                             weights, s_lds);
+    select_and_store<EPL, G>(s, lane, sub, token, active, n_exp, k, norm, rsf, ids, weights);
 }
 
 // Softmax with n_experts == G * EPL (every lane full), logits rows 16-byte
@@ -464,11 +449,6 @@ __global__ __launch_bounds__(kRouterBlock) void router_softmax_lean(
     // (score, ~expert), and a tie between rank k - 1 and the next key (which
     // could let an expert outside the k in) sends the wavefront to the
     // k-round selection on the full scores, as do NaN scores and k > G.
-    // Keys as doubles (see kmax): high word e's bits + 2^20.
-    constexpr uint32_t kHiBias = 0x00100000u;
-    auto dkey = [](uint32_t hi, uint32_t lo) {
-        return __longlong_as_double((long long)(((uint64_t)(hi + kHiBias) << 32) | lo));
-    };
     double L[8], below = 0.0;
     bool bad = false;
     if constexpr (kFastRank<EPL, G>) {
@@ -505,17 +485,15 @@ __global__ __launch_bounds__(kRouterBlock) void router_softmax_lean(
             const float q0 = e * y;
             return __builtin_fmaf(__builtin_fmaf(-d, q0, e), y, q0);
         };
-        auto hi_of = [](double v) { return (uint32_t)((uint64_t)__double_as_longlong(v) >> 32) - kHiBias; };
-        auto lo_of = [](double v) { return (uint32_t)(uint64_t)__double_as_longlong(v); };
         double sk[8];  // keys (score bits, ~expert) of ranks 0..k-1, 0 past k
         float e_last = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float e = __uint_as_float(hi_of(L[i]));
+            const float e = __uint_as_float(dkey_hi(L[i]));
             if ((uint32_t)i + 1 == k) e_last = e;
-            sk[i] = (uint32_t)i < k ? dkey(__float_as_uint(quot(e)), lo_of(L[i])) : 0.0;
+            sk[i] = (uint32_t)i < k ? dkey(__float_as_uint(quot(e)), dkey_lo(L[i])) : 0.0;
         }
-        const float e_next = below == 0.0 ? 0.0f : __uint_as_float(hi_of(below));
+        const float e_next = below == 0.0 ? 0.0f : __uint_as_float(dkey_hi(below));
         const float s_next = e_next >= 0x1p-100f ? quot(e_next) : e_next / d;
         // Every winner's e at least 2^-100 (the last one decides), so the
         // quotient sequence holds for all of them.
@@ -532,11 +510,11 @@ __global__ __launch_bounds__(kRouterBlock) void router_softmax_lean(
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 if ((uint32_t)i < k) {
-                    const float v = __uint_as_float(hi_of(sk[i]));
+                    const float v = __uint_as_float(dkey_hi(sk[i]));
                     sum += v;
                     if ((uint32_t)i == sub) {
                         mine = v;
-                        my_e = 0xFFFFFFFFu - lo_of(sk[i]);
+                        my_e = 0xFFFFFFFFu - dkey_lo(sk[i]);
                     }
                 }
             }
@@ -560,7 +538,7 @@ __global__ __launch_bounds__(kRouterBlock) void router_softmax_lean(
     } else if (d > 0.0f) {
         divide_by(s, d);
     }
-    select_and_store<EPL, G, false>(s, true, lane, sub, token, active, E, k, norm, rsf, ids, weights, nullptr);
+    select_and_store<EPL, G, false>(s, lane, sub, token, active, E, k, norm, rsf, ids, weights);
 }
 
 }  // namespace
