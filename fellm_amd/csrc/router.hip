@@ -488,18 +488,21 @@ __global__ __launch_bounds__(kRouterBlock) void router_softmax_lean(
         double sk[8];  // keys (score bits, ~expert) of ranks 0..k-1, 0 past k
         float e_last = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < 8; ++i) {  // branch-free: every rank's quotient, then selects
             const float e = __uint_as_float(dkey_hi(L[i]));
-            if ((uint32_t)i + 1 == k) e_last = e;
-            sk[i] = (uint32_t)i < k ? dkey(__float_as_uint(quot(e)), dkey_lo(L[i])) : 0.0;
+            const double key = dkey(__float_as_uint(quot(e)), dkey_lo(L[i]));
+            e_last = (uint32_t)i + 1 == k ? e : e_last;
+            sk[i] = (uint32_t)i < k ? key : 0.0;
         }
         const float e_next = below == 0.0 ? 0.0f : __uint_as_float(dkey_hi(below));
-        const float s_next = e_next >= 0x1p-100f ? quot(e_next) : e_next / d;
         // Every winner's e at least 2^-100 (the last one decides), so the
-        // quotient sequence holds for all of them.
+        // quotient sequence holds for all of them.  Below 2^-100 the next
+        // key's quotient is not formed: rank k - 1 at least 2^-99 puts every
+        // later quotient strictly under it (a factor of 2 survives rounding).
         const float s_last = quot(e_last);
+        const bool boundary = e_next >= 0x1p-100f ? s_last > quot(e_next) : e_last >= 0x1p-99f;
         const uint64_t gmask = ((1ull << G) - 1) << (lane - sub);
-        const bool ok = k <= (uint32_t)G && quot_ok && e_last >= 0x1p-100f && s_last > s_next &&
+        const bool ok = k <= (uint32_t)G && quot_ok && e_last >= 0x1p-100f && boundary &&
                         (__ballot(bad) & gmask) == 0;
         if (__ballot(active && !ok) == 0) {
             sort8_desc(sk);
