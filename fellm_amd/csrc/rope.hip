@@ -48,6 +48,11 @@
 #define FELLM_ROPE_WAVES 8
 #endif
 // Build knob: (row, head) slots each thread loads before rotating/storing.
+// Build knob: 16-bit items kept packed in registers between load and
+// rotation in the fast slot walk (1) or widened to f32 at the load (0).
+#ifndef FELLM_ROPE_RAW
+#define FELLM_ROPE_RAW 1
+#endif
 #ifndef FELLM_ROPE_UNROLL
 #define FELLM_ROPE_UNROLL 3
 #endif
@@ -290,14 +295,53 @@ __device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typenam
         return h < nh1 ? (size_t)(row0 + r) * w1 + (size_t)h * head_dim
                        : (size_t)(row0 + r) * w2 + (size_t)(h - nh1) * head_dim;
     };
+    // 16-bit activations stay packed between the loads and the rotation
+    // (2 elements per register): a batch of U items then holds half the
+    // registers, which keeps the row-group walk at 8 waves per SIMD without
+    // spilling (bf16 needs more temporaries than f16 for its rounding).
+    constexpr bool RAW = sizeof(T) == 2 && FELLM_ROPE_RAW;
+    constexpr int RW = RAW ? (int)sizeof(T) * PV / 4 : 1;  // 32-bit words per run
     for (; slot < total_slots; slot += step * U) {
-        float e[U][2 * PV];
+        float e[RAW ? 1 : U][2 * PV];
+        uint32_t raw[RAW ? U : 1][2 * RW];
         uint32_t srr[U], sh[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t h = h0 + hd;
             srr[u] = rr;
             sh[u] = h;
+            if constexpr (RAW) {
+                if (slot + u * step < total_slots) {
+                    const T *src = (h < nh1 ? x1 : x2) + slot_off(rr, h);
+                    const uint32_t *pa = reinterpret_cast<const uint32_t *>(src + lo);
+                    const uint32_t *pb = reinterpret_cast<const uint32_t *>(src + (KIND == kRopeSplit ? hi : lo + PV));
+                    if constexpr (RW == 2 && KIND != kRopeSplit) {  // one 16-byte run
+                        const uint4 a = *reinterpret_cast<const uint4 *>(pa);
+                        raw[u][0] = a.x;
+                        raw[u][1] = a.y;
+                        raw[u][2] = a.z;
+                        raw[u][3] = a.w;
+                    } else if constexpr (RW == 2) {
+                        const uint2 a = *reinterpret_cast<const uint2 *>(pa), b = *reinterpret_cast<const uint2 *>(pb);
+                        raw[u][0] = a.x;
+                        raw[u][1] = a.y;
+                        raw[u][2] = b.x;
+                        raw[u][3] = b.y;
+                    } else {
+#pragma unroll
+                        for (int w = 0; w < RW; ++w) {
+                            raw[u][w] = pa[w];
+                            raw[u][RW + w] = pb[w];
+                        }
+                    }
+                }
+                hd += step;
+                while (hd >= heads) {
+                    hd -= heads;
+                    ++rr;
+                }
+                continue;
+            }
             if (slot + u * step < total_slots) {
                 const T *src = (h < nh1 ? x1 : x2) + slot_off(rr, h);
                 if constexpr (KIND == kRopeSplit) {
@@ -337,6 +381,12 @@ __device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typenam
             T *dst = (first ? out1 : out2);
             if (!dst) continue;
             dst += off;
+            float (&ev)[2 * PV] = e[RAW ? 0 : u];
+            if constexpr (RAW) {
+#pragma unroll
+                for (int i = 0; i < 2 * PV; ++i)
+                    ev[i] = A::load(__builtin_bit_cast(T, (uint16_t)(raw[u][i / 2] >> (16 * (i % 2)))));
+            }
             if constexpr (KIND == kRopePass) {
                 if (dst == src) continue;  // in place: the span is already there
             } else {
@@ -344,22 +394,22 @@ __device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typenam
                 for (int k = 0; k < PV; ++k) {
                     const float2 sc = R == 1 ? sc1[k] : cs_all[srr[u]][i0 + k];  // (sin, cos)
                     const int ia = KIND == kRopeSplit ? k : 2 * k, ib = KIND == kRopeSplit ? PV + k : 2 * k + 1;
-                    const float a = e[u][ia], b = e[u][ib];
-                    e[u][ia] = a * sc.y - b * sc.x;
-                    e[u][ib] = a * sc.x + b * sc.y;
+                    const float a = ev[ia], b = ev[ib];
+                    ev[ia] = a * sc.y - b * sc.x;
+                    ev[ib] = a * sc.x + b * sc.y;
                 }
             }
             if constexpr (KIND == kRopeSplit) {
                 float a[PV], b[PV];
 #pragma unroll
                 for (int k = 0; k < PV; ++k) {
-                    a[k] = e[u][k];
-                    b[k] = e[u][PV + k];
+                    a[k] = ev[k];
+                    b[k] = ev[PV + k];
                 }
                 act_store<A, PV>(dst + lo, a);
                 act_store<A, PV>(dst + hi, b);
             } else {
-                act_store<A, 2 * PV>(dst + lo, e[u]);
+                act_store<A, 2 * PV>(dst + lo, ev);
             }
         }
     }
