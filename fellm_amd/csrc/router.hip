@@ -32,8 +32,8 @@ namespace {
 #define FELLM_ROUTER_EPL 16
 #endif
 
-// Build knob: the ranking on unique 32-bit keys where it applies (1), or the
-// k-round selection on 64-bit keys for every wavefront (0).
+// Build knob: the sorting-network ranking on unique 64-bit keys where it
+// applies (1), or the k-round selection for every wavefront (0).
 #ifndef FELLM_ROUTER_FAST
 #define FELLM_ROUTER_FAST 1
 #endif
@@ -125,7 +125,7 @@ __device__ __forceinline__ void merge_lanes(K (&l)[8]) {
 
 constexpr uint32_t ilog2_u32(uint32_t v) { return v <= 1 ? 0 : 1 + ilog2_u32(v / 2); }
 
-// Layouts the ranking on 32-bit keys serves.
+// Layouts the sorting-network ranking serves.
 template <int EPL, int G>
 constexpr bool kFastRank = (EPL == 8 || EPL == 16) && G >= 2 && G <= 16 && G * EPL <= 256 && FELLM_ROUTER_FAST;
 
