@@ -35,6 +35,10 @@
 //   row: serial f32 sum over blocks from 0.0.
 // The CPU's SIMD paths for Q4_K/Q5_K (AVX2/VNNI/AVX-512) share the integer
 // parts and reorder only that f32 combine.
+#include <mutex>
+#include <tuple>
+#include <vector>
+
 #include "common.hpp"
 
 // Build knob: workgroups in the grid-stride launch (each quantizes x once).
@@ -42,6 +46,17 @@
 #ifndef FELLM_GEMV_MAX_GRID
 #define FELLM_GEMV_MAX_GRID 512
 #endif
+
+// Build knob: the widest grid for launches with many units per wavefront.
+#ifndef FELLM_GEMV_WIDE_GRID
+#define FELLM_GEMV_WIDE_GRID 768
+#endif
+
+// Build knob: weight units in flight per wavefront (1 or 2 register sets).
+#ifndef FELLM_GEMV_DEPTH
+#define FELLM_GEMV_DEPTH 1
+#endif
+
 
 namespace fellm {
 namespace {
@@ -75,12 +90,22 @@ __device__ __forceinline__ XLds carve_lds(uint8_t *base, uint32_t nb) {
 // quantize_row_q8_k_avx2 (matmul.rs:213-270) for the 256-element blocks of x:
 // wavefront `first` takes blocks first, first + stride, ...; lane l holds
 // elements 4l..4l+3.  xl may point into LDS or global memory.  The x loads of
-// kBatch blocks go out together before any of them is reduced: one memory
-// latency per batch instead of one per block (the per-workgroup prologue of
-// a 14336-column GEMV went from 11 us to ~2 us).
-__device__ __forceinline__ void quantize_block(const float4 v, uint32_t b, const XLds &xl, uint32_t lane) {
+// kXBatch blocks go out together before any of them is reduced, and the
+// batch's amax reductions (DPP inside each 16-lane row, then the four rows'
+// values read as scalars) run side by side: the prologue is a short chain,
+// not one LDS shuffle round trip per reduction step and block.
+// fmaxf ignores a NaN operand, so the reduction order does not change amax.
+__device__ __forceinline__ float block_absmax(const float4 v) {
     float a = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)), fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
-    a = wave_max(a);
+    a = group_max_f32<16>(a);
+    const int ai = __float_as_int(a);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(ai, 0)), r1 = __int_as_float(__builtin_amdgcn_readlane(ai, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(ai, 32)), r3 = __int_as_float(__builtin_amdgcn_readlane(ai, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ void quantize_block(const float4 v, const float a, uint32_t b, const XLds &xl,
+                                               uint32_t lane) {
     int32_t q[4] = {0, 0, 0, 0};
     if (a != 0.0f) {
         const float iscale = 127.0f / a;
@@ -98,29 +123,44 @@ __device__ __forceinline__ void quantize_block(const float4 v, uint32_t b, const
                             (uint32_t)(q[3] & 0xff) << 24;
     *reinterpret_cast<uint32_t *>(&xl.qs[b * 256 + lane * 4]) = packed;
     int32_t s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, kWave);
-    s += __shfl_xor(s, 2, kWave);
+    s += (int32_t)dpp_u32<0xB1>((uint32_t)s);  // quad xor 1
+    s += (int32_t)dpp_u32<0x4E>((uint32_t)s);  // quad xor 2
     if ((lane & 3) == 0) xl.bs[b * 16 + lane / 4] = (int16_t)s;
     if (lane == 0) xl.d[b] = a / 127.0f;
 }
 
+constexpr int kXBatch = 8;
+
+__device__ __forceinline__ void load_x_batch(const float *__restrict__ x, uint32_t nb, uint32_t b0, uint32_t stride,
+                                             float4 (&v)[kXBatch]) {
+    const uint32_t lane = threadIdx.x % kWave;
+#pragma unroll
+    for (int j = 0; j < kXBatch; ++j) {
+        const uint32_t b = b0 + j * stride;
+        v[j] = b < nb ? *reinterpret_cast<const float4 *>(x + (size_t)b * 256 + lane * 4)
+                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+}
+
+__device__ __forceinline__ void quantize_batch(const float4 (&v)[kXBatch], uint32_t nb, uint32_t b0, uint32_t stride,
+                                               const XLds &xl) {
+    const uint32_t lane = threadIdx.x % kWave;
+    float a[kXBatch];
+#pragma unroll
+    for (int j = 0; j < kXBatch; ++j) a[j] = block_absmax(v[j]);
+#pragma unroll
+    for (int j = 0; j < kXBatch; ++j) {
+        const uint32_t b = b0 + j * stride;
+        if (b < nb) quantize_block(v[j], a[j], b, xl, lane);
+    }
+}
+
 __device__ void quantize_x(const float *__restrict__ x, uint32_t nb, const XLds &xl, uint32_t first,
                            uint32_t stride) {
-    constexpr int kBatch = 8;
-    const uint32_t lane = threadIdx.x % kWave;
-    for (uint32_t b0 = first; b0 < nb; b0 += stride * kBatch) {
-        float4 v[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const uint32_t b = b0 + j * stride;
-            v[j] = b < nb ? *reinterpret_cast<const float4 *>(x + (size_t)b * 256 + lane * 4)
-                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const uint32_t b = b0 + j * stride;
-            if (b < nb) quantize_block(v[j], b, xl, lane);
-        }
+    for (uint32_t b0 = first; b0 < nb; b0 += stride * kXBatch) {
+        float4 v[kXBatch];
+        load_x_batch(x, nb, b0, stride, v);
+        quantize_batch(v, nb, b0, stride, xl);
     }
 }
 
@@ -129,30 +169,74 @@ __device__ void quantize_x(const float *__restrict__ x, uint32_t nb, const XLds 
 __host__ __device__ constexpr uint32_t q8k_blob_bytes(uint32_t nb) { return nb * 292; }
 
 // x into the workgroup's LDS: quantized here (PREQ = false), or copied from a
-// blob that fellm_rocm_quantize_q8k wrote once for the whole launch.
+// blob that fellm_rocm_quantize_q8k wrote once for the whole launch.  In two
+// halves: x_issue requests the thread's first batch of x (or of the blob)
+// into registers, x_finish quantizes (copies) it and the rest.  The kernel
+// issues x before its first weight loads, so that x does not queue behind
+// the weight stream (x is on every wavefront's critical path).
+constexpr int kBlobBatch = 4;
 template <bool PREQ>
-__device__ __forceinline__ void fill_x(const void *__restrict__ xsrc, uint32_t nb, const XLds &xl, uint8_t *smem) {
+struct XFirst {
+    float4 v[kXBatch];
+};
+template <>
+struct XFirst<true> {
+    uint32_t v[kBlobBatch];
+};
+
+template <bool PREQ>
+__device__ __forceinline__ void x_issue(const void *__restrict__ xsrc, uint32_t nb, XFirst<PREQ> &f) {
+    if constexpr (PREQ) {
+        const uint32_t words = q8k_blob_bytes(nb) / 4;
+        const uint32_t *src = static_cast<const uint32_t *>(xsrc);
+#pragma unroll
+        for (int j = 0; j < kBlobBatch; ++j) {
+            const uint32_t i = threadIdx.x + j * blockDim.x;
+            f.v[j] = i < words ? src[i] : 0u;
+        }
+    } else {
+        load_x_batch(static_cast<const float *>(xsrc), nb, threadIdx.x / kWave, kGemvWaves, f.v);
+    }
+}
+
+template <bool PREQ>
+__device__ __forceinline__ void x_finish(const void *__restrict__ xsrc, uint32_t nb, const XLds &xl, uint8_t *smem,
+                                         const XFirst<PREQ> &f) {
     if constexpr (PREQ) {
         const uint32_t words = q8k_blob_bytes(nb) / 4;
         const uint32_t *src = static_cast<const uint32_t *>(xsrc);
         uint32_t *dst = reinterpret_cast<uint32_t *>(smem);
-        constexpr int kBatch = 4;
-        for (uint32_t i0 = threadIdx.x; i0 < words; i0 += blockDim.x * kBatch) {
-            uint32_t v[kBatch];
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
+        for (int j = 0; j < kBlobBatch; ++j) {
+            const uint32_t i = threadIdx.x + j * blockDim.x;
+            if (i < words) dst[i] = f.v[j];
+        }
+        for (uint32_t i0 = threadIdx.x + blockDim.x * kBlobBatch; i0 < words; i0 += blockDim.x * kBlobBatch) {
+            uint32_t v[kBlobBatch];
+#pragma unroll
+            for (int j = 0; j < kBlobBatch; ++j) {
                 const uint32_t i = i0 + j * blockDim.x;
                 v[j] = i < words ? src[i] : 0u;
             }
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
+            for (int j = 0; j < kBlobBatch; ++j) {
                 const uint32_t i = i0 + j * blockDim.x;
                 if (i < words) dst[i] = v[j];
             }
         }
     } else {
-        quantize_x(static_cast<const float *>(xsrc), nb, xl, threadIdx.x / kWave, kGemvWaves);
+        const float *x = static_cast<const float *>(xsrc);
+        const uint32_t first = threadIdx.x / kWave;
+        quantize_batch(f.v, nb, first, kGemvWaves, xl);
+        quantize_x(x, nb, xl, first + kGemvWaves * kXBatch, kGemvWaves);
     }
+}
+
+template <bool PREQ>
+__device__ __forceinline__ void fill_x(const void *__restrict__ xsrc, uint32_t nb, const XLds &xl, uint8_t *smem) {
+    XFirst<PREQ> f;
+    x_issue<PREQ>(xsrc, nb, f);
+    x_finish<PREQ>(xsrc, nb, xl, smem, f);
 }
 
 __device__ __forceinline__ uint4 lds_u4(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
@@ -516,6 +600,16 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *
         }
     };
 
+    // Everything the prologue waits for (x, the exp table) is requested
+    // before the first unit's weights: loads complete in order, so a wait
+    // for a later load would wait for the whole weight burst too.
+    XFirst<PREQ> xf;
+    x_issue<PREQ>(x, nb, xf);
+    uint64_t tab_v = 0;
+    {
+        constexpr ExpfTable T = make_expf_table();
+        if (threadIdx.x < 32) tab_v = T.tab[threadIdx.x];
+    }
     Staged<GW> sg;
     Staged<UW> su;
     uint32_t gb0, gb1, ub0 = 0, ub1 = 0;
@@ -525,11 +619,19 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *
         range(0, urb, UW::kBytes, u_end, ub0, ub1);
         stage_issue(wu, ub0, ub1, lane, su);
     }
-    {
-        constexpr ExpfTable T = make_expf_table();
-        if (threadIdx.x < 32) tab_lds[threadIdx.x] = T.tab[threadIdx.x];
+#if FELLM_GEMV_DEPTH == 2
+    Staged<GW> sg2;
+    Staged<UW> su2;
+    uint32_t gb0b, gb1b, ub0b = 0, ub1b = 0;
+    range(1, grb, GW::kBytes, g_end, gb0b, gb1b);
+    stage_issue(wg, gb0b, gb1b, lane, sg2);
+    if constexpr (FUSED) {
+        range(1, urb, UW::kBytes, u_end, ub0b, ub1b);
+        stage_issue(wu, ub0b, ub1b, lane, su2);
     }
-    fill_x<PREQ>(x, nb, xl, gemv_smem);
+#endif
+    if (threadIdx.x < 32) tab_lds[threadIdx.x] = tab_v;
+    x_finish<PREQ>(x, nb, xl, gemv_smem, xf);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
@@ -541,16 +643,10 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *
     stage_store(stage, lane, sg);
     if constexpr (FUSED) stage_store(ustage, lane, su);
 
-    for (uint32_t n = 0;; ++n) {
+    // Block values of the staged unit n (byte ranges starting at cg0 / cu0),
+    // and after a row's last unit the row folds and the stores.
+    auto work = [&](uint32_t n, uint32_t cg0, uint32_t cu0) {
         const uint32_t row0 = unit_row(n), p = unit_pass(n);
-        if (row0 >= rows) break;
-        const uint32_t cg0 = gb0, cu0 = ub0;  // staged unit's byte ranges start here
-        range(n + 1, grb, GW::kBytes, g_end, gb0, gb1);
-        stage_issue(wg, gb0, gb1, lane, sg);
-        if constexpr (FUSED) {
-            range(n + 1, urb, UW::kBytes, u_end, ub0, ub1);
-            stage_issue(wu, ub0, ub1, lane, su);
-        }
         wave_lds_sync();
         const uint32_t b = MULTI ? 32 * p + slot : bfix;  // block index within its row
         const bool on = MULTI ? b < nb : slot_on;
@@ -580,9 +676,51 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *
             }
             wave_lds_sync();
         }
+    };
+
+#if FELLM_GEMV_DEPTH == 2
+    // Two units in flight: register sets A (sg, su) and B (sg2, su2) take
+    // alternate units; the LDS stage holds the unit being reduced.
+    for (uint32_t n = 0;; n += 2) {
+        if (unit_row(n) >= rows) break;
+        uint32_t cg0 = gb0, cu0 = ub0;
+        range(n + 2, grb, GW::kBytes, g_end, gb0, gb1);
+        stage_issue(wg, gb0, gb1, lane, sg);
+        if constexpr (FUSED) {
+            range(n + 2, urb, UW::kBytes, u_end, ub0, ub1);
+            stage_issue(wu, ub0, ub1, lane, su);
+        }
+        work(n, cg0, cu0);
+        stage_store(stage, lane, sg2);
+        if constexpr (FUSED) stage_store(ustage, lane, su2);
+        if (unit_row(n + 1) >= rows) break;
+        cg0 = gb0b;
+        cu0 = ub0b;
+        range(n + 3, grb, GW::kBytes, g_end, gb0b, gb1b);
+        stage_issue(wg, gb0b, gb1b, lane, sg2);
+        if constexpr (FUSED) {
+            range(n + 3, urb, UW::kBytes, u_end, ub0b, ub1b);
+            stage_issue(wu, ub0b, ub1b, lane, su2);
+        }
+        work(n + 1, cg0, cu0);
         stage_store(stage, lane, sg);
         if constexpr (FUSED) stage_store(ustage, lane, su);
     }
+#else
+    for (uint32_t n = 0;; ++n) {
+        if (unit_row(n) >= rows) break;
+        const uint32_t cg0 = gb0, cu0 = ub0;  // staged unit's byte ranges start here
+        range(n + 1, grb, GW::kBytes, g_end, gb0, gb1);
+        stage_issue(wg, gb0, gb1, lane, sg);
+        if constexpr (FUSED) {
+            range(n + 1, urb, UW::kBytes, u_end, ub0, ub1);
+            stage_issue(wu, ub0, ub1, lane, su);
+        }
+        work(n, cg0, cu0);
+        stage_store(stage, lane, sg);
+        if constexpr (FUSED) stage_store(ustage, lane, su);
+    }
+#endif
 }
 
 // Rows whose bytes do not end on a 16-byte boundary (Q6_K rows of nb % 8 != 0
@@ -636,12 +774,41 @@ __global__ __launch_bounds__(kGemvBlock) void quantize_q8k_kernel(const float *_
     quantize_x(x, nb, xl, blockIdx.x * kGemvWaves + threadIdx.x / kWave, gridDim.x * kGemvWaves);
 }
 
+// Workgroups for `units` row groups (or rows of passes).  Each workgroup
+// quantizes x once, so a launch keeps to FELLM_GEMV_MAX_GRID (512) unless
+// its wavefronts would each get more than two units; then it widens to at
+// most FELLM_GEMV_WIDE_GRID (768), and never past the workgroups that can be
+// resident at once (the LDS stage sets that).  With x already quantized the
+// prologue is a copy, so more workgroups pay off at every size.
+template <bool PREQ, typename K>
+uint32_t gemv_grid(K kernel, uint32_t lds, uint32_t units) {
+    const uint32_t need = (units + kGemvWaves - 1) / kGemvWaves;
+    uint32_t grid = PREQ ? kGemvMaxGridPre : FELLM_GEMV_MAX_GRID;
+    if (!PREQ && units / (2 * kGemvWaves) > grid) {
+        // resident workgroups for this kernel and LDS size, looked up once each
+        static std::mutex mu;
+        static std::vector<std::tuple<const void *, uint32_t, uint32_t>> seen;
+        uint32_t cap = 0;
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            for (const auto &[k, l, c] : seen)
+                if (k == reinterpret_cast<const void *>(kernel) && l == lds) cap = c;
+            if (cap == 0) {
+                cap = resident_grid(kernel, kGemvBlock, lds, 8);
+                seen.emplace_back(reinterpret_cast<const void *>(kernel), lds, cap);
+            }
+        }
+        uint32_t wide = units / (2 * kGemvWaves);
+        if (wide > FELLM_GEMV_WIDE_GRID) wide = FELLM_GEMV_WIDE_GRID;
+        if (wide > cap) wide = cap;
+        if (wide > grid) grid = wide;
+    }
+    return need < grid ? need : grid;
+}
+
 template <typename GW, typename UW, bool FUSED, bool PREQ = false>
 int launch_gemv(const void *gw, const void *uw, const void *x, float *out, uint32_t rows, uint32_t cols,
                 hipStream_t s) {
-    // With x already quantized the prologue is a copy, so more workgroups
-    // (more wavefronts in flight) pay off.
-    const uint32_t max_grid = PREQ ? kGemvMaxGridPre : FELLM_GEMV_MAX_GRID;
     const uint32_t nb = cols / 256;
     const uint32_t mats = FUSED ? 2 : 1;
     const uint32_t nbp = (nb + 3) & ~3u;
@@ -659,15 +826,14 @@ int launch_gemv(const void *gw, const void *uw, const void *x, float *out, uint3
         const uint8_t *u = FUSED ? u8 + (uint64_t)r0 * nb * UW::kBytes : nullptr;
         if (nb <= 32) {
             const uint32_t rp = 32 / nb;
-            uint32_t grid = (n + kGemvWaves * rp - 1) / (kGemvWaves * rp);
-            if (grid > max_grid) grid = max_grid;
             const uint32_t lds = gemv_lds_bytes(nb, mats * rp * nbp) + kGemvWaves * kStagePerWave<GW, UW, FUSED>;
+            const uint32_t units = (n + rp - 1) / rp;
+            const uint32_t grid = gemv_grid<PREQ>(kquant_gemv_kernel<GW, UW, FUSED, false, PREQ>, lds, units);
             FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, false, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
                                out + r0, n, nb, rp);
         } else {
-            uint32_t grid = (n + kGemvWaves - 1) / kGemvWaves;
-            if (grid > max_grid) grid = max_grid;
             const uint32_t lds = gemv_lds_bytes(nb, mats * nbp) + kGemvWaves * kStagePerWave<GW, UW, FUSED>;
+            const uint32_t grid = gemv_grid<PREQ>(kquant_gemv_kernel<GW, UW, FUSED, true, PREQ>, lds, n);
             FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, true, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
                                out + r0, n, nb, 1u);
         }
