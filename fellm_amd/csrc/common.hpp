@@ -194,6 +194,12 @@ __device__ __forceinline__ Pack<T, N> load_pack_nt(const T *p) {
     return pk;
 }
 
+// Raw N-element packs with the default cache policy.
+template <typename T, int N>
+__device__ __forceinline__ Pack<T, N> load_pack(const T *p) {
+    return *reinterpret_cast<const Pack<T, N> *>(p);
+}
+
 template <typename T, int N>
 __device__ __forceinline__ void store_pack_nt(T *p, const Pack<T, N> &pk) {
     constexpr int W = sizeof(Pack<T, N>) / 4;

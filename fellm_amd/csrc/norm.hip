@@ -42,6 +42,16 @@
 // per wavefront; the workgroup's rows share one LDS copy of the weights).
 // Measured at configs[4] (16384 x 2048 bf16, interleaved on one box): 256
 // 25.1-25.2 us, 512 25.1-25.2, 1024 26.8-27.0, 128 27.2-27.6.
+// Build knob: rows per wavefront in the wavefront-per-row layout (each
+// wavefront requests all of its rows before reducing the first).
+#ifndef FELLM_NORM_WAVE_ROWS
+#define FELLM_NORM_WAVE_ROWS 1
+#endif
+// Build knob: the wavefront-per-row layout reads x and r non-temporally (1)
+// or with the default cache policy (0).
+#ifndef FELLM_NORM_WAVE_XNT
+#define FELLM_NORM_WAVE_XNT 1
+#endif
 #ifndef FELLM_NORM_WAVE_BLOCK
 #define FELLM_NORM_WAVE_BLOCK 256
 #endif
@@ -153,26 +163,33 @@ __global__ __launch_bounds__(FELLM_NORM_WAVE_BLOCK) void add_rmsnorm_wave_kernel
     using T = typename A::T;
     constexpr int VEC = 16 / sizeof(T);
     using P = Pack<T, VEC>;
+    constexpr int RW = FELLM_NORM_WAVE_ROWS;
     const uint32_t lane = threadIdx.x % kWave;
-    const uint32_t row = blockIdx.x * (FELLM_NORM_WAVE_BLOCK / kWave) + threadIdx.x / kWave;
-    const bool live = row < rows;
-    const size_t off = (size_t)row * group;
+    const uint32_t row0 = (blockIdx.x * (FELLM_NORM_WAVE_BLOCK / kWave) + threadIdx.x / kWave) * RW;
+    const bool live = row0 < rows;
     const uint32_t nvec = group / VEC;
-    // The row's x and r are requested first: their latency overlaps the
+    // The rows' x and r are requested first: their latency overlaps the
     // weight staging and its barrier.
-    P xv[NCH], rv[ADD ? NCH : 1];
+    P xv[RW][NCH], rv[RW][ADD ? NCH : 1];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const uint32_t i = c * kWave + lane;
-        if (live && i < nvec) {
-            xv[c] = load_pack_nt<T, VEC>(x + off + (size_t)i * VEC);
-            if constexpr (ADD) rv[c] = load_pack_nt<T, VEC>(r + off + (size_t)i * VEC);
+    for (int q = 0; q < RW; ++q) {
+        const size_t off = (size_t)(row0 + q) * group;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t i = c * kWave + lane;
+            if (row0 + q < rows && i < nvec) {
+                xv[q][c] = FELLM_NORM_WAVE_XNT ? load_pack_nt<T, VEC>(x + off + (size_t)i * VEC)
+                                               : load_pack<T, VEC>(x + off + (size_t)i * VEC);
+                if constexpr (ADD)
+                    rv[q][c] = FELLM_NORM_WAVE_XNT ? load_pack_nt<T, VEC>(r + off + (size_t)i * VEC)
+                                                   : load_pack<T, VEC>(r + off + (size_t)i * VEC);
+            }
         }
     }
     if constexpr (FELLM_NORM_WAVE_WLDS) {
-        // The workgroup's four rows share one copy of the weights in LDS
-        // (group floats, at most 8 KB), instead of each wavefront reading
-        // them from the caches.
+        // The workgroup's rows share one copy of the weights in LDS (group
+        // floats, at most 8 KB), instead of each wavefront reading them from
+        // the caches.
         extern __shared__ float4 w_lds4[];
         for (uint32_t i = threadIdx.x; i < group / 4; i += FELLM_NORM_WAVE_BLOCK)
             w_lds4[i] = reinterpret_cast<const float4 *>(w)[i];
@@ -180,35 +197,40 @@ __global__ __launch_bounds__(FELLM_NORM_WAVE_BLOCK) void add_rmsnorm_wave_kernel
         w = reinterpret_cast<const float *>(w_lds4);
     }
     if (!live) return;  // whole wavefronts only: no block-level barrier follows
-    float ss = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const uint32_t i = c * kWave + lane;
-        if (i < nvec) {
+    for (int q = 0; q < RW; ++q) {
+        const size_t off = (size_t)(row0 + q) * group;
+        const bool qlive = row0 + q < rows;
+        float ss = 0.0f;
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                float hv = A::load(xv[c].v[k]);
-                if constexpr (ADD) {
-                    // h is stored in the activation dtype and normalised as stored.
-                    xv[c].v[k] = A::store(hv + A::load(rv[c].v[k]));
-                    hv = A::load(xv[c].v[k]);
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t i = c * kWave + lane;
+            if (qlive && i < nvec) {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) {
+                    float hv = A::load(xv[q][c].v[k]);
+                    if constexpr (ADD) {
+                        // h is stored in the activation dtype and normalised as stored.
+                        xv[q][c].v[k] = A::store(hv + A::load(rv[q][c].v[k]));
+                        hv = A::load(xv[q][c].v[k]);
+                    }
+                    ss += hv * hv;
                 }
-                ss += hv * hv;
+                if constexpr (STORE_H) store_pack_nt<T, VEC>(h + off + (size_t)i * VEC, xv[q][c]);
             }
-            if constexpr (STORE_H) store_pack_nt<T, VEC>(h + off + (size_t)i * VEC, xv[c]);
         }
-    }
-    ss = wave_sum(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)group + eps);
+        ss = wave_sum(ss);
+        const float scale = 1.0f / sqrtf(ss / (float)group + eps);
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const uint32_t i = c * kWave + lane;
-        if (i < nvec) {
-            float wv[VEC], o[VEC];
-            load_f32<F32, VEC>(w + (size_t)i * VEC, wv);
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t i = c * kWave + lane;
+            if (qlive && i < nvec) {
+                float wv[VEC], o[VEC];
+                load_f32<F32, VEC>(w + (size_t)i * VEC, wv);
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) o[k] = (A::load(xv[c].v[k]) * scale) * wv[k];
-            store_f32_nt<O, VEC>(y + off + (size_t)i * VEC, o);
+                for (int k = 0; k < VEC; ++k) o[k] = (A::load(xv[q][c].v[k]) * scale) * wv[k];
+                store_f32_nt<O, VEC>(y + off + (size_t)i * VEC, o);
+            }
         }
     }
 }
@@ -218,7 +240,7 @@ int launch_wave(const void *x, const void *r, void *h, const float *w, void *y, 
                 float eps, hipStream_t s) {
     using TA = typename A::T;
     using TO = typename O::T;
-    constexpr uint32_t RPB = FELLM_NORM_WAVE_BLOCK / kWave;  // rows per workgroup
+    constexpr uint32_t RPB = FELLM_NORM_WAVE_BLOCK / kWave * FELLM_NORM_WAVE_ROWS;  // rows per workgroup
     const dim3 grid((uint32_t)((rows + RPB - 1) / RPB)), block(FELLM_NORM_WAVE_BLOCK);
     const size_t wl = FELLM_NORM_WAVE_WLDS ? (size_t)group * sizeof(float) : 0;
     if (r == nullptr) {
