@@ -19,6 +19,7 @@
 // K row and the V row are also rounded once to the cache dtype and written
 // into their paged slots, so K never makes an extra HBM round trip.
 #include <initializer_list>
+#include <type_traits>
 
 #include "common.hpp"
 #include "norm_body.hpp"
@@ -52,6 +53,14 @@
 // rotation in the fast slot walk (1) or widened to f32 at the load (0).
 #ifndef FELLM_ROPE_RAW
 #define FELLM_ROPE_RAW 1
+#endif
+// Build knob: bf16 outputs through the hardware conversion with a NaN
+// fallback per lane (1), or the integer rounding for every element (0).
+// Measured interleaved on one box: configs[4] RoPE 57.3 against 55.4 us
+// (the bf16 row-group walk then spills a register), the configs[3] decode
+// step 16.8-17.0 against 17.3-17.4 us; kept off.
+#ifndef FELLM_ROPE_BF16_HW
+#define FELLM_ROPE_BF16_HW 0
 #endif
 #ifndef FELLM_ROPE_UNROLL
 #define FELLM_ROPE_UNROLL 3
@@ -110,8 +119,28 @@ __device__ __forceinline__ void act_load(const typename A::T *p, float (&v)[N]) 
     if constexpr (FELLM_ROPE_NT & 1) load_f32_nt<A, N>(p, v); else load_f32<A, N>(p, v);
 }
 
+// bf16 outputs: a lane whose values are all non-NaN converts them with the
+// hardware (v_cvt_pk_bf16_f32, round to nearest even: the integer rounding's
+// result for every non-NaN f32, checked exhaustively on the device); a lane
+// with a NaN takes the integer path, which keeps the NaN's payload bits.
+// One compare per element instead of the per-element NaN select.
 template <typename A, int N>
 __device__ __forceinline__ void act_store(typename A::T *p, const float (&v)[N]) {
+    if constexpr (std::is_same_v<A, BF16> && FELLM_ROPE_BF16_HW && N % 2 == 0) {
+        bool nan = false;
+#pragma unroll
+        for (int i = 0; i < N; ++i) nan |= v[i] != v[i];
+        if (!nan) {
+            Pack<uint16_t, N> pk;
+#pragma unroll
+            for (int i = 0; i < N; ++i) pk.v[i] = __builtin_bit_cast(uint16_t, (__bf16)v[i]);
+            if constexpr (FELLM_ROPE_NT & 2)
+                store_pack_nt<uint16_t, N>(p, pk);
+            else
+                *reinterpret_cast<Pack<uint16_t, N> *>(p) = pk;
+            return;
+        }
+    }
     if constexpr (FELLM_ROPE_NT & 2) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
 }
 
