@@ -2,6 +2,8 @@
 // reductions, bit-exact glibc expf, launch bookkeeping.
 #pragma once
 
+#include <type_traits>
+
 // Build knob: BF16HW stores through the hardware conversion (1) or integer
 // rounding (0); both round to nearest even.
 #ifndef FELLM_BF16_HW
@@ -15,6 +17,12 @@
 
 #include "fellm_abi.h"
 #include "fellm_rocm.h"
+
+// Build knob: the bf16 SwiGLU interval test rounds both ends with one packed
+// hardware conversion (1) or through the output type's store (0).
+#ifndef FELLM_SILU_BF16_PK
+#define FELLM_SILU_BF16_PK 1
+#endif
 
 // Bit distance bound of silu_fast; kept equal to the measured maximum.
 #ifndef FELLM_SILU_FAST_DIST
@@ -646,15 +654,30 @@ __device__ __forceinline__ float silu_fast(float g) {
 // monotone), and so does its 16-bit rounding, which therefore equals O::store
 // of either end when those agree.  Returns false (out unset) otherwise, and
 // outside the fast domain.
+// bf16 outputs (BF16, BF16HW): with u not NaN neither end product is NaN (s
+// is finite and nonzero on the fast domain), so both ends are rounded by one
+// v_cvt_pk_bf16_f32, which equals the integer rounding for every non-NaN
+// f32; a NaN u takes the exact path.
 template <typename O>
 __device__ __forceinline__ bool silu_mul_fast(float g, float u, typename O::T &out) {
     static_assert(sizeof(typename O::T) == 2, "the interval test needs a 16-bit output");
-    if (!silu_fast_domain(g)) return false;
-    const uint32_t b = __float_as_uint(silu_fast(g));
-    const typename O::T lo = O::store(__uint_as_float(b - kSiluFastDist) * u);
-    const typename O::T hi = O::store(__uint_as_float(b + kSiluFastDist) * u);
-    out = lo;
-    return __builtin_bit_cast(uint16_t, lo) == __builtin_bit_cast(uint16_t, hi);
+    if constexpr (std::is_base_of_v<BF16, O> && FELLM_SILU_BF16_PK) {
+        if (!silu_fast_domain(g) || u != u) return false;
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const uint32_t b = __float_as_uint(silu_fast(g));
+        const f32x2 ends = {__uint_as_float(b - kSiluFastDist) * u, __uint_as_float(b + kSiluFastDist) * u};
+        const uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(ends, bf16x2));
+        out = (typename O::T)(r & 0xffffu);
+        return (r & 0xffffu) == (r >> 16);
+    } else {
+        if (!silu_fast_domain(g)) return false;
+        const uint32_t b = __float_as_uint(silu_fast(g));
+        const typename O::T lo = O::store(__uint_as_float(b - kSiluFastDist) * u);
+        const typename O::T hi = O::store(__uint_as_float(b + kSiluFastDist) * u);
+        out = lo;
+        return __builtin_bit_cast(uint16_t, lo) == __builtin_bit_cast(uint16_t, hi);
+    }
 }
 
 // Copies the 32-entry table into LDS once per block; returns the LDS pointer.

@@ -134,6 +134,24 @@ def test_silu_gate_rounding_boundaries(ops, dev, kind):
     assert_exact(got, oracle.narrow(p, kind), f"silu_gate {kind} near rounding midpoints")
 
 
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+def test_silu_gate_16bit_specials(ops, dev, kind):
+    """16-bit SwiGLU over every pair of special gates and ups: signed zeros,
+    tiny and boundary gates of the fast domain (|g| in [2^-100, 64)), +-inf,
+    NaN, and ups that are NaN, infinite or large enough to overflow the
+    product.  The fast interval decides only non-NaN ups; everything else
+    takes the exact path.  Bit-exact against the oracle, NaN bits included."""
+    gs = np.array([0.0, -0.0, 1e-30, -1e-30, 2.0 ** -99, -(2.0 ** -99), 1.0, -1.0, 3.5, -3.5, 63.9, -63.9,
+                   64.0, -64.0, 100.0, -100.0, np.inf, -np.inf, np.nan], np.float32)
+    big = 60000.0 if kind == "f16" else 3e38
+    us = np.array([0.0, -0.0, 1.5, -1.5, big, -big, np.inf, -np.inf, np.nan], np.float32)
+    g32, u32 = (a.ravel() for a in np.meshgrid(gs, us, indexing="ij"))
+    g, u = oracle.narrow(g32, kind), oracle.narrow(u32, kind)
+    ref = oracle.narrow(oracle.silu_gate(oracle.widen(g, kind), oracle.widen(u, kind)), kind)
+    got = from_dev(ops.silu_gate(to_dev(g, kind, dev), to_dev(u, kind, dev)))
+    assert_exact(got, ref, f"silu_gate {kind} specials")
+
+
 def test_silu_gate_unaligned_and_extremes(ops, dev):
     g = np.array([0.0, -0.0, 100.0, -100.0, 20.0, -20.0, 88.0, -88.0, 1e-30, np.inf, -np.inf, 3.5], np.float32)
     u = np.full_like(g, 1.5)
