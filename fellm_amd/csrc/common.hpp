@@ -18,10 +18,10 @@
 #include "fellm_abi.h"
 #include "fellm_rocm.h"
 
-// Build knob: the bf16 SwiGLU interval test rounds both ends with one packed
-// hardware conversion (1) or through the output type's store (0).
-#ifndef FELLM_SILU_BF16_PK
-#define FELLM_SILU_BF16_PK 1
+// Build knob: the 16-bit SwiGLU interval test rounds both ends with one
+// packed hardware conversion (1) or through the output type's store (0).
+#ifndef FELLM_SILU_PK
+#define FELLM_SILU_PK 1
 #endif
 
 // Bit distance bound of silu_fast; kept equal to the measured maximum.
@@ -654,21 +654,40 @@ __device__ __forceinline__ float silu_fast(float g) {
 // monotone), and so does its 16-bit rounding, which therefore equals O::store
 // of either end when those agree.  Returns false (out unset) otherwise, and
 // outside the fast domain.
-// bf16 outputs (BF16, BF16HW): with u not NaN neither end product is NaN (s
+// Two f32 values rounded to nearest-even f16 by one v_cvt_pk_f16_f32 (a in
+// the low half); equal to the scalar conversion for every non-NaN f32
+// (checked exhaustively on the device).
+__device__ __forceinline__ uint32_t f16_pack_bits(float a, float b) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+__device__ __forceinline__ uint32_t bf16_pack_bits(float a, float b) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// 16-bit outputs (F16, BF16, BF16HW): with u not NaN neither end product is NaN (s
 // is finite and nonzero on the fast domain), so both ends are rounded by one
-// v_cvt_pk_bf16_f32, which equals the integer rounding for every non-NaN
-// f32; a NaN u takes the exact path.
+// packed conversion (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32), which equals
+// the output type's rounding for every non-NaN f32; a NaN u takes the exact
+// path.
 template <typename O>
 __device__ __forceinline__ bool silu_mul_fast(float g, float u, typename O::T &out) {
     static_assert(sizeof(typename O::T) == 2, "the interval test needs a 16-bit output");
-    if constexpr (std::is_base_of_v<BF16, O> && FELLM_SILU_BF16_PK) {
+    constexpr bool kBf = std::is_base_of_v<BF16, O>, kF16 = std::is_same_v<O, F16>;
+    if constexpr ((kBf || kF16) && FELLM_SILU_PK) {
         if (!silu_fast_domain(g) || u != u) return false;
-        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-        typedef float f32x2 __attribute__((ext_vector_type(2)));
         const uint32_t b = __float_as_uint(silu_fast(g));
-        const f32x2 ends = {__uint_as_float(b - kSiluFastDist) * u, __uint_as_float(b + kSiluFastDist) * u};
-        const uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(ends, bf16x2));
-        out = (typename O::T)(r & 0xffffu);
+        float lo = __uint_as_float(b - kSiluFastDist) * u, hi = __uint_as_float(b + kSiluFastDist) * u;
+        // Pin the f32 products (see F16::store): a mixed-precision FMA would
+        // round the exact product straight to 16 bits.
+        __asm__("" : "+v"(lo), "+v"(hi));
+        const uint32_t r = kBf ? bf16_pack_bits(lo, hi) : f16_pack_bits(lo, hi);
+        out = __builtin_bit_cast(typename O::T, (uint16_t)(r & 0xffffu));
         return (r & 0xffffu) == (r >> 16);
     } else {
         if (!silu_fast_domain(g)) return false;

@@ -123,6 +123,7 @@ __global__ __launch_bounds__(kEwBlock) void mathf_kernel(uint32_t fn, const floa
         out[i] = fn == 0   ? logf_glibc(in[i])
                  : fn == 1 ? sqrtf_rn(in[i])
                  : fn == 2 ? __uint_as_float((uint32_t)BF16HW::store(in[i]))  // bf16 bits in the low half
+                 : fn == 4 ? __uint_as_float(f16_pack_bits(in[i], in[i]) & 0xffffu)  // f16 bits, low half
                            : expf_glibc_nonpos(in[i], tab);
 }
 
@@ -258,7 +259,7 @@ extern "C" void fellm_rocm_timing_disarm(void) { fellm::g_launch_timing = fellm:
 
 extern "C" int fellm_rocm_mathf(uint32_t fn, const float *in, float *out, uint64_t n, void *stream) {
     using namespace fellm;
-    if (fn > 3) return FELLM_ERR_SHAPE;
+    if (fn > 4) return FELLM_ERR_SHAPE;
     if (n == 0) return FELLM_OK;
     if (!in || !out) return FELLM_ERR_ARITY;
     FELLM_LAUNCH(mathf_kernel, dim3(ew_grid(n)), dim3(kEwBlock), 0, as_stream(stream), fn, in, out, n);

@@ -13,6 +13,9 @@
 * the bf16 activation store (round to nearest even, quiet NaN with its top
   payload bits) against the oracle's rounding, all 2^32 inputs, bits exact
   including NaNs;
+* the packed f16 conversion of the 16-bit SwiGLU interval test against the
+  oracle's f16 rounding, every non-NaN input (the test never converts a NaN:
+  a NaN up takes the exact path);
 * SwiGLU's silu(g) = g / (1 + exp(-g)) (kernels/swiglu.rs:5-7) through the
   product kernel with up = 1, against the oracle, all 2^32 values of g.
   silu depends on g alone, so this proves the kernel's exp + division path
@@ -156,6 +159,29 @@ def test_sqrtf_all_inputs(dev):
         return ops.sqrtf(torch.from_numpy(_bits(start)).to(dev)).cpu().numpy()
 
     _sweep(dev_fn, _host_sqrtf, "sqrtf")
+
+
+def _host_f16_nonnan(start: int) -> np.ndarray:
+    x = _bits(start)
+    out = oracle.f32_to_f16_bits(x).astype(np.uint32)
+    out[np.isnan(x)] = 0
+    return out.view(np.float32)
+
+
+def test_f16_pack_all_inputs(dev):
+    from fellm_amd import _lib
+
+    lib = _lib.lib()
+
+    def dev_fn(start):
+        x = torch.from_numpy(_bits(start)).to(dev)
+        out = torch.empty_like(x)
+        assert lib.fellm_rocm_mathf(4, x.data_ptr(), out.data_ptr(), x.numel(),
+                                    torch.cuda.current_stream().cuda_stream) == 0
+        out = torch.where(torch.isnan(x), torch.zeros_like(out), out)
+        return out.cpu().numpy()
+
+    _sweep(dev_fn, _host_f16_nonnan, "f16 packed conversion")
 
 
 def test_bf16_store_all_inputs(dev):
