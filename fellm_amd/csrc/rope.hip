@@ -62,6 +62,10 @@
 #ifndef FELLM_ROPE_BF16_HW
 #define FELLM_ROPE_BF16_HW 0
 #endif
+// The same for the RoPE + K/V append launches (q outputs and cache slots).
+#ifndef FELLM_ROPE_BF16_HW_KV
+#define FELLM_ROPE_BF16_HW_KV 1
+#endif
 #ifndef FELLM_ROPE_UNROLL
 #define FELLM_ROPE_UNROLL 3
 #endif
@@ -108,10 +112,43 @@ __device__ __forceinline__ uint64_t kv_slot_offset(const KvDev &kv, uint32_t row
     return base;
 }
 
-template <typename C, int N>
+// bf16 stores through the hardware: a lane whose values are all non-NaN
+// converts them with v_cvt_pk_bf16_f32 (round to nearest even: the integer
+// rounding's result for every non-NaN f32, checked exhaustively on the
+// device); a lane with a NaN takes the integer path, which keeps the NaN's
+// payload bits.  One compare per element instead of the per-element NaN
+// select.  HW = false (or a non-bf16 type): the type's own rounding.
+template <typename A, int N, bool NT, bool HW>
+__device__ __forceinline__ void store16(typename A::T *p, const float (&v)[N]) {
+    if constexpr (HW && std::is_same_v<A, BF16> && N % 2 == 0) {
+        bool nan = false;
+        uint32_t w[N / 2];
+#pragma unroll
+        for (int i = 0; i < N; i += 2) {
+            nan |= (v[i] != v[i]) | (v[i + 1] != v[i + 1]);
+            w[i / 2] = bf16_pack_bits(v[i], v[i + 1]);
+        }
+        if (!nan) {
+            uint32_t *dst = reinterpret_cast<uint32_t *>(p);
+#pragma unroll
+            for (int i = 0; i < N / 2; ++i) {
+                if constexpr (NT)
+                    __builtin_nontemporal_store(w[i], dst + i);
+                else
+                    dst[i] = w[i];
+            }
+        } else {
+            if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
+        }
+    } else {
+        if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
+    }
+}
+
+template <typename C, int N, bool HW = false>
 __device__ __forceinline__ void store_cache(uint8_t *arena, uint64_t byte_off, uint32_t elem,
                                             const float (&v)[N]) {
-    store_f32<C, N>(reinterpret_cast<typename C::T *>(arena + byte_off) + elem, v);
+    store16<C, N, false, HW>(reinterpret_cast<typename C::T *>(arena + byte_off) + elem, v);
 }
 
 template <typename A, int N>
@@ -119,29 +156,9 @@ __device__ __forceinline__ void act_load(const typename A::T *p, float (&v)[N]) 
     if constexpr (FELLM_ROPE_NT & 1) load_f32_nt<A, N>(p, v); else load_f32<A, N>(p, v);
 }
 
-// bf16 outputs: a lane whose values are all non-NaN converts them with the
-// hardware (v_cvt_pk_bf16_f32, round to nearest even: the integer rounding's
-// result for every non-NaN f32, checked exhaustively on the device); a lane
-// with a NaN takes the integer path, which keeps the NaN's payload bits.
-// One compare per element instead of the per-element NaN select.
-template <typename A, int N>
+template <typename A, int N, bool HW = (FELLM_ROPE_BF16_HW != 0)>
 __device__ __forceinline__ void act_store(typename A::T *p, const float (&v)[N]) {
-    if constexpr (std::is_same_v<A, BF16> && FELLM_ROPE_BF16_HW && N % 2 == 0) {
-        bool nan = false;
-#pragma unroll
-        for (int i = 0; i < N; ++i) nan |= v[i] != v[i];
-        if (!nan) {
-            Pack<uint16_t, N> pk;
-#pragma unroll
-            for (int i = 0; i < N; ++i) pk.v[i] = __builtin_bit_cast(uint16_t, (__bf16)v[i]);
-            if constexpr (FELLM_ROPE_NT & 2)
-                store_pack_nt<uint16_t, N>(p, pk);
-            else
-                *reinterpret_cast<Pack<uint16_t, N> *>(p) = pk;
-            return;
-        }
-    }
-    if constexpr (FELLM_ROPE_NT & 2) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
+    store16<A, N, (FELLM_ROPE_NT & 2) != 0, HW>(p, v);
 }
 
 // Element offset, within its head, of item `it`'s first run and of its
@@ -269,10 +286,11 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
     }
     const bool write = dst && (dst != src || it < n_rot);
     const bool cache = MODE == 1 && second && kbase != ~0ull;
+    constexpr bool HW = MODE == 1 ? FELLM_ROPE_BF16_HW_KV != 0 : FELLM_ROPE_BF16_HW != 0;
     if (hi == lo + PV) {
-        if (write) act_store<A, 2 * PV>(dst + base + lo, e);
+        if (write) act_store<A, 2 * PV, HW>(dst + base + lo, e);
         if constexpr (MODE == 1)
-            if (cache) store_cache<C, 2 * PV>(kv.arena, kbase, h * head_dim + lo, e);
+            if (cache) store_cache<C, 2 * PV, HW>(kv.arena, kbase, h * head_dim + lo, e);
     } else {
         float a[PV], b[PV];
 #pragma unroll
@@ -281,13 +299,13 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
             b[k] = e[PV + k];
         }
         if (write) {
-            act_store<A, PV>(dst + base + lo, a);
-            act_store<A, PV>(dst + base + hi, b);
+            act_store<A, PV, HW>(dst + base + lo, a);
+            act_store<A, PV, HW>(dst + base + hi, b);
         }
         if constexpr (MODE == 1) {
             if (cache) {
-                store_cache<C, PV>(kv.arena, kbase, h * head_dim + lo, a);
-                store_cache<C, PV>(kv.arena, kbase, h * head_dim + hi, b);
+                store_cache<C, PV, HW>(kv.arena, kbase, h * head_dim + lo, a);
+                store_cache<C, PV, HW>(kv.arena, kbase, h * head_dim + hi, b);
             }
         }
     }

@@ -416,9 +416,13 @@ def test_kv_write_paged(ops, dev, kv_kind, act):
     assert_exact(arena.cpu().numpy(), ref, "arena")
 
 
-@pytest.mark.parametrize("kind,kv_kind", [("bf16", "bf16"), ("f32", "f16"), ("f16", "f16")])
+@pytest.mark.parametrize("kind,kv_kind,specials", [("bf16", "bf16", False), ("bf16", "bf16", True),
+                                                   ("f32", "f16", False), ("f16", "f16", False)])
 @pytest.mark.parametrize("pairing", [0, 1])
-def test_rope_kv_write_fused(ops, dev, kind, kv_kind, pairing):
+def test_rope_kv_write_fused(ops, dev, kind, kv_kind, specials, pairing):
+    """specials: NaNs with payloads in V (stored unrotated, so their bits must
+    survive the cache store: bf16 stores take the integer path for a lane
+    holding a NaN) and infinities in rotated q and k elements."""
     from fellm_amd import synth
     from fellm_amd.ops import PagedKvCache
 
@@ -431,6 +435,9 @@ def test_rope_kv_write_fused(ops, dev, kind, kv_kind, pairing):
     q = random_stored(rng, (batch, nq * hd), kind)
     k = random_stored(rng, (batch, stride), kind)
     v = random_stored(rng, (batch, stride), kind)
+    if specials:
+        v[3, 5], v[4, 9], v[4, 200] = 0x7FE1, 0xFFC3, 0x7FC0
+        k[2, 0], q[1, 2], q[6, 77] = 0x7F80, 0xFF80, 0x7F80
     bb, arena = _cache(dev, n_blocks, bs, stride, kv_kind)
     cache = PagedKvCache(arena, torch.from_numpy(table.view(np.int32)).to(dev), 1, n_logical, bs, bb, stride,
                          KINDS[kv_kind])
