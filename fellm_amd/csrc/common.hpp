@@ -670,6 +670,38 @@ __device__ __forceinline__ uint32_t bf16_pack_bits(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
+// N f32 values (N even) rounded to bf16 as N/2 packed words, element 2i in
+// the low half of word i: the packed hardware conversion when the lane holds
+// no NaN (equal to BF16::store for every non-NaN f32), else BF16::store per
+// element (a NaN keeps its top payload bits, quiet bit set).  One compare
+// per element instead of BF16::store's per-element NaN select.
+template <int N>
+__device__ __forceinline__ void bf16_round_words(const float (&v)[N], uint32_t (&w)[N / 2]) {
+    static_assert(N % 2 == 0, "pairs");
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+        nan |= (v[i] != v[i]) | (v[i + 1] != v[i + 1]);
+        w[i / 2] = bf16_pack_bits(v[i], v[i + 1]);
+    }
+    if (nan) {
+#pragma unroll
+        for (int i = 0; i < N; i += 2)
+            w[i / 2] = (uint32_t)BF16::store(v[i]) | (uint32_t)BF16::store(v[i + 1]) << 16;
+    }
+}
+
+template <int W>
+__device__ __forceinline__ void store_words(uint32_t *dst, const uint32_t (&w)[W], bool nt) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+        if (nt)
+            __builtin_nontemporal_store(w[i], dst + i);
+        else
+            dst[i] = w[i];
+    }
+}
+
 // 16-bit outputs (F16, BF16, BF16HW): with u not NaN neither end product is NaN (s
 // is finite and nonzero on the fast domain), so both ends are rounded by one
 // packed conversion (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32), which equals

@@ -229,7 +229,7 @@ __global__ __launch_bounds__(FELLM_NORM_WAVE_BLOCK) void add_rmsnorm_wave_kernel
                 load_f32<F32, VEC>(w + (size_t)i * VEC, wv);
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) o[k] = (A::load(xv[q][c].v[k]) * scale) * wv[k];
-                store_f32_nt<O, VEC>(y + off + (size_t)i * VEC, o);
+                norm_store<O, VEC, true>(y + off + (size_t)i * VEC, o);
             }
         }
     }

@@ -7,6 +7,8 @@
 // sumsq = sum(h^2), scale = 1 / sqrt(sumsq / group + eps), y = (h * scale) * w.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 #ifndef FELLM_NORM_W_EARLY
@@ -25,9 +27,45 @@ template <typename A, int N>
 __device__ __forceinline__ void norm_load(const typename A::T *p, float (&v)[N]) {
     load_f32_nt<A, N>(p, v);
 }
+// Build knob: bf16 rows rounded by the packed hardware conversion with a
+// per-lane NaN fallback (bf16_round_words) (1), or element by element (0).
+#ifndef FELLM_NORM_BF16_PK
+#define FELLM_NORM_BF16_PK 1
+#endif
+template <typename A>
+constexpr bool kNormPk = FELLM_NORM_BF16_PK && std::is_base_of_v<BF16, A>;
+
 template <typename A, int N, bool NT>
 __device__ __forceinline__ void norm_store(typename A::T *p, const float (&v)[N]) {
-    if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
+    if constexpr (kNormPk<A> && N % 2 == 0) {
+        uint32_t w[N / 2];
+        bf16_round_words<N>(v, w);
+        store_words<N / 2>(reinterpret_cast<uint32_t *>(p), w, NT);
+    } else {
+        if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
+    }
+}
+// h = x + r rounded to the activation type, in place, for VEC values; with
+// STORE the rounded values are also stored (non-temporally) at p.
+template <typename A, int N, bool STORE>
+__device__ __forceinline__ void norm_add_round(float (&v)[N], const float (&r)[N], typename A::T *p) {
+    if constexpr (kNormPk<A> && N % 2 == 0) {
+        float s[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) s[i] = v[i] + r[i];
+        uint32_t w[N / 2];
+        bf16_round_words<N>(s, w);
+#pragma unroll
+        for (int i = 0; i < N; i += 2) {
+            v[i] = __uint_as_float(w[i / 2] << 16);
+            v[i + 1] = __uint_as_float(w[i / 2] & 0xffff0000u);
+        }
+        if constexpr (STORE) store_words<N / 2>(reinterpret_cast<uint32_t *>(p), w, true);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = A::load(A::store(v[i] + r[i]));
+        if constexpr (STORE) norm_store<A, N, true>(p, v);
+    }
 }
 namespace {
 
@@ -60,12 +98,8 @@ __device__ __forceinline__ void add_rmsnorm_row(
         const uint32_t base = (uint32_t)(c * BLOCK + threadIdx.x) * VEC;
         if (base < group) {
             if constexpr (ADD) {
-#pragma unroll
-                for (int i = 0; i < VEC; ++i) {
-                    // h is stored in the activation dtype and normalised as stored.
-                    v[c][i] = A::load(A::store(v[c][i] + rv[c][i]));
-                }
-                if constexpr (STORE_H) norm_store<A, VEC, true>(h + row * group + base, v[c]);
+                // h is stored in the activation dtype and normalised as stored.
+                norm_add_round<A, VEC, STORE_H>(v[c], rv[c], STORE_H ? h + row * group + base : nullptr);
             }
 #pragma unroll
             for (int i = 0; i < VEC; ++i) ss += v[c][i] * v[c][i];
