@@ -181,6 +181,34 @@ def test_add_rmsnorm(ops, dev, kind, rows, group):
     assert_close(from_dev(y), y_ref, kind, what=f"y {kind} {rows}x{group}")
 
 
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+@pytest.mark.parametrize("rows,group", [(6, 2048), (6, 8192), (1030, 4096)])
+def test_add_rmsnorm_specials(ops, dev, kind, rows, group):
+    """16-bit rows holding NaNs with payloads, infinities, sums that overflow
+    the 16-bit type and signed zeros, beside ordinary rows (the row layouts of
+    every size class).  h bit-exact (a lane with a NaN rounds element by
+    element), y NaN exactly where the oracle's is and within tolerance
+    elsewhere."""
+    rng = np.random.default_rng(rows + group)
+    x = random_stored(rng, (rows, group), kind)
+    r = random_stored(rng, (rows, group), kind, sigma=2.0)
+    nan_a, nan_b = (0x7E01, 0xFE07) if kind == "f16" else (0x7FC1, 0xFFC7)
+    inf, big = (0x7C00, 0x7BFF) if kind == "f16" else (0x7F80, 0x7F7F)
+    x[1, 3], x[1, 100], r[2, 7] = nan_a, nan_b, nan_a
+    x[3, 0], r[3, 1] = inf, inf | 0x8000
+    x[4, 5], r[4, 5] = big, big
+    x[5, :], r[5, :] = 0x8000, 0
+    w = rng.normal(1.0, 0.1, size=group).astype(np.float32)
+    h_ref, y_ref = oracle.add_rmsnorm(x, r, w, 1e-5, kind)
+    h, y = ops.add_rmsnorm(to_dev(x, kind, dev), to_dev(r, kind, dev), torch.from_numpy(w).to(dev), 1e-5)
+    assert_exact(from_dev(h), h_ref, f"h {kind} specials")
+    yg, yr = from_dev(y), y_ref
+    wide = lambda a: oracle.widen(a, kind)
+    assert np.array_equal(np.isnan(wide(yg)), np.isnan(wide(yr)))
+    ok = ~np.isnan(wide(yr))
+    assert_close(yg[ok], yr[ok], kind, what=f"y {kind} specials")
+
+
 @pytest.mark.parametrize("kind", ["f32", "bf16"])
 def test_rmsnorm_plain_and_no_h(ops, dev, kind):
     rng = np.random.default_rng(5)
