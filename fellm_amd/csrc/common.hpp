@@ -655,11 +655,12 @@ __device__ __forceinline__ float silu_fast(float g) {
 // of either end when those agree.  Returns false (out unset) otherwise, and
 // outside the fast domain.
 // Two f32 values rounded to nearest-even f16 by one v_cvt_pk_f16_f32 (a in
-// the low half); equal to the scalar conversion for every non-NaN f32
-// (checked exhaustively on the device).
+// the low half); equal to the scalar conversion of F16::store for every f32,
+// NaNs included (checked exhaustively on the device).
 __device__ __forceinline__ uint32_t f16_pack_bits(float a, float b) {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     typedef float f32x2 __attribute__((ext_vector_type(2)));
+    __asm__("" : "+v"(a), "+v"(b));  // keep the f32 roundings (see F16::store)
     const f32x2 v = {a, b};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
 }
@@ -670,25 +671,36 @@ __device__ __forceinline__ uint32_t bf16_pack_bits(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-// N f32 values (N even) rounded to bf16 as N/2 packed words, element 2i in
-// the low half of word i: the packed hardware conversion when the lane holds
-// no NaN (equal to BF16::store for every non-NaN f32), else BF16::store per
-// element (a NaN keeps its top payload bits, quiet bit set).  One compare
+// N f32 values (N even) rounded to the 16-bit type A as N/2 packed words,
+// element 2i in the low half of word i.  f16: the packed conversion, equal
+// to F16::store for every input.  bf16: the packed conversion when the lane
+// holds no NaN (equal to BF16::store for every non-NaN f32), else BF16::store
+// per element (a NaN keeps its top payload bits, quiet bit set): one compare
 // per element instead of BF16::store's per-element NaN select.
+template <typename A, int N>
+__device__ __forceinline__ void round_words(const float (&v)[N], uint32_t (&w)[N / 2]) {
+    static_assert(N % 2 == 0, "pairs");
+    if constexpr (std::is_same_v<A, F16>) {
+#pragma unroll
+        for (int i = 0; i < N; i += 2) w[i / 2] = f16_pack_bits(v[i], v[i + 1]);
+    } else {
+        static_assert(std::is_base_of_v<BF16, A>, "16-bit types");
+        bool nan = false;
+#pragma unroll
+        for (int i = 0; i < N; i += 2) {
+            nan |= (v[i] != v[i]) | (v[i + 1] != v[i + 1]);
+            w[i / 2] = bf16_pack_bits(v[i], v[i + 1]);
+        }
+        if (nan) {
+#pragma unroll
+            for (int i = 0; i < N; i += 2)
+                w[i / 2] = (uint32_t)BF16::store(v[i]) | (uint32_t)BF16::store(v[i + 1]) << 16;
+        }
+    }
+}
 template <int N>
 __device__ __forceinline__ void bf16_round_words(const float (&v)[N], uint32_t (&w)[N / 2]) {
-    static_assert(N % 2 == 0, "pairs");
-    bool nan = false;
-#pragma unroll
-    for (int i = 0; i < N; i += 2) {
-        nan |= (v[i] != v[i]) | (v[i + 1] != v[i + 1]);
-        w[i / 2] = bf16_pack_bits(v[i], v[i + 1]);
-    }
-    if (nan) {
-#pragma unroll
-        for (int i = 0; i < N; i += 2)
-            w[i / 2] = (uint32_t)BF16::store(v[i]) | (uint32_t)BF16::store(v[i + 1]) << 16;
-    }
+    round_words<BF16, N>(v, w);
 }
 
 template <int W>

@@ -123,7 +123,8 @@ __global__ __launch_bounds__(kEwBlock) void mathf_kernel(uint32_t fn, const floa
         out[i] = fn == 0   ? logf_glibc(in[i])
                  : fn == 1 ? sqrtf_rn(in[i])
                  : fn == 2 ? __uint_as_float((uint32_t)BF16HW::store(in[i]))  // bf16 bits in the low half
-                 : fn == 4 ? __uint_as_float(f16_pack_bits(in[i], in[i]) & 0xffffu)  // f16 bits, low half
+                 : fn == 4 ? __uint_as_float((f16_pack_bits(in[i], in[i]) & 0xffffu) |
+                                             (uint32_t)__builtin_bit_cast(uint16_t, F16::store(in[i])) << 16)
                            : expf_glibc_nonpos(in[i], tab);
 }
 

@@ -112,9 +112,11 @@ __global__ __launch_bounds__(BLOCK) void add_rmsnorm_pipe_kernel(const typename 
     for (; row < rows; row += gridDim.x) {
         float hv[NCHUNK][VEC];
 #pragma unroll
-        for (int c = 0; c < NCHUNK; ++c)
+        for (int c = 0; c < NCHUNK; ++c) {
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) hv[c][i] = A::load(A::store(xv[c][i] + rv[c][i]));
+            for (int i = 0; i < VEC; ++i) hv[c][i] = xv[c][i];
+            norm_add_round<A, VEC, false>(hv[c], rv[c], nullptr);
+        }
         const uint32_t next = row + gridDim.x;
         if (next < rows) load_row(next, xv, rv);  // in flight during this row's reduction and stores
         float ss = 0.0f;

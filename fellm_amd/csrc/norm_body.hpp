@@ -27,19 +27,19 @@ template <typename A, int N>
 __device__ __forceinline__ void norm_load(const typename A::T *p, float (&v)[N]) {
     load_f32_nt<A, N>(p, v);
 }
-// Build knob: bf16 rows rounded by the packed hardware conversion with a
-// per-lane NaN fallback (bf16_round_words) (1), or element by element (0).
+// Build knob: 16-bit rows rounded by the packed hardware conversions
+// (round_words) (1), or element by element (0).
 #ifndef FELLM_NORM_BF16_PK
 #define FELLM_NORM_BF16_PK 1
 #endif
 template <typename A>
-constexpr bool kNormPk = FELLM_NORM_BF16_PK && std::is_base_of_v<BF16, A>;
+constexpr bool kNormPk = FELLM_NORM_BF16_PK && (std::is_base_of_v<BF16, A> || std::is_same_v<A, F16>);
 
 template <typename A, int N, bool NT>
 __device__ __forceinline__ void norm_store(typename A::T *p, const float (&v)[N]) {
     if constexpr (kNormPk<A> && N % 2 == 0) {
         uint32_t w[N / 2];
-        bf16_round_words<N>(v, w);
+        round_words<A, N>(v, w);
         store_words<N / 2>(reinterpret_cast<uint32_t *>(p), w, NT);
     } else {
         if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
@@ -54,11 +54,11 @@ __device__ __forceinline__ void norm_add_round(float (&v)[N], const float (&r)[N
 #pragma unroll
         for (int i = 0; i < N; ++i) s[i] = v[i] + r[i];
         uint32_t w[N / 2];
-        bf16_round_words<N>(s, w);
+        round_words<A, N>(s, w);
 #pragma unroll
         for (int i = 0; i < N; i += 2) {
-            v[i] = __uint_as_float(w[i / 2] << 16);
-            v[i + 1] = __uint_as_float(w[i / 2] & 0xffff0000u);
+            v[i] = A::load(__builtin_bit_cast(typename A::T, (uint16_t)(w[i / 2] & 0xffffu)));
+            v[i + 1] = A::load(__builtin_bit_cast(typename A::T, (uint16_t)(w[i / 2] >> 16)));
         }
         if constexpr (STORE) store_words<N / 2>(reinterpret_cast<uint32_t *>(p), w, true);
     } else {

@@ -481,8 +481,9 @@ int fellm_rocm_sincosf(const float *in, float *sin_out, float *cos_out, uint64_t
  * (round to nearest even), its 16 bits returned in the low half of out[i]'s
  * bit pattern; fn 3: the router's branch-free expf for in[i] <= 0 or NaN
  * (other inputs: unspecified); fn 4: in[i] rounded to f16 by the packed
- * conversion the 16-bit SwiGLU interval test uses, its 16 bits in the low
- * half.  Diagnostic only (no counterpart in the reference).
+ * conversion (low half of out[i]'s bits) and by the scalar conversion of the
+ * f16 activation store (high half).  Diagnostic only (no counterpart in the
+ * reference).
  */
 int fellm_rocm_mathf(uint32_t fn, const float *in, float *out, uint64_t n, void *stream);
 
