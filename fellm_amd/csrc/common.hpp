@@ -703,14 +703,41 @@ __device__ __forceinline__ void bf16_round_words(const float (&v)[N], uint32_t (
     round_words<BF16, N>(v, w);
 }
 
+// W packed words stored at dst as 16-byte (or 8-byte) vectors, so that the
+// store is as wide as the activation pack it replaces (dst aligned to the
+// vector size).
 template <int W>
 __device__ __forceinline__ void store_words(uint32_t *dst, const uint32_t (&w)[W], bool nt) {
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t v2 __attribute__((ext_vector_type(2)));
+    if constexpr (W % 4 == 0) {
 #pragma unroll
-    for (int i = 0; i < W; ++i) {
-        if (nt)
-            __builtin_nontemporal_store(w[i], dst + i);
-        else
-            dst[i] = w[i];
+        for (int i = 0; i < W; i += 4) {
+            const v4 x = {w[i], w[i + 1], w[i + 2], w[i + 3]};
+            v4 *d = reinterpret_cast<v4 *>(dst + i);
+            if (nt)
+                __builtin_nontemporal_store(x, d);
+            else
+                *d = x;
+        }
+    } else if constexpr (W % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < W; i += 2) {
+            const v2 x = {w[i], w[i + 1]};
+            v2 *d = reinterpret_cast<v2 *>(dst + i);
+            if (nt)
+                __builtin_nontemporal_store(x, d);
+            else
+                *d = x;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+            if (nt)
+                __builtin_nontemporal_store(w[i], dst + i);
+            else
+                dst[i] = w[i];
+        }
     }
 }
 

@@ -112,34 +112,15 @@ __device__ __forceinline__ uint64_t kv_slot_offset(const KvDev &kv, uint32_t row
     return base;
 }
 
-// bf16 stores through the hardware: a lane whose values are all non-NaN
-// converts them with v_cvt_pk_bf16_f32 (round to nearest even: the integer
-// rounding's result for every non-NaN f32, checked exhaustively on the
-// device); a lane with a NaN takes the integer path, which keeps the NaN's
-// payload bits.  One compare per element instead of the per-element NaN
-// select.  HW = false (or a non-bf16 type): the type's own rounding.
+// 16-bit stores through the packed hardware conversions (round_words: f16
+// always, bf16 for lanes without a NaN, which otherwise round element by
+// element).  HW = false (or an f32 type): the type's own rounding.
 template <typename A, int N, bool NT, bool HW>
 __device__ __forceinline__ void store16(typename A::T *p, const float (&v)[N]) {
-    if constexpr (HW && std::is_same_v<A, BF16> && N % 2 == 0) {
-        bool nan = false;
+    if constexpr (HW && (std::is_same_v<A, BF16> || std::is_same_v<A, F16>) && N % 2 == 0) {
         uint32_t w[N / 2];
-#pragma unroll
-        for (int i = 0; i < N; i += 2) {
-            nan |= (v[i] != v[i]) | (v[i + 1] != v[i + 1]);
-            w[i / 2] = bf16_pack_bits(v[i], v[i + 1]);
-        }
-        if (!nan) {
-            uint32_t *dst = reinterpret_cast<uint32_t *>(p);
-#pragma unroll
-            for (int i = 0; i < N / 2; ++i) {
-                if constexpr (NT)
-                    __builtin_nontemporal_store(w[i], dst + i);
-                else
-                    dst[i] = w[i];
-            }
-        } else {
-            if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
-        }
+        round_words<A, N>(v, w);
+        store_words<N / 2>(reinterpret_cast<uint32_t *>(p), w, NT);
     } else {
         if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
     }
