@@ -60,10 +60,18 @@ __device__ __forceinline__ void silu_gate_blocks(const typename I::T *__restrict
                     // The exact silu runs only for the elements (and only in
                     // the wavefronts) whose rounding the interval leaves open.
                     typename O::T o[VEC];
+                    bool fast[VEC];
+                    bool all = true;
 #pragma unroll
-                    for (int k = 0; k < VEC; ++k)
-                        if (__builtin_expect(!silu_mul_fast<O>(gv[j][k], uv[j][k], o[k]), 0))
-                            o[k] = O::store(silu(gv[j][k], tab) * uv[j][k]);
+                    for (int k = 0; k < VEC; ++k) {
+                        fast[k] = silu_mul_fast<O>(gv[j][k], uv[j][k], o[k]);
+                        all = all && fast[k];
+                    }
+                    if (__builtin_expect(!all, 0)) {
+#pragma unroll
+                        for (int k = 0; k < VEC; ++k)
+                            if (!fast[k]) o[k] = O::store(silu(gv[j][k], tab) * uv[j][k]);
+                    }
                     store_raw_nt<O, VEC>(out + i * VEC, o);
                 } else {
                     float o[VEC];
