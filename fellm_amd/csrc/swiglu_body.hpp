@@ -5,6 +5,8 @@
 //   out[i] = (g / (1 + exp(-g))) * u       (f32, libm expf)
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace fellm {
@@ -59,18 +61,28 @@ __device__ __forceinline__ void silu_gate_blocks(const typename I::T *__restrict
                 if constexpr (FELLM_SWIGLU_FAST && sizeof(typename O::T) == 2 && VEC % 2 == 0) {
                     // The exact silu runs only for the elements (and only in
                     // the wavefronts) whose rounding the interval leaves open.
+                    // bf16: one branch per vector for the exact fallback
+                    // (configs[4] routed 94.6 -> 92.8 us); f16 keeps one per
+                    // element (configs[1] 56.3 against 57.3 us the other way).
                     typename O::T o[VEC];
-                    bool fast[VEC];
-                    bool all = true;
-#pragma unroll
-                    for (int k = 0; k < VEC; ++k) {
-                        fast[k] = silu_mul_fast<O>(gv[j][k], uv[j][k], o[k]);
-                        all = all && fast[k];
-                    }
-                    if (__builtin_expect(!all, 0)) {
+                    if constexpr (std::is_same_v<O, F16>) {
 #pragma unroll
                         for (int k = 0; k < VEC; ++k)
-                            if (!fast[k]) o[k] = O::store(silu(gv[j][k], tab) * uv[j][k]);
+                            if (__builtin_expect(!silu_mul_fast<O>(gv[j][k], uv[j][k], o[k]), 0))
+                                o[k] = O::store(silu(gv[j][k], tab) * uv[j][k]);
+                    } else {
+                        bool fast[VEC];
+                        bool all = true;
+#pragma unroll
+                        for (int k = 0; k < VEC; ++k) {
+                            fast[k] = silu_mul_fast<O>(gv[j][k], uv[j][k], o[k]);
+                            all = all && fast[k];
+                        }
+                        if (__builtin_expect(!all, 0)) {
+#pragma unroll
+                            for (int k = 0; k < VEC; ++k)
+                                if (!fast[k]) o[k] = O::store(silu(gv[j][k], tab) * uv[j][k]);
+                        }
                     }
                     store_raw_nt<O, VEC>(out + i * VEC, o);
                 } else {
