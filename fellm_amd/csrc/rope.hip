@@ -54,13 +54,13 @@
 #ifndef FELLM_ROPE_RAW
 #define FELLM_ROPE_RAW 1
 #endif
-// Build knob: bf16 outputs through the hardware conversion with a NaN
-// fallback per lane (1), or the integer rounding for every element (0).
-// Measured interleaved on one box: configs[4] RoPE 57.3 against 55.4 us
-// (the bf16 row-group walk then spills a register), the configs[3] decode
-// step 16.8-17.0 against 17.3-17.4 us; kept off.
+// Build knob: 16-bit outputs of the prefill walk through the packed
+// hardware conversions (round_words: a bf16 lane holding a NaN rounds
+// element by element) (1), or element by element (0).  Measured interleaved
+// on one box with word-wise non-temporal stores: configs[1] 14.4-14.5
+// against 14.7-14.8 us, configs[4] 54.4-54.7 against 55.0 us.
 #ifndef FELLM_ROPE_BF16_HW
-#define FELLM_ROPE_BF16_HW 0
+#define FELLM_ROPE_BF16_HW 1
 #endif
 // The same for the RoPE + K/V append launches (q outputs and cache slots).
 #ifndef FELLM_ROPE_BF16_HW_KV
@@ -115,12 +115,12 @@ __device__ __forceinline__ uint64_t kv_slot_offset(const KvDev &kv, uint32_t row
 // 16-bit stores through the packed hardware conversions (round_words: f16
 // always, bf16 for lanes without a NaN, which otherwise round element by
 // element).  HW = false (or an f32 type): the type's own rounding.
-template <typename A, int N, bool NT, bool HW>
+template <typename A, int N, bool NT, bool HW, bool WORD_NT = false>
 __device__ __forceinline__ void store16(typename A::T *p, const float (&v)[N]) {
     if constexpr (HW && (std::is_same_v<A, BF16> || std::is_same_v<A, F16>) && N % 2 == 0) {
         uint32_t w[N / 2];
         round_words<A, N>(v, w);
-        store_words<N / 2>(reinterpret_cast<uint32_t *>(p), w, NT);
+        store_words<N / 2, WORD_NT>(reinterpret_cast<uint32_t *>(p), w, NT);
     } else {
         if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
     }
@@ -137,9 +137,11 @@ __device__ __forceinline__ void act_load(const typename A::T *p, float (&v)[N]) 
     if constexpr (FELLM_ROPE_NT & 1) load_f32_nt<A, N>(p, v); else load_f32<A, N>(p, v);
 }
 
-template <typename A, int N, bool HW = (FELLM_ROPE_BF16_HW != 0)>
+// The prefill walk (MODE 0) stores word by word, the append path (MODE 1)
+// as vectors (see store_words).
+template <typename A, int N, bool HW = (FELLM_ROPE_BF16_HW != 0), bool WORD_NT = true>
 __device__ __forceinline__ void act_store(typename A::T *p, const float (&v)[N]) {
-    store16<A, N, (FELLM_ROPE_NT & 2) != 0, HW>(p, v);
+    store16<A, N, (FELLM_ROPE_NT & 2) != 0, HW, WORD_NT>(p, v);
 }
 
 // Element offset, within its head, of item `it`'s first run and of its
@@ -269,7 +271,7 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
     const bool cache = MODE == 1 && second && kbase != ~0ull;
     constexpr bool HW = MODE == 1 ? FELLM_ROPE_BF16_HW_KV != 0 : FELLM_ROPE_BF16_HW != 0;
     if (hi == lo + PV) {
-        if (write) act_store<A, 2 * PV, HW>(dst + base + lo, e);
+        if (write) act_store<A, 2 * PV, HW, MODE != 1>(dst + base + lo, e);
         if constexpr (MODE == 1)
             if (cache) store_cache<C, 2 * PV, HW>(kv.arena, kbase, h * head_dim + lo, e);
     } else {
@@ -280,8 +282,8 @@ __device__ __forceinline__ void rope_finish(const typename A::T *x1, typename A:
             b[k] = e[PV + k];
         }
         if (write) {
-            act_store<A, PV, HW>(dst + base + lo, a);
-            act_store<A, PV, HW>(dst + base + hi, b);
+            act_store<A, PV, HW, MODE != 1>(dst + base + lo, a);
+            act_store<A, PV, HW, MODE != 1>(dst + base + hi, b);
         }
         if constexpr (MODE == 1) {
             if (cache) {
