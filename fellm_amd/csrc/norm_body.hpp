@@ -32,6 +32,11 @@ __device__ __forceinline__ void norm_load(const typename A::T *p, float (&v)[N])
 #ifndef FELLM_NORM_BF16_PK
 #define FELLM_NORM_BF16_PK 1
 #endif
+// Build knob: non-temporal stores of the packed rows word by word (1) or as
+// 16-byte vectors (0).
+#ifndef FELLM_NORM_WORD_NT
+#define FELLM_NORM_WORD_NT 0
+#endif
 template <typename A>
 constexpr bool kNormPk = FELLM_NORM_BF16_PK && (std::is_base_of_v<BF16, A> || std::is_same_v<A, F16>);
 
@@ -40,7 +45,7 @@ __device__ __forceinline__ void norm_store(typename A::T *p, const float (&v)[N]
     if constexpr (kNormPk<A> && N % 2 == 0) {
         uint32_t w[N / 2];
         round_words<A, N>(v, w);
-        store_words<N / 2>(reinterpret_cast<uint32_t *>(p), w, NT);
+        store_words<N / 2, FELLM_NORM_WORD_NT != 0>(reinterpret_cast<uint32_t *>(p), w, NT);
     } else {
         if constexpr (NT) store_f32_nt<A, N>(p, v); else store_f32<A, N>(p, v);
     }
@@ -60,7 +65,7 @@ __device__ __forceinline__ void norm_add_round(float (&v)[N], const float (&r)[N
             v[i] = A::load(__builtin_bit_cast(typename A::T, (uint16_t)(w[i / 2] & 0xffffu)));
             v[i + 1] = A::load(__builtin_bit_cast(typename A::T, (uint16_t)(w[i / 2] >> 16)));
         }
-        if constexpr (STORE) store_words<N / 2>(reinterpret_cast<uint32_t *>(p), w, true);
+        if constexpr (STORE) store_words<N / 2, FELLM_NORM_WORD_NT != 0>(reinterpret_cast<uint32_t *>(p), w, true);
     } else {
 #pragma unroll
         for (int i = 0; i < N; ++i) v[i] = A::load(A::store(v[i] + r[i]));
