@@ -44,6 +44,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 using Rsrc = __amdgpu_buffer_rsrc_t;
 
 constexpr uint32_t kBlockTokens = 16;  // tokens per cache block handled by one MFMA tile
+// A split's partial record per head slot: HD sums, m, l and two unused
+// floats, so that every record starts on a 16-byte boundary.
+constexpr uint32_t kRecTail = 4;
 
 struct PagedGeom {
     const uint8_t *arena;
@@ -385,18 +388,18 @@ __global__ __launch_bounds__(kWave) void paged_decode_kernel(const typename Q::T
         }
     } else {
         // partial record per (b, g, s, head slot): HD sums, then m, l
-        float *rec = part + ((size_t)bg * splits + s) * GM * (HD + 2);
+        float *rec = part + ((size_t)bg * splits + s) * GM * (HD + kRecTail);
         if (grp == 0) {
 #pragma unroll kEpiUnroll
             for (int h = 0; h < GM; ++h) {
                 if ((uint32_t)h < G) {
 #pragma unroll
-                    for (int d = 0; d < DP; ++d) rec[h * (HD + 2) + col * DP + d] = acc[h][d];
+                    for (int d = 0; d < DP; ++d) rec[h * (HD + kRecTail) + col * DP + d] = acc[h][d];
                 }
             }
             if (col < G) {
-                rec[col * (HD + 2) + HD] = m;
-                rec[col * (HD + 2) + HD + 1] = l;
+                rec[col * (HD + kRecTail) + HD] = m;
+                rec[col * (HD + kRecTail) + HD + 1] = l;
             }
         }
     }
@@ -423,8 +426,8 @@ __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine(const fl
     __shared__ float acc_lds[kParts][HD];
     const uint32_t bh = blockIdx.x, h = bh % n_heads, b = bh / n_heads;
     const uint32_t G = n_heads / n_kv, g = h / G, slot = h % G;
-    constexpr uint32_t kRec = GM * (HD + 2);
-    const float *base = part + ((size_t)(b * n_kv + g) * splits) * kRec + slot * (HD + 2);
+    constexpr uint32_t kRec = GM * (HD + kRecTail);
+    const float *base = part + ((size_t)(b * n_kv + g) * splits) * kRec + slot * (HD + kRecTail);
     const uint32_t t = threadIdx.x, d = t % HD, p = t / HD;
     float av[kPer];
 #pragma unroll
@@ -465,12 +468,107 @@ __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine(const fl
     }
 }
 
+// The same combine by one wavefront per (b, query head), for the launches
+// where the 1024-thread form's barriers and width cost more than its work:
+// lanes take the splits for m and l (wavefront reductions, no barrier); for
+// the sums HD/4 lanes cover a record's dims with 16-byte loads and the
+// 64 / (HD/4) lane groups take interleaved splits, every load issued before
+// the sums.  M, the weights and L as in paged_decode_combine.
+template <typename O, int HD, int GM>
+__global__ __launch_bounds__(kWave) void paged_decode_combine_wave(const float *__restrict__ part,
+                                                                   typename O::T *__restrict__ out,
+                                                                   uint32_t n_heads, uint32_t n_kv,
+                                                                   uint32_t splits) {
+    constexpr uint32_t kRec = HD + kRecTail;
+    constexpr uint32_t LPR = HD / 4, SG = kWave / LPR;  // lanes per record, split groups
+    constexpr uint32_t kPerLane = kMaxSplits / kWave;
+    __shared__ float w_lds[kMaxSplits];
+    const uint32_t bh = blockIdx.x, h = bh % n_heads, b = bh / n_heads;
+    const uint32_t G = n_heads / n_kv, g = h / G, slot = h % G;
+    const float *base = part + ((size_t)(b * n_kv + g) * splits * GM + slot) * kRec;  // split s: + s * GM * kRec
+    const uint32_t lane = threadIdx.x, dq = lane % LPR, sg = lane / LPR;
+    // the first batch of record sums first: its latency overlaps the m / l
+    // reductions
+    constexpr uint32_t kBatch = 16;
+    float4 v[kBatch];
+    auto load_batch = [&](uint32_t s0) {
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            const uint32_t sp = s0 + sg + j * SG;
+            v[j] = sp < splits ? *reinterpret_cast<const float4 *>(base + (size_t)sp * GM * kRec + 4 * dq)
+                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    load_batch(0);
+    float ms[kPerLane], ls[kPerLane];
+    float M = -__builtin_inff();
+#pragma unroll
+    for (uint32_t i = 0; i < kPerLane; ++i) {
+        const uint32_t sp = lane + i * kWave;
+        ms[i] = sp < splits ? base[(size_t)sp * GM * kRec + HD] : -__builtin_inff();
+        ls[i] = sp < splits ? base[(size_t)sp * GM * kRec + HD + 1] : 0.0f;
+        M = fmaxf(M, ms[i]);
+    }
+    M = wave_max(M);
+    float Lp = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < kPerLane; ++i) {
+        const uint32_t sp = lane + i * kWave;
+        const float w = (sp < splits && ms[i] > -__builtin_inff()) ? __expf(ms[i] - M) : 0.0f;
+        w_lds[sp] = w;
+        Lp += w * ls[i];
+    }
+    const float L = wave_sum(Lp);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t s0 = 0;;) {
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            const uint32_t sp = s0 + sg + j * SG;
+            const float w = sp < splits ? w_lds[sp] : 0.0f;
+            o.x += w * v[j].x;
+            o.y += w * v[j].y;
+            o.z += w * v[j].z;
+            o.w += w * v[j].w;
+        }
+        s0 += kBatch * SG;
+        if (s0 >= splits) break;
+        load_batch(s0);
+    }
+#pragma unroll
+    for (uint32_t off = LPR; off < kWave; off *= 2) {
+        o.x += __shfl_xor(o.x, off, kWave);
+        o.y += __shfl_xor(o.y, off, kWave);
+        o.z += __shfl_xor(o.z, off, kWave);
+        o.w += __shfl_xor(o.w, off, kWave);
+    }
+    if (sg == 0) {
+        const float inv = 1.0f / L;
+        const float r[4] = {L > 0.0f ? o.x * inv : 0.0f, L > 0.0f ? o.y * inv : 0.0f, L > 0.0f ? o.z * inv : 0.0f,
+                            L > 0.0f ? o.w * inv : 0.0f};
+        store_f32<O, 4>(out + ((size_t)b * n_heads + h) * HD + 4 * dq, r);
+    }
+}
+
 // Split count: about kTargetWaves wavefronts when batch * n_kv is small, at
 // least kMinSplitBlocks blocks per split, at most kMaxSplits.
 // Measured (one Llama-3-8B sequence, 8 KV heads): 2048 keys took 32 us with
 // 16-block splits and 17.5 us with 2-block ones; 32768 keys did best at
 // 128 splits (1024 wavefronts) rather than 256.
 constexpr uint32_t kMinSplitBlocks = 2;
+// Build knobs: the one-wavefront combine for launches of at most
+// COMBINE_WAVE_MAX splits (1), or the 1024-thread combine always (0).
+// Measured interleaved on one box: one 2048-key sequence (64 splits) 11.96
+// against 12.16 us; one 32768-key sequence (128 splits) 35.9 against 34.0 us
+// with the wavefront form, hence the limit.
+#ifndef FELLM_ATT_COMBINE_WAVE
+#define FELLM_ATT_COMBINE_WAVE 1
+#endif
+#ifndef FELLM_ATT_COMBINE_WAVE_MAX
+#define FELLM_ATT_COMBINE_WAVE_MAX 64
+#endif
 // Build knob: wavefronts the split policy aims for.  With two blocks in
 // flight from 8-block walks, one 32768-key sequence measured 34.0-34.2 us at
 // 1024, 41.3-41.4 at 2048 and 52.3 at 512 (interleaved on one box).
@@ -501,7 +599,7 @@ int launch_decode(const void *q, void *out, uint32_t batch, uint32_t n_heads, ui
                   uint32_t max_seq, float scale, uint32_t causal, uint32_t window, const PagedGeom &geo,
                   float *ws, uint64_t ws_bytes, hipStream_t st) {
     uint32_t splits = choose_splits(batch, n_kv, max_seq);
-    const uint64_t need = (uint64_t)batch * n_kv * splits * GM * (HD + 2) * 4;
+    const uint64_t need = (uint64_t)batch * n_kv * splits * GM * (HD + kRecTail) * 4;
     if (splits > 1 && (!ws || ws_bytes < need)) splits = 1;
     const uint32_t blocks = (max_seq + kBlockTokens - 1) / kBlockTokens;
     const uint32_t bps = (blocks + splits - 1) / splits;
@@ -518,8 +616,12 @@ int launch_decode(const void *q, void *out, uint32_t batch, uint32_t n_heads, ui
                            geo.table, geo, n_heads, n_kv, scale, causal, window, splits, bps > 0 ? bps : 1);
     int rc = launch_status();
     if (rc != FELLM_OK || splits == 1) return rc;
-    FELLM_LAUNCH((paged_decode_combine<O, HD, GM>), dim3(batch * n_heads), dim3(kCombineThreads), 0, st, ws,
-                       static_cast<typename O::T *>(out), n_heads, n_kv, splits);
+    if (FELLM_ATT_COMBINE_WAVE && splits <= FELLM_ATT_COMBINE_WAVE_MAX && aligned_to(ws, 16))
+        FELLM_LAUNCH((paged_decode_combine_wave<O, HD, GM>), dim3(batch * n_heads), dim3(kWave), 0, st, ws,
+                     static_cast<typename O::T *>(out), n_heads, n_kv, splits);
+    else
+        FELLM_LAUNCH((paged_decode_combine<O, HD, GM>), dim3(batch * n_heads), dim3(kCombineThreads), 0, st, ws,
+                     static_cast<typename O::T *>(out), n_heads, n_kv, splits);
     return launch_status();
 }
 
@@ -737,7 +839,7 @@ extern "C" uint64_t fellm_rocm_paged_attention_workspace(uint32_t batch, uint32_
     const uint32_t splits = choose_splits(batch, n_kv_heads, max_seq);
     if (splits <= 1) return 0;
     const uint32_t gm = n_heads / n_kv_heads <= 8 ? 8 : 16;
-    return (uint64_t)batch * n_kv_heads * splits * gm * (head_dim + 2) * 4;
+    return (uint64_t)batch * n_kv_heads * splits * gm * (head_dim + kRecTail) * 4;
 }
 
 extern "C" int fellm_rocm_paged_attention(const void *q, uint32_t q_dtype, void *out, uint32_t out_dtype,

@@ -256,8 +256,9 @@ int fellm_rocm_matvec_kquant(const void *w, uint32_t w_dtype, uint32_t rows, uin
  * head_dim 64, 128 or 256; n_heads / n_kv_heads <= 16; kv->block_size 16,
  * kv->stride = n_kv_heads * head_dim, kv_dtype F16 or BF16.
  * workspace: fellm_rocm_paged_attention_workspace() bytes for split-key
- * partial sums (used when batch * n_kv_heads is small); with a null or short
- * workspace every (row, KV head) runs in one wavefront.
+ * partial sums (used when batch * n_kv_heads is small; 16-byte aligned for
+ * the fastest combine); with a null or short workspace every (row, KV head)
+ * runs in one wavefront.
  * Products with the f16 cache are exact (q split into f16 high/low parts on
  * the matrix cores); accumulation, exp and the softmax run in f32.
  */
