@@ -25,6 +25,26 @@
 #endif
 
 // Bit distance bound of silu_fast; kept equal to the measured maximum.
+// Build knob: the packed interval test evaluates every element without a
+// branch on the fast domain (1; the domain and NaN tests join the final
+// compare) or returns early outside it (0).
+#ifndef FELLM_SILU_BRANCHLESS
+#define FELLM_SILU_BRANCHLESS 1
+#endif
+
+// Build knob: silu_fast's exp(-g) from the hardware exp2 of the whole
+// argument with a first-order correction (1) or after a reduction by ln 2 (0).
+#ifndef FELLM_SILU_EXP_DIRECT
+#define FELLM_SILU_EXP_DIRECT 1
+#endif
+
+// Build knob (with FELLM_SILU_EXP_DIRECT): g / d in silu_fast as g times the
+// hardware reciprocal (0), with one Newton step on the reciprocal (1), and
+// one residual correction of the quotient (2).
+#ifndef FELLM_SILU_DIV_STEPS
+#define FELLM_SILU_DIV_STEPS 0
+#endif
+
 #ifndef FELLM_SILU_FAST_DIST
 #define FELLM_SILU_FAST_DIST 5
 #endif
@@ -636,6 +656,23 @@ __device__ __forceinline__ bool silu_fast_domain(float g) {
 }
 
 __device__ __forceinline__ float silu_fast(float g) {
+#if FELLM_SILU_EXP_DIRECT
+    // -g log2(e) as an unevaluated sum xh + xl (log2 e = kL2eHi + kL2eLo,
+    // the product's rounding error recovered by an FMA); the hardware exp2
+    // takes xh whole and the first-order factor 1 + xl ln 2 carries xl.
+    constexpr float kL2eHi = 0x1.715476p+0f, kL2eLo = 0x1.4ae0c0p-26f, kLn2 = 0x1.62e430p-1f;
+    const float xh = -g * kL2eHi;
+    const float xl = __builtin_fmaf(-g, kL2eLo, __builtin_fmaf(-g, kL2eHi, -xh));
+    const float e0 = __builtin_amdgcn_exp2f(xh);
+    const float e = __builtin_fmaf(e0, xl * kLn2, e0);
+    const float d = 1.0f + e;
+    const float y0 = __builtin_amdgcn_rcpf(d);
+    if constexpr (FELLM_SILU_DIV_STEPS == 0) return g * y0;
+    const float y1 = __builtin_fmaf(__builtin_fmaf(-d, y0, 1.0f), y0, y0);
+    const float q0 = g * y1;
+    if constexpr (FELLM_SILU_DIV_STEPS == 1) return q0;
+    return __builtin_fmaf(__builtin_fmaf(-d, q0, g), y1, q0);
+#else
     constexpr float kLog2e = 0x1.715476p+0f;
     constexpr float kLn2Hi = 0x1.62e430p-1f;   // ln 2 rounded up to 24 bits
     constexpr float kLn2Lo = -0x1.05c610p-29f;  // ln 2 - kLn2Hi
@@ -645,6 +682,7 @@ __device__ __forceinline__ float silu_fast(float g) {
     r = __builtin_fmaf(n, -kLn2Lo, r);
     const float e = __builtin_ldexpf(__builtin_amdgcn_exp2f(r * kLog2e), (int)n);
     return g * __builtin_amdgcn_rcpf(1.0f + e);
+#endif
 }
 
 // out = O::store(RN(silu(g) * u)) without evaluating the exact silu when the
@@ -755,7 +793,20 @@ template <typename O>
 __device__ __forceinline__ bool silu_mul_fast(float g, float u, typename O::T &out) {
     static_assert(sizeof(typename O::T) == 2, "the interval test needs a 16-bit output");
     constexpr bool kBf = std::is_base_of_v<BF16, O>, kF16 = std::is_same_v<O, F16>;
-    if constexpr ((kBf || kF16) && FELLM_SILU_PK) {
+    if constexpr ((kBf || kF16) && FELLM_SILU_PK && FELLM_SILU_BRANCHLESS) {
+        // Straight-line code: outside the domain the fast value is computed
+        // and discarded.  With the reduction by ln 2, med3 keeps the
+        // exponent's integer conversion in range for any g; inside the domain
+        // it changes nothing.
+        const bool ok = silu_fast_domain(g) && u == u;
+        const float gc = FELLM_SILU_EXP_DIRECT ? g : __builtin_amdgcn_fmed3f(g, -64.0f, 64.0f);
+        const uint32_t b = __float_as_uint(silu_fast(gc));
+        float lo = __uint_as_float(b - kSiluFastDist) * u, hi = __uint_as_float(b + kSiluFastDist) * u;
+        __asm__("" : "+v"(lo), "+v"(hi));
+        const uint32_t r = kBf ? bf16_pack_bits(lo, hi) : f16_pack_bits(lo, hi);
+        out = __builtin_bit_cast(typename O::T, (uint16_t)(r & 0xffffu));
+        return ok && (r & 0xffffu) == (r >> 16);
+    } else if constexpr ((kBf || kF16) && FELLM_SILU_PK) {
         if (!silu_fast_domain(g) || u != u) return false;
         const uint32_t b = __float_as_uint(silu_fast(g));
         float lo = __uint_as_float(b - kSiluFastDist) * u, hi = __uint_as_float(b + kSiluFastDist) * u;
