@@ -22,6 +22,13 @@
 namespace fellm {
 namespace {
 
+// Build knob: 8-element vectors per thread in the SwiGLU launch.  Measured
+// interleaved on one box: configs[1] 55.6-56.7 us at 1 and 2, 60.0-60.5 at 4;
+// configs[4] routed 95.6 (1), 92.5 (2), 97.6 (4).
+#ifndef FELLM_SWIGLU_UNROLL
+#define FELLM_SWIGLU_UNROLL 2
+#endif
+
 inline uint32_t ew_grid(uint64_t units) {
     uint64_t g = (units + kEwBlock - 1) / kEwBlock;
     const uint64_t cap = 256ull * 32;  // 256 CUs x 32 blocks: enough to saturate HBM
@@ -154,7 +161,7 @@ __global__ __launch_bounds__(kEwBlock) void silu_fast_bound_kernel(uint32_t *__r
 // VEC = 8 elements: 16 B for 16-bit types, 32 B for f32.
 template <typename I, typename O>
 int launch_silu(const void *g, const void *u, void *out, uint64_t n, hipStream_t s) {
-    constexpr int VEC = 8, UNROLL = 2;
+    constexpr int VEC = 8, UNROLL = FELLM_SWIGLU_UNROLL;
     using TI = typename I::T;
     using TO = typename O::T;
     if (!aligned_to(g, sizeof(TI) * VEC) || !aligned_to(u, sizeof(TI) * VEC) ||
