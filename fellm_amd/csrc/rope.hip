@@ -18,6 +18,7 @@
 // item for 16-bit activations) spread over the block.  In KV mode the rotated
 // K row and the V row are also rounded once to the cache dtype and written
 // into their paged slots, so K never makes an extra HBM round trip.
+#include <algorithm>
 #include <initializer_list>
 #include <type_traits>
 
@@ -68,6 +69,12 @@
 #endif
 #ifndef FELLM_ROPE_UNROLL
 #define FELLM_ROPE_UNROLL 3
+#endif
+// Build knob: workgroups per row of the standalone RoPE + K/V append launch
+// (0: rope_head_split).  Measured at configs[3], interleaved on one box: the
+// rule's 4 6.24-6.28 us, 1 8.08-8.16, 2 6.64-6.72, 8 7.16.
+#ifndef FELLM_KV_HSPLIT
+#define FELLM_KV_HSPLIT 0
 #endif
 
 namespace fellm {
@@ -781,7 +788,7 @@ extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q
             const bool vec = rope_vec_ok(head_dim, rope_dim, pairing, sizeof(T), {q, q_out, k, k_out, v}) &&
                              aligned_to(kvp->arena, 16) && kv.block_bytes % 16 == 0;
             auto go = [&]<int PV>() {
-                const uint32_t hs = rope_head_split(batch, n_q_heads + 2 * n_kv_heads);
+                const uint32_t hs = FELLM_KV_HSPLIT ? FELLM_KV_HSPLIT : rope_head_split(batch, n_q_heads + 2 * n_kv_heads);
                 FELLM_LAUNCH((rope_kernel<A, C, PV, 1, 1>), dim3(batch * hs), dim3(kRopeBlock), 0, s,
                                    (const T *)q, (T *)q_out, n_q_heads, (const T *)k, (T *)k_out, n_kv_heads,
                                    (const T *)v, batch, head_dim, rope_dim, pairing, inv_freqs, rope_positions, 0u,
@@ -797,9 +804,10 @@ extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q
 // One decode step's three memory-bound ops in one launch.  At decode batch
 // sizes each op moves 10-44 MB, a few microseconds of traffic, and as
 // separate kernels each pays its own fill and drain.  Here the grid is the
-// concatenation of the three launches' grids, workgroup ranges in order:
-//   [0, nb_rope)                RoPE(q), RoPE(k) + paged K/V append,
-//   [nb_rope, + rows)           residual add + RMSNorm, one row each,
+// concatenation of the three launches' grids, workgroup ranges in order
+// (FELLM_STEP_ORDER 1):
+//   [0, rows)                   residual add + RMSNorm, one row each,
+//   [rows, + nb_rope)           RoPE(q), RoPE(k) + paged K/V append,
 //   [.., + nb_silu)             SwiGLU,
 // each range running the same device code as its standalone kernel
 // (rope_block, add_rmsnorm_row, silu_gate_blocks), so the results are the
@@ -817,8 +825,22 @@ extern "C" int fellm_rocm_rope_kv_write(const void *q, void *q_out, uint32_t n_q
 #ifndef FELLM_STEP_WAVES
 #define FELLM_STEP_WAVES 6
 #endif
+// Build knob: rows per RoPE workgroup in the one-launch decode step.
+#ifndef FELLM_STEP_ROWS
+#define FELLM_STEP_ROWS 1
+#endif
+// Build knob: workgroups per RoPE row in the one-launch decode step (0: the
+// rule in fellm_rocm_decode_step).  Measured at configs[3] (256 rows, 80
+// q/k/v heads), interleaved on one box: 1 per row 13.6-13.8 us, 2 14.6,
+// 4 (the standalone launch's split) 15.6, 8 18.0-18.1; two or four rows per
+// workgroup (one per row group) 17.1 and 24.7.
+#ifndef FELLM_STEP_HSPLIT
+#define FELLM_STEP_HSPLIT 0
+#endif
+// Build knob: role order along the grid (see decode_step_kernel).  With one
+// RoPE workgroup per row: norm first 13.52 us, RoPE first 13.6-13.64.
 #ifndef FELLM_STEP_ORDER
-#define FELLM_STEP_ORDER 0
+#define FELLM_STEP_ORDER 1
 #endif
 
 namespace fellm {
@@ -857,8 +879,9 @@ __global__ __launch_bounds__(kRopeBlock)
 __attribute__((amdgpu_waves_per_eu(NCHUNK <= 4 && FELLM_STEP_WAVES ? FELLM_STEP_WAVES : 1)))
 void decode_step_kernel(StepArgs<A> p) {
     static_assert(kRopeBlock == 256 && kEwBlock == 256, "the three roles share one workgroup size");
-    __shared__ float2 cs_all[1][kMaxHalf];
-    __shared__ uint64_t kbase_all[1];
+    constexpr int SR = FELLM_STEP_ROWS;
+    __shared__ float2 cs_all[SR][kMaxHalf / SR];
+    __shared__ uint64_t kbase_all[SR];
     __shared__ float red[256 / kWave];
     __shared__ uint64_t tab_lds[32];
     // Role order along the grid (build knob FELLM_STEP_ORDER): 0 RoPE, norm,
@@ -877,7 +900,7 @@ void decode_step_kernel(StepArgs<A> p) {
         b -= nb[r];
     }
     if (role == 0) {
-        rope_block<A, C, 4, 1, 1>(p.q, p.q_out, p.nq, p.k, p.k_out, p.nkv, p.v, p.batch, p.head_dim, p.rope_dim,
+        rope_block<A, C, 4, 1, SR>(p.q, p.q_out, p.nq, p.k, p.k_out, p.nkv, p.v, p.batch, p.head_dim, p.rope_dim,
                                   p.pairing, p.inv_freqs, p.rope_pos, 0u, p.kv_pos, p.kv, p.err, p.hsplit, b, cs_all,
                                   kbase_all);
     } else if (role == 1) {
@@ -902,6 +925,7 @@ extern "C" int fellm_rocm_decode_step(const FellmRocmDecodeStep *d, void *stream
     const bool norm_fits = d->residual && d->h_out && d->group && d->group % 8 == 0 && d->group > 2048 &&
                            d->group <= 16384 && d->norm_elems % d->group == 0 && d->norm_elems / d->group <= 0x7fffffffull;
     bool fuse = norm_fits && d->swiglu_elems % 8 == 0 && d->batch > 0 && d->kv &&
+                d->rope_dim / 2 <= kMaxHalf / FELLM_STEP_ROWS &&
                 rope_vec_ok(d->head_dim, d->rope_dim, d->pairing, es, {d->q, d->q_out, d->k, d->k_out, d->v}) &&
                 aligned_to(d->kv->arena, 16) && d->kv->block_bytes % 16 == 0;
     for (const void *p : {d->x, d->residual, (const void *)d->h_out, (const void *)d->y, d->gate, d->up,
@@ -951,7 +975,13 @@ extern "C" int fellm_rocm_decode_step(const FellmRocmDecodeStep *d, void *stream
             p.head_dim = d->head_dim;
             p.rope_dim = d->rope_dim;
             p.pairing = d->pairing;
-            p.hsplit = rope_head_split(d->batch, d->n_q_heads + 2 * d->n_kv_heads);
+            // RoPE workgroups wait mostly on latency (sin/cos table, slot
+            // lookups); split a row's heads only until the RoPE range covers
+            // the CUs once, so that it does not hold the slots the streaming
+            // roles need.
+            const uint32_t cover = (cu_count() + d->batch - 1) / d->batch;
+            const uint32_t auto_split = rope_head_split(d->batch, d->n_q_heads + 2 * d->n_kv_heads);
+            p.hsplit = FELLM_STEP_HSPLIT ? FELLM_STEP_HSPLIT : std::max(1u, std::min(auto_split, cover));
             p.inv_freqs = d->inv_freqs;
             p.rope_pos = d->rope_positions;
             p.kv_pos = d->kv_positions;
@@ -968,7 +998,7 @@ extern "C" int fellm_rocm_decode_step(const FellmRocmDecodeStep *d, void *stream
             p.up = (const T *)d->up;
             p.act = (T *)d->act_out;
             p.n_silu = d->swiglu_elems;
-            p.nb_rope = d->batch * p.hsplit;
+            p.nb_rope = (d->batch + FELLM_STEP_ROWS - 1) / FELLM_STEP_ROWS * p.hsplit;
             p.nb_norm = (uint32_t)(d->norm_elems / d->group);
             const uint64_t units = d->swiglu_elems / 8;
             p.nb_silu = (uint32_t)((units + kEwBlock * 2 - 1) / (kEwBlock * 2));
