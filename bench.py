@@ -1025,7 +1025,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every op shards by tokens "
-              "with no exchange; see DESIGN.md).  Run with --gpus 1.", file=sys.stderr)
+              "or rows with no exchange between GPUs).  Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
 
