@@ -779,6 +779,14 @@ __global__ __launch_bounds__(BLOCK) void kquant_gather_lds_kernel(const uint8_t 
     }
 }
 
+// Build knob: the fused gather + RMSNorm has an instantiation for 7 parts a
+// thread (1), so rows of 3584 elements hold 56 decoded values in registers
+// instead of 64 (Q6_K f16: 74 VGPRs, 6 waves per SIMD, against 82 and 5):
+// configs[2] Q6_K gather + RMSNorm 24.16-24.24 against 24.48-24.72 us.
+#ifndef FELLM_EMB_NORM_NP7
+#define FELLM_EMB_NORM_NP7 1
+#endif
+
 // Launches kquant_gather_lds_kernel with B threads per workgroup when a
 // thread's share fits the unrolled counts (whole rows of up to 16384
 // elements at 64 threads); -1 otherwise.  Without the norm, `split` cuts
@@ -823,6 +831,7 @@ int launch_kquant_lds_b(const void *table, uint64_t vocab, uint32_t dim, const u
         FELLM_Q6L(1, 1)
         FELLM_Q6L(1, 2)
         FELLM_Q6L(2, 4)
+        if (w && FELLM_EMB_NORM_NP7) FELLM_Q6L(4, 7)  // 7 parts a thread: rows of 3584 (Qwen2-7B) at 64 threads
         FELLM_Q6L(4, 8)
         if (!w) {
             FELLM_Q6L(8, 16)
