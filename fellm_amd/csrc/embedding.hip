@@ -786,6 +786,13 @@ __global__ __launch_bounds__(BLOCK) void kquant_gather_lds_kernel(const uint8_t 
 #ifndef FELLM_EMB_NORM_NP7
 #define FELLM_EMB_NORM_NP7 1
 #endif
+// Build knob: the plain Q5_K / Q6_K gathers take the 7-part instantiation
+// too (1).  configs[2], interleaved on one box: Q6_K 13.2 against 13.4-13.56
+// us, Q5_K 12.4 against 12.8-12.9; Q8_0 slower with it (12.48 against
+// 12.08), so it keeps 8.
+#ifndef FELLM_EMB_PLAIN_NP7
+#define FELLM_EMB_PLAIN_NP7 1
+#endif
 
 // Launches kquant_gather_lds_kernel with B threads per workgroup when a
 // thread's share fits the unrolled counts (whole rows of up to 16384
@@ -831,7 +838,8 @@ int launch_kquant_lds_b(const void *table, uint64_t vocab, uint32_t dim, const u
         FELLM_Q6L(1, 1)
         FELLM_Q6L(1, 2)
         FELLM_Q6L(2, 4)
-        if (w && FELLM_EMB_NORM_NP7) FELLM_Q6L(4, 7)  // 7 parts a thread: rows of 3584 (Qwen2-7B) at 64 threads
+        // 7 parts a thread: rows of 3584 (Qwen2-7B) at 64 threads
+        if ((w || (FELLM_EMB_PLAIN_NP7 && F::kElems == 256)) && FELLM_EMB_NORM_NP7) FELLM_Q6L(4, 7)
         FELLM_Q6L(4, 8)
         if (!w) {
             FELLM_Q6L(8, 16)
