@@ -67,6 +67,14 @@
 #ifndef FELLM_ROPE_BF16_HW_KV
 #define FELLM_ROPE_BF16_HW_KV 1
 #endif
+// Build knob: row-group launches (R > 1: 8192 rows and more) read their
+// packed 16-bit items non-temporally (1).  Measured interleaved on one box:
+// configs[4] 53.6 against 54.8-54.9 us; one-row launches stay regular
+// (configs[1] 17.1-17.3 against 14.1-14.3 us with non-temporal loads: its
+// 42 MB of inputs are read from the last-level cache).
+#ifndef FELLM_ROPE_RAW_NT
+#define FELLM_ROPE_RAW_NT 1
+#endif
 #ifndef FELLM_ROPE_UNROLL
 #define FELLM_ROPE_UNROLL 3
 #endif
@@ -353,7 +361,13 @@ __device__ __forceinline__ void rope_fast_slots(const typename A::T *x1, typenam
                     const uint32_t *pa = reinterpret_cast<const uint32_t *>(src + lo);
                     const uint32_t *pb = reinterpret_cast<const uint32_t *>(src + (KIND == kRopeSplit ? hi : lo + PV));
                     if constexpr (RW == 2 && KIND != kRopeSplit) {  // one 16-byte run
-                        const uint4 a = *reinterpret_cast<const uint4 *>(pa);
+                        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+                        u4v av;
+                        if constexpr (FELLM_ROPE_RAW_NT && R > 1)
+                            av = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(pa));
+                        else
+                            av = *reinterpret_cast<const u4v *>(pa);
+                        const uint4 a = make_uint4(av.x, av.y, av.z, av.w);
                         raw[u][0] = a.x;
                         raw[u][1] = a.y;
                         raw[u][2] = a.z;
