@@ -610,10 +610,12 @@ __attribute__((amdgpu_waves_per_eu(MODE == 0 && BLOCK == 256 ? FELLM_ROPE_WAVES 
 // 4096 rows one row per workgroup streams fastest (18.7 us against 21.4 us
 // for four: more workgroups keep more loads in flight); at 16384 rows four
 // rows per workgroup win (63.3 us against 69.1 us for one) by sharing the
-// launch and sin/cos set-up.  R * rope_dim/2 (sin, cos) pairs must fit the
-// LDS table.
+// launch and sin/cos set-up.  With the row-group walk's non-temporal loads,
+// two rows per workgroup measured 53.0 against 53.6 us for four at 16384
+// rows (configs[4], interleaved on one box), so the cap is two.  R *
+// rope_dim/2 (sin, cos) pairs must fit the LDS table.
 #ifndef FELLM_ROPE_MAX_R
-#define FELLM_ROPE_MAX_R 4
+#define FELLM_ROPE_MAX_R 2
 #endif
 inline int rope_rows_per_block(uint32_t rows, uint32_t rope_dim) {
     const uint32_t half = rope_dim / 2;
