@@ -578,9 +578,10 @@ def test_router_near_ties_and_specials(ops, dev, gating, n_exp, k):
 @pytest.mark.parametrize("rows", [2051, 8193, 16385])
 def test_rope_many_rows(ops, dev, kind, rows):
     """configs[4]'s RoPE shape (head_dim 128, 32 q / 4 kv heads, theta 1e6,
-    positions 0..rows-1) at row counts that select 1, 2 and 4 rows per
-    workgroup (the launcher switches at 8192 and 16384 rows), each with a
-    ragged last workgroup; bit-exact against the oracle."""
+    positions 0..rows-1) at row counts on either side of the launcher's
+    switch from one to two rows per workgroup (8192 rows; the row-group walk
+    reads non-temporally), each with a ragged last workgroup; bit-exact
+    against the oracle."""
     rng = np.random.default_rng(rows)
     nq, nk, hd = 32, 4, 128
     inv = oracle.rope_inv_freqs(1.0e6, hd)
