@@ -63,6 +63,15 @@ namespace {
 
 constexpr int kGemvBlock = 256;
 constexpr int kGemvWaves = kGemvBlock / kWave;
+// Build knob: wavefronts per workgroup for rows of more than 32 blocks (the
+// multi-pass layout), whose workgroups each quantize all of a long x: 8
+// halves that work against 4.  Measured interleaved on one box: Llama-3-8B
+// down projection (4096 x 14336 Q4_K) 12.9 against 15.5 us; the 8B gate/up
+// shape (one pass per row) measured 16.1 against 14.4 us with 8, so it
+// keeps 4.
+#ifndef FELLM_GEMV_MULTI_WAVES
+#define FELLM_GEMV_MULTI_WAVES 8
+#endif
 constexpr uint32_t kGemvMaxCols = 49152;
 #ifndef FELLM_GEMV_MAX_GRID_PRE
 #define FELLM_GEMV_MAX_GRID_PRE 1024
@@ -79,8 +88,9 @@ struct XLds {
 };
 __host__ __device__ constexpr uint32_t gemv_fold_off(uint32_t nb) { return (nb * 292 + 15) / 16 * 16; }
 // fold_per_wave: floats of row-fold buffer per wavefront.
-__host__ __device__ constexpr uint32_t gemv_lds_bytes(uint32_t nb, uint32_t fold_per_wave) {
-    return gemv_fold_off(nb) + kGemvWaves * fold_per_wave * 4;
+__host__ __device__ constexpr uint32_t gemv_lds_bytes(uint32_t nb, uint32_t fold_per_wave,
+                                                     uint32_t waves = kGemvWaves) {
+    return gemv_fold_off(nb) + waves * fold_per_wave * 4;
 }
 __device__ __forceinline__ XLds carve_lds(uint8_t *base, uint32_t nb) {
     return {reinterpret_cast<int8_t *>(base), reinterpret_cast<int16_t *>(base + nb * 256),
@@ -195,7 +205,7 @@ __device__ __forceinline__ void x_issue(const void *__restrict__ xsrc, uint32_t 
             f.v[j] = i < words ? src[i] : 0u;
         }
     } else {
-        load_x_batch(static_cast<const float *>(xsrc), nb, threadIdx.x / kWave, kGemvWaves, f.v);
+        load_x_batch(static_cast<const float *>(xsrc), nb, threadIdx.x / kWave, blockDim.x / kWave, f.v);
     }
 }
 
@@ -227,8 +237,9 @@ __device__ __forceinline__ void x_finish(const void *__restrict__ xsrc, uint32_t
     } else {
         const float *x = static_cast<const float *>(xsrc);
         const uint32_t first = threadIdx.x / kWave;
-        quantize_batch(f.v, nb, first, kGemvWaves, xl);
-        quantize_x(x, nb, xl, first + kGemvWaves * kXBatch, kGemvWaves);
+        const uint32_t nw = blockDim.x / kWave;
+        quantize_batch(f.v, nb, first, nw, xl);
+        quantize_x(x, nb, xl, first + nw * kXBatch, nw);
     }
 }
 
@@ -556,8 +567,8 @@ constexpr uint32_t kStagePerWave = 1024 * (kChunks<GW> + (FUSED ? kChunks<UW> : 
 // fold buffer; after a row's last unit, lanes 0 .. mats*rows-1 each fold one
 // (row, matrix) serially over its block values from 0.0 and the even lanes
 // apply silu(gate) * up; then the next unit is written to the stage.
-template <typename GW, typename UW, bool FUSED, bool MULTI, bool PREQ>
-__global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *__restrict__ gw,
+template <typename GW, typename UW, bool FUSED, bool MULTI, bool PREQ, int NW = kGemvWaves>
+__global__ __launch_bounds__(NW * kWave) void kquant_gemv_kernel(const uint8_t *__restrict__ gw,
                                                                   const uint8_t *__restrict__ uw,
                                                                   const void *__restrict__ x, float *__restrict__ out,
                                                                   uint32_t rows, uint32_t nb, uint32_t rp) {
@@ -569,7 +580,7 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *
     const uint32_t h = lane & 1, slot = lane >> 1;
     const uint32_t nbp = (nb + 3) & ~3u;
     const uint32_t fold_floats = MULTI ? kMats * nbp : kMats * rp * nbp;
-    uint8_t *stage = reinterpret_cast<uint8_t *>(xl.fold + kGemvWaves * fold_floats) + wave * kStagePerWave<GW, UW, FUSED>;
+    uint8_t *stage = reinterpret_cast<uint8_t *>(xl.fold + NW * fold_floats) + wave * kStagePerWave<GW, UW, FUSED>;
     uint8_t *ustage = stage + 1024 * kChunks<GW>;
     float *fold = xl.fold + wave * fold_floats;
     const uint32_t grb = nb * GW::kBytes, urb = nb * UW::kBytes;
@@ -577,8 +588,8 @@ __global__ __launch_bounds__(kGemvBlock) void kquant_gemv_kernel(const uint8_t *
     const Rsrc wg = weight_rsrc(gw, g_end);
     const Rsrc wu = weight_rsrc(FUSED ? uw : gw, FUSED ? u_end : g_end);
     const uint32_t passes = MULTI ? (nb + 31) / 32 : 1;
-    const uint32_t wstride = gridDim.x * kGemvWaves;
-    const uint32_t wid = blockIdx.x * kGemvWaves + wave;
+    const uint32_t wstride = gridDim.x * NW;
+    const uint32_t wid = blockIdx.x * NW + wave;
 
     // unit n of this wavefront: (first row, pass) and its byte range per matrix
     auto unit_row = [&](uint32_t n) { return MULTI ? wid + (n / passes) * wstride : (wid + n * wstride) * rp; };
@@ -781,10 +792,11 @@ __global__ __launch_bounds__(kGemvBlock) void quantize_q8k_kernel(const float *_
 // resident at once (the LDS stage sets that).  With x already quantized the
 // prologue is a copy, so more workgroups pay off at every size.
 template <bool PREQ, typename K>
-uint32_t gemv_grid(K kernel, uint32_t lds, uint32_t units) {
-    const uint32_t need = (units + kGemvWaves - 1) / kGemvWaves;
-    uint32_t grid = PREQ ? kGemvMaxGridPre : FELLM_GEMV_MAX_GRID;
-    if (!PREQ && units / (2 * kGemvWaves) > grid) {
+uint32_t gemv_grid(K kernel, uint32_t lds, uint32_t units, uint32_t nw = kGemvWaves) {
+    const uint32_t need = (units + nw - 1) / nw;
+    // the caps count wavefronts in kGemvWaves-wavefront workgroups
+    uint32_t grid = (PREQ ? kGemvMaxGridPre : FELLM_GEMV_MAX_GRID) * kGemvWaves / nw;
+    if (!PREQ && units / (2 * nw) > grid) {
         // resident workgroups for this kernel and LDS size, looked up once each
         static std::mutex mu;
         static std::vector<std::tuple<const void *, uint32_t, uint32_t>> seen;
@@ -794,12 +806,12 @@ uint32_t gemv_grid(K kernel, uint32_t lds, uint32_t units) {
             for (const auto &[k, l, c] : seen)
                 if (k == reinterpret_cast<const void *>(kernel) && l == lds) cap = c;
             if (cap == 0) {
-                cap = resident_grid(kernel, kGemvBlock, lds, 8);
+                cap = resident_grid(kernel, (int)nw * kWave, lds, 8);
                 seen.emplace_back(reinterpret_cast<const void *>(kernel), lds, cap);
             }
         }
-        uint32_t wide = units / (2 * kGemvWaves);
-        if (wide > FELLM_GEMV_WIDE_GRID) wide = FELLM_GEMV_WIDE_GRID;
+        uint32_t wide = units / (2 * nw);
+        if (wide > FELLM_GEMV_WIDE_GRID * kGemvWaves / nw) wide = FELLM_GEMV_WIDE_GRID * kGemvWaves / nw;
         if (wide > cap) wide = cap;
         if (wide > grid) grid = wide;
     }
@@ -832,9 +844,10 @@ int launch_gemv(const void *gw, const void *uw, const void *x, float *out, uint3
             FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, false, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
                                out + r0, n, nb, rp);
         } else {
-            const uint32_t lds = gemv_lds_bytes(nb, mats * nbp) + kGemvWaves * kStagePerWave<GW, UW, FUSED>;
-            const uint32_t grid = gemv_grid<PREQ>(kquant_gemv_kernel<GW, UW, FUSED, true, PREQ>, lds, n);
-            FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, true, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
+            constexpr int NWM = FELLM_GEMV_MULTI_WAVES;
+            const uint32_t lds = gemv_lds_bytes(nb, mats * nbp, NWM) + NWM * kStagePerWave<GW, UW, FUSED>;
+            const uint32_t grid = gemv_grid<PREQ>(kquant_gemv_kernel<GW, UW, FUSED, true, PREQ, NWM>, lds, n, NWM);
+            FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, true, PREQ, NWM>), dim3(grid), dim3(NWM * kWave), lds, s, g, u, x,
                                out + r0, n, nb, 1u);
         }
         const int rc = launch_status();
