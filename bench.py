@@ -490,7 +490,6 @@ def decode_graph_report(torch, ops, dev, steps, warmup):
          "att": torch.empty(1, H, device=dev), "o": torch.empty(H, device=dev), "h2": torch.empty(1, H, device=dev),
          "y2": torch.empty(1, H, device=dev), "act": torch.empty(I, device=dev), "down": torch.empty(H, device=dev),
          "out": torch.empty(1, H, device=dev),
-         "actq": torch.empty(ops._lib.lib().fellm_rocm_q8k_bytes(I), dtype=torch.uint8, device=dev),
          "ws": torch.empty(max(ops._lib.lib().fellm_rocm_paged_attention_workspace(1, nq, nkv, hd, max_seq) // 4, 1),
                            dtype=torch.float32, device=dev)}
     qkv = b["qkv"]
@@ -507,9 +506,7 @@ def decode_graph_report(torch, ops, dev, steps, warmup):
         ops.matvec_kquant(w_o, b["att"].view(-1), qtype="q4k", out=b["o"])
         ops.add_rmsnorm(b["o"].view(1, H), b["x"], n2, 1e-5, h_out=b["h2"], y_out=b["y2"])
         ops.gate_up_swiglu(w_g, w_u, b["y2"].view(-1), qtype="q4k", out=b["act"])
-        # long rows (14336 columns): quantize the activation once, then the _q8k GEMV
-        ops.quantize_q8k(b["act"], out=b["actq"])
-        ops.matvec_kquant_q8k(w_d, b["actq"], qtype="q4k", out=b["down"])
+        ops.matvec_kquant(w_d, b["act"].view(-1), qtype="q4k", out=b["down"])
         ops.add(b["down"].view(1, H), b["h2"], out=b["out"])
 
     out["llama8b_decode_layer_q4k"] = time_eager_vs_graph(torch, layer, steps, warmup)
