@@ -69,6 +69,12 @@ constexpr int kGemvWaves = kGemvBlock / kWave;
 // down projection (4096 x 14336 Q4_K) 12.9 against 15.5 us; the 8B gate/up
 // shape (one pass per row) measured 16.1 against 14.4 us with 8, so it
 // keeps 4.
+// Build knob: wavefronts per workgroup for rows of at most 32 blocks.  8
+// measured slower at the 8B gate/up shape: 16.2 us with 384 workgroups, 18.8
+// with 512, against 14.5 us for 4.
+#ifndef FELLM_GEMV_ONE_WAVES
+#define FELLM_GEMV_ONE_WAVES 4
+#endif
 #ifndef FELLM_GEMV_MULTI_WAVES
 #define FELLM_GEMV_MULTI_WAVES 8
 #endif
@@ -838,10 +844,11 @@ int launch_gemv(const void *gw, const void *uw, const void *x, float *out, uint3
         const uint8_t *u = FUSED ? u8 + (uint64_t)r0 * nb * UW::kBytes : nullptr;
         if (nb <= 32) {
             const uint32_t rp = 32 / nb;
-            const uint32_t lds = gemv_lds_bytes(nb, mats * rp * nbp) + kGemvWaves * kStagePerWave<GW, UW, FUSED>;
+            constexpr int NWO = FELLM_GEMV_ONE_WAVES;
+            const uint32_t lds = gemv_lds_bytes(nb, mats * rp * nbp, NWO) + NWO * kStagePerWave<GW, UW, FUSED>;
             const uint32_t units = (n + rp - 1) / rp;
-            const uint32_t grid = gemv_grid<PREQ>(kquant_gemv_kernel<GW, UW, FUSED, false, PREQ>, lds, units);
-            FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, false, PREQ>), dim3(grid), dim3(kGemvBlock), lds, s, g, u, x,
+            const uint32_t grid = gemv_grid<PREQ>(kquant_gemv_kernel<GW, UW, FUSED, false, PREQ, NWO>, lds, units, NWO);
+            FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, false, PREQ, NWO>), dim3(grid), dim3(NWO * kWave), lds, s, g, u, x,
                                out + r0, n, nb, rp);
         } else {
             constexpr int NWM = FELLM_GEMV_MULTI_WAVES;
