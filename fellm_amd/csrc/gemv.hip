@@ -79,6 +79,9 @@ constexpr int kGemvWaves = kGemvBlock / kWave;
 #define FELLM_GEMV_MULTI_WAVES 8
 #endif
 constexpr uint32_t kGemvMaxCols = 49152;
+// Dynamic LDS a workgroup may take: the CU's 160 KB less the kernel's static
+// LDS (the exp table) with room to spare.
+constexpr uint32_t kGemvLdsLimit = 160 * 1024 - 1024;
 #ifndef FELLM_GEMV_MAX_GRID_PRE
 #define FELLM_GEMV_MAX_GRID_PRE 1024
 #endif
@@ -851,11 +854,19 @@ int launch_gemv(const void *gw, const void *uw, const void *x, float *out, uint3
             FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, false, PREQ, NWO>), dim3(grid), dim3(NWO * kWave), lds, s, g, u, x,
                                out + r0, n, nb, rp);
         } else {
+            auto go_multi = [&]<int NW>() {
+                const uint32_t lds = gemv_lds_bytes(nb, mats * nbp, NW) + NW * kStagePerWave<GW, UW, FUSED>;
+                const uint32_t grid = gemv_grid<PREQ>(kquant_gemv_kernel<GW, UW, FUSED, true, PREQ, NW>, lds, n, NW);
+                FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, true, PREQ, NW>), dim3(grid), dim3(NW * kWave), lds, s, g,
+                             u, x, out + r0, n, nb, 1u);
+            };
+            // FELLM_GEMV_MULTI_WAVES wavefronts while their stages and x fit the
+            // workgroup's LDS (fused Q5_K / Q6_K rows of ~40k columns do not).
             constexpr int NWM = FELLM_GEMV_MULTI_WAVES;
-            const uint32_t lds = gemv_lds_bytes(nb, mats * nbp, NWM) + NWM * kStagePerWave<GW, UW, FUSED>;
-            const uint32_t grid = gemv_grid<PREQ>(kquant_gemv_kernel<GW, UW, FUSED, true, PREQ, NWM>, lds, n, NWM);
-            FELLM_LAUNCH((kquant_gemv_kernel<GW, UW, FUSED, true, PREQ, NWM>), dim3(grid), dim3(NWM * kWave), lds, s, g, u, x,
-                               out + r0, n, nb, 1u);
+            if (gemv_lds_bytes(nb, mats * nbp, NWM) + NWM * kStagePerWave<GW, UW, FUSED> <= kGemvLdsLimit)
+                go_multi.template operator()<NWM>();
+            else
+                go_multi.template operator()<kGemvWaves>();
         }
         const int rc = launch_status();
         if (rc != FELLM_OK) return rc;

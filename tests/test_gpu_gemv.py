@@ -62,6 +62,34 @@ def test_matvec_kquant_shapes(ops, dev, dtype, cols):
     assert_exact(got, ref, f"matvec {NAMES[dtype]} cols={cols}")
 
 
+@pytest.mark.parametrize("gt,ut", [(12, 12), (13, 13), (14, 14), (14, 12)])
+@pytest.mark.parametrize("cols", [16640, 49152])
+def test_gate_up_swiglu_long_rows(ops, dev, gt, ut, cols):
+    """Multi-pass rows (more than 32 blocks) of the fused GEMV up to the
+    longest accepted row: 8-wavefront workgroups where their LDS stages fit,
+    4 where they do not (fused Q5_K / Q6_K at 49152 columns)."""
+    rng = np.random.default_rng(gt * 1000 + ut * 10 + cols)
+    rows = 37
+    g, u = weights(rng, gt, rows, cols), weights(rng, ut, rows, cols)
+    x = rng.normal(size=cols).astype(np.float32)
+    ref = oracle.gate_up_swiglu(gt, g, ut, u, rows, cols, x)
+    got = ops.gate_up_swiglu(to_dev(g, dev), to_dev(u, dev), to_dev(x, dev), qtype=NAMES[gt],
+                             up_qtype=NAMES[ut]).cpu().numpy()
+    assert_exact(got, ref, f"gate_up_swiglu {NAMES[gt]}/{NAMES[ut]} cols={cols}")
+
+
+@pytest.mark.parametrize("dtype", [12, 13, 14])
+def test_matvec_kquant_longest_rows(ops, dev, dtype):
+    """The plain GEMV at the longest accepted row (192 blocks, six passes)."""
+    rng = np.random.default_rng(dtype + 49152)
+    rows, cols = 41, 49152
+    w = weights(rng, dtype, rows, cols)
+    x = (rng.normal(size=cols) * rng.uniform(0.01, 20.0, size=cols)).astype(np.float32)
+    ref = oracle.matvec_kquant(dtype, w, rows, cols, x)
+    got = ops.matvec_kquant(to_dev(w, dev), to_dev(x, dev), qtype=NAMES[dtype]).cpu().numpy()
+    assert_exact(got, ref, f"matvec {NAMES[dtype]} cols={cols}")
+
+
 @pytest.mark.parametrize("dtype", [12, 13, 14])
 def test_matvec_q8k_edges(ops, dev, dtype):
     """Zero blocks, round-half-even ties (amax 127 makes iscale 1), a block
