@@ -798,7 +798,10 @@ __device__ __forceinline__ bool silu_mul_fast(float g, float u, typename O::T &o
         // and discarded.  With the reduction by ln 2, med3 keeps the
         // exponent's integer conversion in range for any g; inside the domain
         // it changes nothing.
-        const bool ok = silu_fast_domain(g) && u == u;
+        // f16: a NaN u gives both ends u's NaN, quieted, which the packed
+        // conversion rounds as F16::store does (equal for every input), and
+        // the exact path's product is that same NaN: no NaN test needed.
+        const bool ok = silu_fast_domain(g) && (kF16 || u == u);
         const float gc = FELLM_SILU_EXP_DIRECT ? g : __builtin_amdgcn_fmed3f(g, -64.0f, 64.0f);
         const uint32_t b = __float_as_uint(silu_fast(gc));
         float lo = __uint_as_float(b - kSiluFastDist) * u, hi = __uint_as_float(b + kSiluFastDist) * u;
